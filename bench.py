@@ -1,0 +1,322 @@
+#!/usr/bin/env python3
+"""Causal GQA flash-attention fwd+bwd throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu]
+
+A step is one forward + backward of the attention op over one batch of the
+BASELINE.json workload (default config 3: batch 2, seq 8192, 10 query heads,
+2 KV heads, head_dim 128, causal, bf16, synthetic N(0,1) inputs resident in
+HBM).  The step runs exactly the kernels ``FlashAttention`` runs -- forward,
+Delta, dK/dV, dK/dV group reduce, dQ -- through the library's C ABI, with HIP
+events between them on the launch stream so every kernel's average duration
+is measured live over the timed region.
+
+Printed: one JSON line.  ``value`` is algorithmic TFLOP/s of the whole step
+(7 * B * H * S^2 * D for causal fwd+bwd: fwd 2 GEMMs + bwd 5 GEMMs of
+2*S^2*D/2 each per head); ``roofline`` is the dominant kernel's algorithmic
+TFLOP/s against the bf16 dense MFMA peak; ``cpu_baseline`` is the fp32
+reference math (oracle, torch autograd) timed on this host's cores on one KV
+group of one batch element of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA, published
+HBM_TBPS = 8.0
+
+CONFIGS = {
+    2: dict(batch=8, seq=2048),
+    3: dict(batch=2, seq=8192),
+    4: dict(batch=4, seq=4096),
+}
+HEADS, KV_HEADS, DIM = 10, 2, 128
+
+
+def gemm_unit(batch, seq, heads=HEADS, dim=DIM, causal=True):
+    """One causal attention GEMM over all heads: 2*S*S*D/2 * B*H flops."""
+    return 2.0 * batch * heads * seq * seq * dim * (0.5 if causal else 1.0)
+
+
+def parse(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--also", type=int, nargs="*", default=[2],
+                    help="extra configs reported beside the main one")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-autograd", action="store_true", help="skip the autograd cross-check")
+    ap.add_argument("--traffic", default=None,
+                    help="JSON with HBM bytes per launch from rocprofv3 --pmc "
+                         "(default profiles/traffic_config<N>.json if present)")
+    return ap.parse_args(argv)
+
+
+class Workload:
+    def __init__(self, lib, batch, seq, device, seed=0):
+        import torch
+        self.lib, self.B, self.S = lib, batch, seq
+        self.H, self.Hkv, self.D = HEADS, KV_HEADS, DIM
+        gen = torch.Generator().manual_seed(seed)
+        mk = lambda *shape: torch.randn(*shape, generator=gen).to(torch.bfloat16).to(device)
+        self.q = mk(batch, seq, HEADS, DIM)
+        self.k = mk(batch, seq, KV_HEADS, DIM)
+        self.v = mk(batch, seq, KV_HEADS, DIM)
+        self.do = mk(batch, seq, HEADS, DIM)
+        self.o = torch.empty_like(self.q)
+        self.lse = torch.empty(batch, HEADS, seq, dtype=torch.float32, device=device)
+        self.delta = torch.empty_like(self.lse)
+        self.dq = torch.empty_like(self.q)
+        self.dk = torch.empty_like(self.k)
+        self.dv = torch.empty_like(self.v)
+        self.ws_bytes = lib.mm1_attn_bwd_workspace_size(batch, seq, HEADS, KV_HEADS, DIM)
+        self.ws = torch.empty(max(self.ws_bytes // 4, 1), dtype=torch.float32, device=device)
+        self.scale = DIM ** -0.5
+        self.stream = torch.cuda.current_stream(device)
+
+    STAGES = ("fwd", "delta", "dkdv", "reduce", "dq")
+
+    def step(self, marks=None):
+        """One fwd+bwd; if `marks` is given, records an event after each stage."""
+        L, B, S, H, Hkv, D, sp = self.lib, self.B, self.S, self.H, self.Hkv, self.D, self.stream.cuda_stream
+        p = lambda t: t.data_ptr()
+
+        def chk(rc, name):
+            if rc != 0:
+                raise RuntimeError(f"{name}: {L.mm1_attn_strerror(rc).decode()}")
+
+        chk(L.mm1_attn_fwd(p(self.q), p(self.k), p(self.v), p(self.o), p(self.lse),
+                           B, S, H, Hkv, D, 1, self.scale, sp), "fwd")
+        if marks is not None:
+            marks[0].record(self.stream)
+        chk(L.mm1_attn_delta(p(self.o), p(self.do), p(self.delta), B, S, H, D, sp), "delta")
+        if marks is not None:
+            marks[1].record(self.stream)
+        chk(L.mm1_attn_bwd_dkdv(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
+                                p(self.delta), p(self.dk), p(self.dv), p(self.ws), self.ws_bytes,
+                                B, S, H, Hkv, D, 1, self.scale, sp), "dkdv")
+        if marks is not None:
+            marks[2].record(self.stream)
+        chk(L.mm1_attn_bwd_dkdv_reduce(p(self.ws), self.ws_bytes, p(self.dk), p(self.dv),
+                                       B, S, H, Hkv, D, sp), "reduce")
+        if marks is not None:
+            marks[3].record(self.stream)
+        chk(L.mm1_attn_bwd_dq(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
+                              p(self.delta), p(self.dq), B, S, H, Hkv, D, 1, self.scale, sp), "dq")
+        if marks is not None:
+            marks[4].record(self.stream)
+
+
+def time_workload(wl, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    start = ev()
+    marks = [[ev() for _ in Workload.STAGES] for _ in range(steps)]
+    begins = [ev() for _ in range(steps)]
+    start.record(wl.stream)
+    for i in range(steps):
+        begins[i].record(wl.stream)
+        wl.step(marks[i])
+    end = ev()
+    end.record(wl.stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    per_stage = {name: 0.0 for name in Workload.STAGES}
+    for i in range(steps):
+        prev = begins[i]
+        for name, mk in zip(Workload.STAGES, marks[i]):
+            per_stage[name] += prev.elapsed_time(mk)
+            prev = mk
+    return total_ms / steps, {k: v / steps for k, v in per_stage.items()}
+
+
+def time_autograd(batch, seq, device, steps, warmup):
+    """The same step through the drop-in autograd op (cross-check)."""
+    import torch
+    import mimansm1_v1_amd as mm
+    gen = torch.Generator().manual_seed(0)
+    mk = lambda *s: torch.randn(*s, generator=gen).to(torch.bfloat16).to(device).requires_grad_(True)
+    q, k, v = mk(batch, seq, HEADS, DIM), mk(batch, seq, KV_HEADS, DIM), mk(batch, seq, KV_HEADS, DIM)
+    do = torch.randn(batch, seq, HEADS, DIM, generator=gen).to(torch.bfloat16).to(device)
+
+    def run():
+        mm.flash_attention(q, k, v, True, HEADS // KV_HEADS).backward(do)
+        q.grad = k.grad = v.grad = None
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        run()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def cpu_baseline(seq):
+    """fp32 reference math (oracle restatement of AT:521-530, autograd backward)
+    on one KV group (5 query heads, 1 KV head) of one batch element, full seq."""
+    import torch
+    from oracle import reference as R
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    q, k, v, do = R.make_inputs(1, seq, HEADS // KV_HEADS, 1, DIM, seed=0, dtype=torch.float32)
+    groups = HEADS // KV_HEADS
+    flops = 7 * gemm_unit(1, seq, heads=groups) / 2
+    times = []
+    budget = 30.0
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        R.grads(q, k, v, do, True, groups)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 3 or time.perf_counter() - t_start + times[-1] > budget:
+            break
+    best = sorted(times)[len(times) // 2]
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(flops / best / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"fp32 torch autograd of the reference math (oracle/reference.py) on batch 1 x "
+                   f"1 KV group (5 query heads) x seq {seq} x d 128, causal fwd+bwd; median of "
+                   f"{len(times)} runs, {best:.2f} s each; algorithmic flops 7*B*H*S^2*D with "
+                   f"B*H = 5; CPU: {model}"),
+    }
+
+
+def main(argv=None):
+    args = parse(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: every box in this setup has one MI355X, so "
+              f"--gpus {args.gpus} is not supported (the attention shards per (batch, KV head) "
+              f"with no exchange; see DESIGN.md).", file=sys.stderr)
+        return 2
+    sys.path.insert(0, str(ROOT))
+    import torch
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+
+    results = {}
+    for cfg in [args.config] + [c for c in args.also if c != args.config]:
+        B, S = CONFIGS[cfg]["batch"], CONFIGS[cfg]["seq"]
+        wl = Workload(lib, B, S, device)
+        ms, stages = time_workload(wl, args.steps, args.warmup)
+        unit = gemm_unit(B, S)
+        flops = {"fwd": 2 * unit, "dkdv": 4 * unit, "dq": 3 * unit}
+        res = {
+            "ms_per_step": ms,
+            "tflops": 7 * unit / (ms * 1e-3) / 1e12,
+            "stage_ms": stages,
+            "fwd_tflops": 2 * unit / (stages["fwd"] * 1e-3) / 1e12,
+            "bwd_tflops": 5 * unit / ((ms - stages["fwd"]) * 1e-3) / 1e12,
+            "kernel_tflops": {k: flops[k] / (stages[k] * 1e-3) / 1e12 for k in flops},
+            "kernel_flops": flops,
+        }
+        if not args.no_autograd:
+            res["ms_per_step_autograd"] = time_autograd(B, S, device, args.steps, args.warmup)
+        results[cfg] = res
+        del wl
+        torch.cuda.empty_cache()
+        print(f"[bench] config {cfg}: {ms:.3f} ms/step, {res['tflops']:.1f} TFLOP/s, "
+              f"stages {', '.join(f'{k} {v:.3f}' for k, v in stages.items())}",
+              file=sys.stderr, flush=True)
+
+    main_res = results[args.config]
+    B, S = CONFIGS[args.config]["batch"], CONFIGS[args.config]["seq"]
+    dom = max(("fwd", "dkdv", "dq"), key=lambda k: main_res["stage_ms"][k])
+    achieved = main_res["kernel_tflops"][dom]
+    traffic = None
+    tpath = Path(args.traffic) if args.traffic else ROOT / "profiles" / f"traffic_config{args.config}.json"
+    if tpath.exists():
+        try:
+            traffic = json.loads(tpath.read_text()).get(dom)
+        except ValueError:
+            traffic = None
+
+    out = {
+        "metric": "causal GQA attn fwd+bwd TFLOP/s and % of MI355X bf16 MFMA peak, seq 2048/8192",
+        "value": round(main_res["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"config {args.config}: causal GQA flash attention fwd+bwd, batch {B}, "
+                        f"seq {S}, 10 query heads / 2 KV heads, head_dim 128, bf16",
+            "batch": B, "seq_len": S, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": DIM,
+            "causal": True, "parallelism": "single GPU",
+        },
+        "pct_of_peak": round(100 * main_res["tflops"] / PEAK_BF16_TFLOPS, 2),
+        "fwd_tflops": round(main_res["fwd_tflops"], 2),
+        "bwd_tflops": round(main_res["bwd_tflops"], 2),
+        "stage_ms": {k: round(v, 4) for k, v in main_res["stage_ms"].items()},
+        "reference_flop_count_tflops": round(main_res["tflops"] * 5 / 7, 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": {"fwd": "attn_fwd_kernel", "dkdv": "attn_dkdv_kernel",
+                       "dq": "attn_dq_kernel"}[dom],
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+            "flops_per_launch": main_res["kernel_flops"][dom],
+            "avg_launch_ms": round(main_res["stage_ms"][dom], 4),
+        },
+    }
+    if "ms_per_step_autograd" in main_res:
+        out["ms_per_step_autograd"] = round(main_res["ms_per_step_autograd"], 4)
+    for cfg, res in results.items():
+        if cfg == args.config:
+            continue
+        out[f"config{cfg}"] = {
+            "batch": CONFIGS[cfg]["batch"], "seq_len": CONFIGS[cfg]["seq"],
+            "tflops": round(res["tflops"], 2),
+            "pct_of_peak": round(100 * res["tflops"] / PEAK_BF16_TFLOPS, 2),
+            "ms_per_step": round(res["ms_per_step"], 4),
+            "fwd_tflops": round(res["fwd_tflops"], 2), "bwd_tflops": round(res["bwd_tflops"], 2),
+            "stage_ms": {k: round(v, 4) for k, v in res["stage_ms"].items()},
+        }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(S)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

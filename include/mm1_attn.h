@@ -1,0 +1,100 @@
+/* C ABI of the MI355X (gfx950) causal GQA flash-attention library.
+ *
+ * Drop-in boundary for the attention kernels of Mimans M1
+ * (CODE/mimans/model/attention_tilelang.py).  Plain C: bf16 tensors are passed
+ * as `void*`, fp32 tensors as `float*`, the HIP stream as `void*`
+ * (a hipStream_t; NULL = the default stream).  The caller owns every buffer;
+ * the library allocates nothing, never synchronises, keeps no state and is
+ * safe to call from several host threads.
+ *
+ * Layouts (all contiguous, last dimension stride 1):
+ *   q, o, dO, dq : [B, S, H,   D] bf16
+ *   k, v, dk, dv : [B, S, Hkv, D] bf16
+ *   lse2, delta  : [B, H, S]      fp32
+ * Requirements: B >= 1, S >= 1, H % Hkv == 0, D == 128, sm_scale > 0.
+ *
+ * Return value: 0 on success, a negative MM1_E_* code for an argument error,
+ * or a positive hipError_t from the launch.  mm1_attn_strerror() names both.
+ */
+#ifndef MM1_ATTN_H
+#define MM1_ATTN_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MM1_ATTN_VERSION 1
+
+#define MM1_OK 0
+#define MM1_E_NULL (-1)        /* a required pointer is NULL */
+#define MM1_E_SHAPE (-2)       /* B, S, H or Hkv out of range, or H % Hkv != 0 */
+#define MM1_E_HEAD_DIM (-3)    /* head_dim other than 128 */
+#define MM1_E_WORKSPACE (-4)   /* workspace smaller than mm1_attn_bwd_workspace_size() */
+#define MM1_E_SCALE (-5)       /* sm_scale not a positive finite number */
+#define MM1_E_ALIGN (-6)       /* a tensor pointer is not 16-byte aligned */
+
+/* Library version (MM1_ATTN_VERSION of the build). */
+int mm1_attn_version(void);
+
+/* Forward: o = softmax(q k^T * sm_scale [+ causal mask]) v, per query head h
+ * reading KV head h / (H / Hkv); lse2[b,h,i] = log2(e) * logsumexp_j(s_ij).
+ * Replaces get_kernel("fwd", B, H, S, D, causal, groups)(q, k, v) -> (O, lse),
+ * the TileLang kernel flash_fwd (attention_tilelang.py:110-190, called :364). */
+int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
+                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                 void* stream);
+
+/* Backward preprocess: delta[b,h,i] = sum_d o[b,i,h,d] * dO[b,i,h,d] (fp32).
+ * Replaces flash_delta(B, H, S, D)(O, dO) -> Delta
+ * (attention_tilelang.py:192-217, called :380). */
+int mm1_attn_delta(const void* o, const void* dO, float* delta,
+                   int B, int S, int H, int D, void* stream);
+
+/* Bytes of fp32 scratch mm1_attn_bwd needs for the per-head dK/dV partial sums
+ * (0 when H == Hkv).  No counterpart in the reference, whose backward takes
+ * caller-zeroed fp32 dQ/dK/dV accumulators instead (attention_tilelang.py:381-383). */
+size_t mm1_attn_bwd_workspace_size(int B, int S, int H, int Hkv, int D);
+
+/* Backward: given delta from mm1_attn_delta, writes bf16 dq, dk, dv directly.
+ * Replaces get_kernel("bwd", ...)(q, k, v, dO, lse, Delta, dQ, dK, dV) followed
+ * by flash_unswizzle and the dk/dv casts (attention_tilelang.py:242-323, :385-389).
+ * Deterministic: no atomics; bitwise identical across repeated calls. */
+int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
+                 const float* lse2, const float* delta,
+                 void* dq, void* dk, void* dv,
+                 void* workspace, size_t workspace_bytes,
+                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                 void* stream);
+
+/* The three stages mm1_attn_bwd runs, in order, for callers that schedule or
+ * time them separately (same arguments and checks as mm1_attn_bwd).
+ *  - mm1_attn_bwd_dkdv: dK/dV.  With H == Hkv it writes bf16 dk, dv directly;
+ *    otherwise it writes the per-query-head fp32 partial sums into `workspace`
+ *    ([2][G][B][S][Hkv][D], G = H / Hkv) and leaves dk/dv untouched.
+ *  - mm1_attn_bwd_dkdv_reduce: sums the G partials of each KV head and writes
+ *    bf16 dk, dv (no-op when H == Hkv).
+ *  - mm1_attn_bwd_dq: bf16 dq.
+ * Together they replace flash_bwd + flash_unswizzle + casts
+ * (attention_tilelang.py:242-323, :385-389); no counterpart as separate calls. */
+int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
+                      const float* lse2, const float* delta, void* dk, void* dv,
+                      void* workspace, size_t workspace_bytes,
+                      int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                      void* stream);
+int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
+                             int B, int S, int H, int Hkv, int D, void* stream);
+int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
+                    const float* lse2, const float* delta, void* dq,
+                    int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                    void* stream);
+
+/* Static description of a return code. */
+const char* mm1_attn_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MM1_ATTN_H */

@@ -1,0 +1,78 @@
+"""ctypes binding of the C ABI declared in include/mm1_attn.h.
+
+The library is built in-tree by ``mimansm1_v1_amd.build`` (hipcc, gfx950).  It
+is the only compute path of this package: if it is missing, every entry point
+raises -- there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+from . import build as _build
+
+# Every symbol include/mm1_attn.h declares, with its ctypes signature.
+_c_int, _c_float, _c_size, _vp = ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+SIGNATURES = {
+    "mm1_attn_version": (_c_int, []),
+    "mm1_attn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp,
+                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_delta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "mm1_attn_bwd_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "mm1_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
+                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_bwd_dkdv": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
+                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_bwd_dkdv_reduce": (_c_int, [_vp, _c_size, _vp, _vp,
+                                          _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "mm1_attn_bwd_dq": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_strerror": (ctypes.c_char_p, [_c_int]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def library_path() -> Path:
+    return _build.library_path()
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the attention library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = library_path()
+            if not path.exists():
+                raise LibraryMissing(
+                    f"{path} is not built; run `python -m mimansm1_v1_amd.build` "
+                    "(hipcc, gfx950) first")
+            lib = ctypes.CDLL(str(path))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+class AttnError(RuntimeError):
+    """A nonzero return code of the C ABI."""
+
+    def __init__(self, code: int, where: str):
+        self.code = code
+        msg = load().mm1_attn_strerror(code).decode()
+        super().__init__(f"{where}: {msg} (code {code})")
+
+
+def check(code: int, where: str) -> None:
+    if code != 0:
+        raise AttnError(code, where)

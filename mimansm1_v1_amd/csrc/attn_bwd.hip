@@ -1,0 +1,464 @@
+// Causal / full GQA flash-attention backward for gfx950.
+//
+// The reference computes the backward as one KV-stationary kernel that pushes
+// dQ, dK and dV out with fp32 atomics (flash_delta / flash_bwd,
+// CODE/mimans/model/attention_tilelang.py:192-217 and :242-323).  The
+// arithmetic kept from it:
+//   Delta_i = sum_d O_id dO_id                     (:212-214)
+//   P_ij    = exp2(s_ij * scale2 - lse2_i)         (:297), zero above the diagonal (:298-301)
+//   dP_ij   = dO_i . V_j                           (:304)
+//   dV_j   += sum_i P_ij dO_i                      (:307)
+//   dS_ij   = P_ij (dP_ij - Delta_i)               (:310, rounded to bf16 for the products)
+//   dK_j   += sm_scale * sum_i dS_ij Q_i            (:311)
+//   dQ_i   += sm_scale * sum_j dS_ij K_j            (:314)
+// (sm_scale is applied to the fp32 accumulators instead of to dS.)
+//
+// The decomposition here is atomic-free and deterministic:
+//   * attn_delta_kernel   : Delta, one 16-lane group per (b, s, h) row.
+//   * attn_dkdv_kernel    : key-stationary, one workgroup per (128-key tile,
+//     query head).  Each wave keeps 32 keys of K and V in registers and dK/dV
+//     accumulators in registers while it walks the head's query tiles, which
+//     are staged in LDS both row-major and transposed.  With G > 1 the
+//     per-head partial sums go to an fp32 workspace [G][B][S][Hkv][D] and
+//     attn_dkdv_reduce_kernel adds the G heads of each group and rounds once.
+//   * attn_dq_kernel      : query-stationary over the packed GQA row space
+//     (as in the forward): K/V tiles in LDS serve all G heads of a group and
+//     dQ is written once in bf16 -- no fp32 scratch and no un-swizzle pass.
+#include "mm1_common.h"
+
+namespace mm1 {
+
+// ---------------------------------------------------------------------------
+// Delta = rowsum(O * dO) in fp32.
+__global__ __launch_bounds__(256) void attn_delta_kernel(
+    const __bf16* __restrict__ o, const __bf16* __restrict__ dO, float* __restrict__ delta,
+    int B, int S, int H) {
+  const long nrows = (long)B * S * H;
+  const long row = ((long)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const int c = threadIdx.x & 15;
+  if (row >= nrows) return;   // whole 16-lane groups leave together
+  const bf16x8 a = *reinterpret_cast<const bf16x8*>(o + row * HD + 8 * c);
+  const bf16x8 d = *reinterpret_cast<const bf16x8*>(dO + row * HD + 8 * c);
+  float acc = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc = fmaf((float)a[t], (float)d[t], acc);
+  acc += __shfl_xor(acc, 8);
+  acc += __shfl_xor(acc, 4);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 1);
+  if (c == 0) {
+    const int hh = (int)(row % H);
+    const long bs = row / H;
+    const int s = (int)(bs % S);
+    const int b = (int)(bs / S);
+    delta[((long)b * H + hh) * S + s] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV: one workgroup per (128-key tile, query head); 4 waves x 32 keys.
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_dkdv_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
+    float* __restrict__ ws_dk, float* __restrict__ ws_dv,
+    __bf16* __restrict__ dk, __bf16* __restrict__ dv,
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale) {
+  constexpr int BQ = TILE_ROWS;                      // query positions per iteration
+  constexpr int BUF = 4 * TILE_BYTES + 2 * BQ * 4;   // Q, Q^T, dO, dO^T, lse2, delta
+  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int nbh = B * H;
+  const int kt = blockIdx.x / nbh;        // heaviest key tiles first
+  const int bh = blockIdx.x % nbh;
+  const int b = bh / H, hq = bh % H;
+  const int g = hq / G, hh = hq % G;
+  const int kw0 = kt * 128 + 32 * w;      // this wave's first key
+  const int key = kw0 + l32;
+
+  // K and V rows of this lane's key as B operands (B[k=d][n=key]).
+  bf16x8 kreg[8], vreg[8];
+  {
+    const long off = ((long)(b * S + key) * Hkv + g) * HD + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      if (key < S) {
+        kreg[ks] = *reinterpret_cast<const bf16x8*>(k + off + 16 * ks);
+        vreg[ks] = *reinterpret_cast<const bf16x8*>(v + off + 16 * ks);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) { kreg[ks][t] = (__bf16)0.f; vreg[ks][t] = (__bf16)0.f; }
+      }
+    }
+  }
+
+  const int q_begin = CAUSAL ? kt * 128 : 0;
+  const int n_qt = (S - q_begin + BQ - 1) / BQ;
+  const long qstride = (long)H * HD;
+  const __bf16* qbase = q + ((long)b * S * H + hq) * HD;
+  const __bf16* dobase = dO + ((long)b * S * H + hq) * HD;
+  const float* lse_row = lse2 + ((long)b * H + hq) * S;
+  const float* dl_row = delta + ((long)b * H + hq) * S;
+
+  TileRegs qr, dr;
+  float lse_pre = 0.f, dl_pre = 0.f;
+  auto load_tile = [&](int p0) {
+    tile_load(qr, qbase + (long)p0 * qstride, qstride, S - p0, tid);
+    tile_load(dr, dobase + (long)p0 * qstride, qstride, S - p0, tid);
+    if (tid < BQ) {
+      const int p = p0 + tid;
+      lse_pre = p < S ? lse_row[p] : INFINITY;   // padded rows give P = 0
+      dl_pre = p < S ? dl_row[p] : 0.f;
+    }
+  };
+  auto store_tile = [&](char* buf) {
+    tile_store_rows(qr, buf, tid);
+    tile_store_tr(qr, buf + TILE_BYTES, tid);
+    tile_store_rows(dr, buf + 2 * TILE_BYTES, tid);
+    tile_store_tr(dr, buf + 3 * TILE_BYTES, tid);
+    if (tid < BQ) {
+      reinterpret_cast<float*>(buf + 4 * TILE_BYTES)[tid] = lse_pre;
+      reinterpret_cast<float*>(buf + 4 * TILE_BYTES + BQ * 4)[tid] = dl_pre;
+    }
+  };
+
+  load_tile(q_begin);
+  store_tile(smem);
+  __syncthreads();
+
+  f32x16 dkacc[4], dvacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) { dkacc[db] = zero16(); dvacc[db] = zero16(); }
+
+  for (int it = 0; it < n_qt; ++it) {
+    const char* buf = smem + (it & 1) * BUF;
+    const char* ql = buf;
+    const char* qtl = buf + TILE_BYTES;
+    const char* dol = buf + 2 * TILE_BYTES;
+    const char* dotl = buf + 3 * TILE_BYTES;
+    const float* lsel = reinterpret_cast<const float*>(buf + 4 * TILE_BYTES);
+    const float* dll = lsel + BQ;
+    const int p0 = q_begin + it * BQ;
+    const bool has_next = it + 1 < n_qt;
+    if (has_next) load_tile(p0 + BQ);
+
+    if (!CAUSAL || p0 + BQ - 1 >= kw0) {
+      const bool need_mask = CAUSAL && (p0 < kw0 + 31);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          s = mfma32(lds_a_rows(ql, qb, ks, lane), kreg[ks], s);
+          dp = mfma32(lds_a_rows(dol, qb, ks, lane), vreg[ks], dp);
+        }
+        // D layout: register r holds query 32*qb + 8*(r/4) + 4*h + (r%4) of this tile.
+        f32x16 pv, dsv;
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          const int i0 = 32 * qb + 8 * a4 + 4 * h;
+          const f32x4 lse4 = *reinterpret_cast<const f32x4*>(lsel + i0);
+          const f32x4 dl4 = *reinterpret_cast<const f32x4*>(dll + i0);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int r = 4 * a4 + c;
+            float p = exp2_fast(fmaf(s[r], scale2, -lse4[c]));
+            if (need_mask && key > p0 + i0 + c) p = 0.f;
+            pv[r] = p;
+            dsv[r] = p * (dp[r] - dl4[c]);
+          }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const bf16x8 pb = pack8(pv, 8 * ks);
+          const bf16x8 sb = pack8(dsv, 8 * ks);
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            dvacc[db] = mfma32(lds_a_tr(dotl, db, 2 * qb + ks, lane), pb, dvacc[db]);
+            dkacc[db] = mfma32(lds_a_tr(qtl, db, 2 * qb + ks, lane), sb, dkacc[db]);
+          }
+        }
+      }
+    }
+    if (has_next) store_tile(smem + ((it + 1) & 1) * BUF);
+    __syncthreads();
+  }
+
+  if (key >= S) return;
+  // D layout of dK^T / dV^T: register r of block db holds column
+  // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
+  if (G == 1) {
+    __bf16* dkrow = dk + ((long)(b * S + key) * Hkv + g) * HD;
+    __bf16* dvrow = dv + ((long)(b * S + key) * Hkv + g) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        bf16x4 kv4, vv4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          kv4[c] = (__bf16)(dkacc[db][4 * a4 + c] * sm_scale);
+          vv4[c] = (__bf16)(dvacc[db][4 * a4 + c]);
+        }
+        const int d = 32 * db + 8 * a4 + 4 * h;
+        *reinterpret_cast<bf16x4*>(dkrow + d) = kv4;
+        *reinterpret_cast<bf16x4*>(dvrow + d) = vv4;
+      }
+    }
+  } else {
+    const long slot = (long)hh * B * S * Hkv * HD;
+    float* dkrow = ws_dk + slot + ((long)(b * S + key) * Hkv + g) * HD;
+    float* dvrow = ws_dv + slot + ((long)(b * S + key) * Hkv + g) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        f32x4 kv4, vv4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          kv4[c] = dkacc[db][4 * a4 + c] * sm_scale;
+          vv4[c] = dvacc[db][4 * a4 + c];
+        }
+        const int d = 32 * db + 8 * a4 + 4 * h;
+        *reinterpret_cast<f32x4*>(dkrow + d) = kv4;
+        *reinterpret_cast<f32x4*>(dvrow + d) = vv4;
+      }
+    }
+  }
+}
+
+// Sum the G per-head partials of dK and dV and round to bf16 once.
+__global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(
+    const float* __restrict__ ws_dk, const float* __restrict__ ws_dv,
+    __bf16* __restrict__ dk, __bf16* __restrict__ dv, long n, int G) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  f32x4 sk = *reinterpret_cast<const f32x4*>(ws_dk + i);
+  f32x4 sv = *reinterpret_cast<const f32x4*>(ws_dv + i);
+  for (int j = 1; j < G; ++j) {
+    sk += *reinterpret_cast<const f32x4*>(ws_dk + (long)j * n + i);
+    sv += *reinterpret_cast<const f32x4*>(ws_dv + (long)j * n + i);
+  }
+  bf16x4 ok, ov;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) { ok[c] = (__bf16)sk[c]; ov[c] = (__bf16)sv[c]; }
+  *reinterpret_cast<bf16x4*>(dk + i) = ok;
+  *reinterpret_cast<bf16x4*>(dv + i) = ov;
+}
+
+// ---------------------------------------------------------------------------
+// dQ: one workgroup per 128 packed query rows (4 waves x 32); K/V tiles of 64
+// keys staged in LDS (K row-major and transposed, V row-major).
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_dq_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
+    __bf16* __restrict__ dq,
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles) {
+  constexpr int BM = 128;
+  constexpr int BN = TILE_ROWS;
+  constexpr int BUF = 3 * TILE_BYTES;   // K, K^T, V
+  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int nbg = B * Hkv;
+  int tile = blockIdx.x / nbg;
+  if (CAUSAL) tile = n_tiles - 1 - tile;
+  const int bg = blockIdx.x % nbg;
+  const int b = bg / Hkv, g = bg % Hkv;
+  const int R = G * S;
+  const int r0 = tile * BM;
+  const int rw0 = r0 + 32 * w;
+  const bool wave_active = rw0 < R;
+
+  const int rr = rw0 + l32;
+  const int qp = rr / G;
+  const int hh = rr - qp * G;
+  const bool row_valid = rr < R;
+  const long roff = ((long)(b * S + qp) * H + g * G + hh) * HD;
+  bf16x8 qreg[8], doreg[8];
+  float lse_i = INFINITY, dl_i = 0.f;
+  if (row_valid) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      qreg[ks] = *reinterpret_cast<const bf16x8*>(q + roff + 16 * ks + 8 * h);
+      doreg[ks] = *reinterpret_cast<const bf16x8*>(dO + roff + 16 * ks + 8 * h);
+    }
+    const long li = ((long)b * H + g * G + hh) * S + qp;
+    lse_i = lse2[li];
+    dl_i = delta[li];
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) { qreg[ks][t] = (__bf16)0.f; doreg[ks][t] = (__bf16)0.f; }
+    }
+  }
+
+  const int last_row_wg = min(r0 + BM, R) - 1;
+  const int n_kt = CAUSAL ? (min(S - 1, last_row_wg / G) / BN + 1) : (S + BN - 1) / BN;
+  const int pw_lo = rw0 / G;
+  const int pw_hi = wave_active ? min(S - 1, (min(rw0 + 32, R) - 1) / G) : -1;
+
+  const long kvstride = (long)Hkv * HD;
+  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
+  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
+
+  TileRegs kr, vr;
+  tile_load(kr, kbase, kvstride, S, tid);
+  tile_load(vr, vbase, kvstride, S, tid);
+  tile_store_rows(kr, smem, tid);
+  tile_store_tr(kr, smem + TILE_BYTES, tid);
+  tile_store_rows(vr, smem + 2 * TILE_BYTES, tid);
+  __syncthreads();
+
+  f32x16 dqacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) dqacc[db] = zero16();
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const char* kl = smem + (kt & 1) * BUF;
+    const char* ktl = kl + TILE_BYTES;
+    const char* vl = kl + 2 * TILE_BYTES;
+    const bool has_next = kt + 1 < n_kt;
+    if (has_next) {
+      const int nk = (kt + 1) * BN;
+      tile_load(kr, kbase + (long)nk * kvstride, kvstride, S - nk, tid);
+      tile_load(vr, vbase + (long)nk * kvstride, kvstride, S - nk, tid);
+    }
+    const int k0 = kt * BN;
+    if (wave_active && (!CAUSAL || k0 <= pw_hi)) {
+      f32x16 s[2], dp[2];
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) { s[jb] = zero16(); dp[jb] = zero16(); }
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+          s[jb] = mfma32(lds_a_rows(kl, jb, ks, lane), qreg[ks], s[jb]);
+          dp[jb] = mfma32(lds_a_rows(vl, jb, ks, lane), doreg[ks], dp[jb]);
+        }
+      }
+      const bool need_mask = CAUSAL ? (k0 + BN - 1 > pw_lo) : (k0 + BN > S);
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float p = exp2_fast(fmaf(s[jb][r], scale2, -lse_i));
+          if (need_mask) {
+            const int key = k0 + 32 * jb + 8 * (r >> 2) + 4 * h + (r & 3);
+            const bool masked = CAUSAL ? (key > qp) : (key >= S);
+            if (masked) p = 0.f;
+          }
+          s[jb][r] = p * (dp[jb][r] - dl_i);   // dS^T
+        }
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 sb = pack8(s[ks >> 1], 8 * (ks & 1));
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dqacc[db] = mfma32(lds_a_tr(ktl, db, ks, lane), sb, dqacc[db]);
+      }
+    }
+    if (has_next) {
+      char* nb = smem + ((kt + 1) & 1) * BUF;
+      tile_store_rows(kr, nb, tid);
+      tile_store_tr(kr, nb + TILE_BYTES, tid);
+      tile_store_rows(vr, nb + 2 * TILE_BYTES, tid);
+    }
+    __syncthreads();
+  }
+
+  if (!row_valid) return;
+  __bf16* dst = dq + roff;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      bf16x4 val;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) val[c] = (__bf16)(dqacc[db][4 * a4 + c] * sm_scale);
+      *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * a4 + 4 * h) = val;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int S, int H,
+                        hipStream_t stream) {
+  const long rows = (long)B * S * H;
+  const long blocks = (rows * 16 + 255) / 256;
+  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const __bf16*>(o), static_cast<const __bf16*>(dO), delta, B, S, H);
+  return hipGetLastError();
+}
+
+size_t bwd_workspace_bytes(int B, int S, int H, int Hkv) {
+  const int G = H / Hkv;
+  if (G <= 1) return 0;
+  return (size_t)2 * G * B * S * Hkv * HD * sizeof(float);
+}
+
+hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
+                           const float* lse2, const float* delta, void* dk, void* dv,
+                           void* workspace, int B, int S, int H, int Hkv, bool causal,
+                           float sm_scale, hipStream_t stream) {
+  const int G = H / Hkv;
+  const float scale2 = sm_scale * 1.4426950408889634f;
+  const long n_kv = (long)B * S * Hkv * HD;
+  float* ws_dk = static_cast<float*>(workspace);
+  float* ws_dv = ws_dk ? ws_dk + (long)G * n_kv : nullptr;
+  auto qp = static_cast<const __bf16*>(q);
+  auto kp = static_cast<const __bf16*>(k);
+  auto vp = static_cast<const __bf16*>(v);
+  auto dop = static_cast<const __bf16*>(dO);
+  auto dkp = static_cast<__bf16*>(dk);
+  auto dvp = static_cast<__bf16*>(dv);
+  const int n_ktiles = (S + 127) / 128;
+  dim3 grid(n_ktiles * B * H);
+  if (causal)
+    hipLaunchKernelGGL(attn_dkdv_kernel<true>, grid, dim3(256), 0, stream, qp, kp, vp, dop, lse2, delta,
+                       ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale);
+  else
+    hipLaunchKernelGGL(attn_dkdv_kernel<false>, grid, dim3(256), 0, stream, qp, kp, vp, dop, lse2, delta,
+                       ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
+                             hipStream_t stream) {
+  const int G = H / Hkv;
+  if (G <= 1) return hipSuccess;
+  const long n_kv = (long)B * S * Hkv * HD;
+  const float* ws_dk = static_cast<const float*>(workspace);
+  const float* ws_dv = ws_dk + (long)G * n_kv;
+  const long blocks = (n_kv / 4 + 255) / 256;
+  hipLaunchKernelGGL(attn_dkdv_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     ws_dk, ws_dv, static_cast<__bf16*>(dk), static_cast<__bf16*>(dv), n_kv, G);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
+                         const float* lse2, const float* delta, void* dq,
+                         int B, int S, int H, int Hkv, bool causal, float sm_scale,
+                         hipStream_t stream) {
+  const int G = H / Hkv;
+  const float scale2 = sm_scale * 1.4426950408889634f;
+  auto qp = static_cast<const __bf16*>(q);
+  auto kp = static_cast<const __bf16*>(k);
+  auto vp = static_cast<const __bf16*>(v);
+  auto dop = static_cast<const __bf16*>(dO);
+  auto dqp = static_cast<__bf16*>(dq);
+  const int n_qtiles = (G * S + 127) / 128;
+  dim3 grid(n_qtiles * B * Hkv);
+  if (causal)
+    hipLaunchKernelGGL(attn_dq_kernel<true>, grid, dim3(256), 0, stream, qp, kp, vp, dop, lse2, delta, dqp,
+                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles);
+  else
+    hipLaunchKernelGGL(attn_dq_kernel<false>, grid, dim3(256), 0, stream, qp, kp, vp, dop, lse2, delta, dqp,
+                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles);
+  return hipGetLastError();
+}
+
+}  // namespace mm1

@@ -1,0 +1,151 @@
+// extern "C" entry points: argument checks, then the kernel launchers.
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/mm1_attn.h"
+#include "mm1_common.h"
+
+namespace mm1 {
+hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
+                      int B, int S, int H, int Hkv, bool causal, float sm_scale, int qw,
+                      hipStream_t stream);
+hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int S, int H,
+                        hipStream_t stream);
+size_t bwd_workspace_bytes(int B, int S, int H, int Hkv);
+hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
+                           const float* lse2, const float* delta, void* dk, void* dv,
+                           void* workspace, int B, int S, int H, int Hkv, bool causal,
+                           float sm_scale, hipStream_t stream);
+hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
+                             hipStream_t stream);
+hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
+                         const float* lse2, const float* delta, void* dq,
+                         int B, int S, int H, int Hkv, bool causal, float sm_scale,
+                         hipStream_t stream);
+}  // namespace mm1
+
+namespace {
+
+// Largest sizes the 32-bit index arithmetic inside the kernels allows.
+constexpr long kMaxRows = 1L << 30;
+
+int check_shape(int B, int S, int H, int Hkv, int D) {
+  if (B < 1 || S < 1 || H < 1 || Hkv < 1 || H % Hkv != 0) return MM1_E_SHAPE;
+  if ((long)B * S * H > kMaxRows || (long)(H / Hkv) * S > kMaxRows) return MM1_E_SHAPE;
+  if (D != mm1::HD) return MM1_E_HEAD_DIM;
+  return MM1_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int from_hip(hipError_t e) { return e == hipSuccess ? MM1_OK : static_cast<int>(e); }
+
+}  // namespace
+
+extern "C" {
+
+int mm1_attn_version(void) { return MM1_ATTN_VERSION; }
+
+int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
+                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                 void* stream) {
+  if (!q || !k || !v || !o || !lse2) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MM1_E_ALIGN;
+  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale, 64,
+                                  static_cast<hipStream_t>(stream)));
+}
+
+int mm1_attn_delta(const void* o, const void* dO, float* delta, int B, int S, int H, int D,
+                   void* stream) {
+  if (!o || !dO || !delta) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, 1, D);
+  if (rc) return rc;
+  if (!aligned16(o) || !aligned16(dO)) return MM1_E_ALIGN;
+  return from_hip(mm1::launch_delta(o, dO, delta, B, S, H, static_cast<hipStream_t>(stream)));
+}
+
+size_t mm1_attn_bwd_workspace_size(int B, int S, int H, int Hkv, int D) {
+  if (check_shape(B, S, H, Hkv, D) != MM1_OK) return 0;
+  return mm1::bwd_workspace_bytes(B, S, H, Hkv);
+}
+
+int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
+                      const float* lse2, const float* delta, void* dk, void* dv,
+                      void* workspace, size_t workspace_bytes,
+                      int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                      void* stream) {
+  if (!q || !k || !v || !dO || !lse2 || !delta || !dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
+  const size_t need = mm1::bwd_workspace_bytes(B, S, H, Hkv);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return MM1_E_WORKSPACE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dk) ||
+      !aligned16(dv) || (need > 0 && !aligned16(workspace)))
+    return MM1_E_ALIGN;
+  return from_hip(mm1::launch_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, need > 0 ? workspace : nullptr,
+                                       B, S, H, Hkv, causal != 0, sm_scale,
+                                       static_cast<hipStream_t>(stream)));
+}
+
+int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
+                             int B, int S, int H, int Hkv, int D, void* stream) {
+  if (!dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  const size_t need = mm1::bwd_workspace_bytes(B, S, H, Hkv);
+  if (need == 0) return MM1_OK;
+  if (!workspace || workspace_bytes < need) return MM1_E_WORKSPACE;
+  if (!aligned16(workspace) || !aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
+  return from_hip(mm1::launch_bwd_reduce(workspace, dk, dv, B, S, H, Hkv,
+                                         static_cast<hipStream_t>(stream)));
+}
+
+int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
+                    const float* lse2, const float* delta, void* dq,
+                    int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                    void* stream) {
+  if (!q || !k || !v || !dO || !lse2 || !delta || !dq) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq))
+    return MM1_E_ALIGN;
+  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, B, S, H, Hkv, causal != 0,
+                                     sm_scale, static_cast<hipStream_t>(stream)));
+}
+
+int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
+                 const float* lse2, const float* delta,
+                 void* dq, void* dk, void* dv,
+                 void* workspace, size_t workspace_bytes,
+                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                 void* stream) {
+  if (!dq) return MM1_E_NULL;
+  int rc = mm1_attn_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes,
+                             B, S, H, Hkv, D, causal, sm_scale, stream);
+  if (rc) return rc;
+  rc = mm1_attn_bwd_dkdv_reduce(workspace, workspace_bytes, dk, dv, B, S, H, Hkv, D, stream);
+  if (rc) return rc;
+  return mm1_attn_bwd_dq(q, k, v, dO, lse2, delta, dq, B, S, H, Hkv, D, causal, sm_scale, stream);
+}
+
+const char* mm1_attn_strerror(int code) {
+  switch (code) {
+    case MM1_OK: return "success";
+    case MM1_E_NULL: return "mm1_attn: a required pointer is NULL";
+    case MM1_E_SHAPE: return "mm1_attn: bad shape (need B, S, H, Hkv >= 1 and H % Hkv == 0)";
+    case MM1_E_HEAD_DIM: return "mm1_attn: head_dim must be 128";
+    case MM1_E_WORKSPACE: return "mm1_attn: workspace smaller than mm1_attn_bwd_workspace_size()";
+    case MM1_E_SCALE: return "mm1_attn: sm_scale must be a positive finite number";
+    case MM1_E_ALIGN: return "mm1_attn: tensor pointers must be 16-byte aligned";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "mm1_attn: unknown error";
+}
+
+}  // extern "C"
