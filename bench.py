@@ -55,6 +55,9 @@ def parse(argv=None):
                     help="extra configs reported beside the main one")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-autograd", action="store_true", help="skip the autograd cross-check")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run --steps device-to-device copies of MIB MiB (a plain copy "
+                         "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--traffic", default=None,
                     help="JSON with HBM bytes per launch from rocprofv3 --pmc "
                          "(default profiles/traffic_config<N>.json if present)")
@@ -222,6 +225,16 @@ def main(argv=None):
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     device = torch.device("cuda:0")
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n * 4, "launches": args.steps}), flush=True)
+        return 0
 
     results = {}
     for cfg in [args.config] + [c for c in args.also if c != args.config]:

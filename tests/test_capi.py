@@ -1,0 +1,109 @@
+"""The C-ABI library: loads, exports every declared symbol, validates its
+arguments before touching a device.  No GPU needed (and none is touched: every
+call here returns from the argument checks)."""
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from mimansm1_v1_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mm1_attn.h"
+FAKE = 1 << 20  # aligned, non-null; never dereferenced (calls fail validation first)
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mm1_attn_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_library_built_in_tree(lib):
+    path = _lib.library_path()
+    assert path.exists() and ROOT in path.parents
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 8
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.library_path())],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (mm1_attn_\w+)", out))
+    assert set(names) <= exported, set(names) - exported
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table and header disagree"
+    for n in names:
+        getattr(lib, n)
+
+
+def test_version_matches_header(lib):
+    m = re.search(r"#define MM1_ATTN_VERSION (\d+)", HEADER.read_text())
+    assert lib.mm1_attn_version() == int(m.group(1))
+
+
+def test_error_codes_and_messages(lib):
+    codes = dict(re.findall(r"#define (MM1_E_\w+) \((-\d+)\)", HEADER.read_text()))
+    assert len(codes) == 6
+    for name, code in codes.items():
+        msg = lib.mm1_attn_strerror(int(code)).decode()
+        assert msg.startswith("mm1_attn:") and "unknown" not in msg, name
+    assert lib.mm1_attn_strerror(0) == b"success"
+    assert b"unknown" in lib.mm1_attn_strerror(-99)
+
+
+def fwd(lib, q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=FAKE, B=1, S=64, H=10, Hkv=2, D=128,
+        causal=1, scale=0.088):
+    return lib.mm1_attn_fwd(q, k, v, o, lse, B, S, H, Hkv, D, causal, scale, None)
+
+
+def test_fwd_argument_errors(lib):
+    assert fwd(lib, q=None) == -1
+    assert fwd(lib, lse=None) == -1
+    assert fwd(lib, H=10, Hkv=3) == -2
+    assert fwd(lib, B=0) == -2
+    assert fwd(lib, S=0) == -2
+    assert fwd(lib, D=64) == -3
+    assert fwd(lib, scale=0.0) == -5
+    assert fwd(lib, scale=float("nan")) == -5
+    assert fwd(lib, q=FAKE + 8) == -6
+
+
+def test_bwd_argument_errors(lib):
+    need = lib.mm1_attn_bwd_workspace_size(2, 100, 10, 2, 128)
+    assert need == 2 * 5 * 2 * 100 * 2 * 128 * 4
+    assert lib.mm1_attn_bwd_workspace_size(2, 100, 4, 4, 128) == 0
+    assert lib.mm1_attn_bwd_workspace_size(2, 100, 10, 3, 128) == 0   # invalid shape
+
+    def bwd(ws=FAKE, ws_bytes=None, **kw):
+        a = dict(B=2, S=100, H=10, Hkv=2, D=128, causal=1, scale=0.088)
+        a.update(kw)
+        nb = need if ws_bytes is None else ws_bytes
+        return lib.mm1_attn_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, nb,
+                                a["B"], a["S"], a["H"], a["Hkv"], a["D"], a["causal"], a["scale"],
+                                None)
+
+    assert bwd(ws=None) == -4
+    assert bwd(ws_bytes=need - 1) == -4
+    assert bwd(D=256) == -3
+    assert bwd(H=9) == -2
+    assert bwd(scale=-1.0) == -5
+    assert bwd(ws=FAKE + 4) == -6
+    assert lib.mm1_attn_bwd_dq(FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE,
+                               1, 64, 10, 2, 128, 1, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 10, 2, 128, None) == -4
+    # nothing to reduce without groups: success without a device call
+    assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 4, 4, 128, None) == 0
+    assert lib.mm1_attn_delta(FAKE, None, FAKE, 1, 64, 10, 128, None) == -1
+    assert lib.mm1_attn_delta(FAKE, FAKE, FAKE, 1, 64, 10, 64, None) == -3
+
+
+def test_python_error_wrapper(lib):
+    with pytest.raises(_lib.AttnError, match="head_dim must be 128"):
+        _lib.check(-3, "mm1_attn_fwd")

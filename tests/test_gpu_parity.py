@@ -158,3 +158,16 @@ def test_native_library_is_in_tree(hip_device):
     L.load()
     maps = open("/proc/self/maps").read()
     assert str(L.library_path()) in maps
+
+
+def test_golden_fixtures(hip_device):
+    """Kernel vs the committed fp64 brute-force fixtures (tests/golden)."""
+    from tests.golden.make_golden import load_cases
+    for name, c in load_cases().items():
+        B, S, H, Hkv, causal = c["meta"]
+        log(f"[case] golden {name}")
+        o, lse, dq, dk, dv = hip_run(c["q"], c["k"], c["v"], c["do"], causal, H // Hkv, hip_device)
+        assert_bf16_close("O", o, c["o"], log)
+        assert_lse_close(lse, c["lse2"], log)
+        for key, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+            assert_bf16_close(key, got, c[key], log)

@@ -1,0 +1,212 @@
+"""Pins the CPU oracle (oracle/reference.py) -- no GPU.
+
+Each restated function is checked against something that does not share its
+code: the fp64 C brute force (oracle/brute_attn.c, direct loops and a chain-
+rule backward), torch's scaled_dot_product_attention, closed forms and
+invariants, and the committed fixtures.  The last group plants mistakes in the
+oracle and shows the pins catch them."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import brute
+from oracle import reference as R
+from tests.golden.make_golden import CASES, load_cases
+
+SHAPES = [  # (B, S, H, Hkv)
+    (1, 1, 10, 2),
+    (2, 7, 10, 2),
+    (1, 19, 4, 4),
+    (2, 13, 6, 3),
+    (1, 24, 8, 1),
+]
+
+
+def _np(t):
+    return t.detach().double().numpy()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_forward_and_lse_match_brute_force(shape, causal):
+    B, S, H, Hkv = shape
+    q, k, v, _ = R.make_inputs(B, S, H, Hkv, 128, seed=S, dtype=torch.float64)
+    o_ref, lse_ref = brute.fwd(_np(q), _np(k), _np(v), causal)
+    o = R.attention(q, k, v, causal, H // Hkv, torch.float64)
+    lse = R.lse2(q, k, causal, H // Hkv, torch.float64)
+    assert np.abs(_np(o) - o_ref).max() < 1e-12
+    assert np.abs(_np(lse) - lse_ref).max() < 1e-12
+    o_c, lse_c = R.forward_chunked(q, k, v, causal, H // Hkv, torch.float64)
+    assert np.abs(_np(o_c) - o_ref).max() < 1e-12
+    assert np.abs(_np(lse_c) - lse_ref).max() < 1e-12
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_gradients_match_brute_force(shape, causal):
+    B, S, H, Hkv = shape
+    q, k, v, do = R.make_inputs(B, S, H, Hkv, 128, seed=S + 1, dtype=torch.float64)
+    want = brute.bwd(_np(q), _np(k), _np(v), _np(do), causal)
+    for got in (R.grads(q, k, v, do, causal, H // Hkv, torch.float64),
+                R.grads_analytic(q, k, v, do, causal, H // Hkv, torch.float64)):
+        for g, w in zip(got, want):
+            assert np.abs(_np(g) - w).max() < 1e-11
+
+
+def test_fp32_oracle_close_to_fp64():
+    q, k, v, do = R.make_inputs(2, 64, 10, 2, 128, seed=3)
+    o64 = R.attention(q, k, v, True, 5, torch.float64, cast=False)
+    o32 = R.attention(q, k, v, True, 5, cast=False)
+    assert (o32.double() - o64).abs().max() < 1e-5
+    for a, b in zip(R.grads(q, k, v, do, True, 5), R.grads(q, k, v, do, True, 5, torch.float64)):
+        assert (a.double() - b).abs().max() < 1e-4
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_matches_sdpa(causal):
+    q, k, v, _ = R.make_inputs(2, 96, 10, 2, 128, seed=4, dtype=torch.float32)
+    want = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                          is_causal=causal, enable_gqa=True).transpose(1, 2)
+    got = R.attention(q, k, v, causal, 5)
+    assert (got - want).abs().max() < 2e-5
+
+
+def test_single_position_returns_v():
+    q, k, v, _ = R.make_inputs(3, 1, 10, 2, 128, seed=5, dtype=torch.float64)
+    o = R.attention(q, k, v, True, 5, torch.float64)
+    assert torch.equal(o, v.repeat_interleave(5, dim=2))
+    # one key: lse2 is the single scaled score in log2 units
+    s = (q * k.repeat_interleave(5, dim=2)).sum(-1) / math.sqrt(128) * R.LOG2E
+    assert (R.lse2(q, k, True, 5, torch.float64) - s.permute(0, 2, 1)).abs().max() < 1e-12
+
+
+def test_constant_v_and_constant_k():
+    q, k, v, _ = R.make_inputs(1, 40, 10, 2, 128, seed=6, dtype=torch.float64)
+    c = torch.full_like(v, 0.75)
+    assert (R.attention(q, k, c, True, 5, torch.float64) - 0.75).abs().max() < 1e-14
+    # K = 0: every visible score is 0, so O_i is the prefix mean of V and
+    # lse2_i = log2(i + 1).
+    z = torch.zeros_like(k)
+    o = R.attention(q, z, v, True, 5, torch.float64)
+    prefix = v.cumsum(1) / torch.arange(1, 41, dtype=torch.float64).view(1, 40, 1, 1)
+    assert (o - prefix.repeat_interleave(5, dim=2)).abs().max() < 1e-12
+    lse = R.lse2(q, z, True, 5, torch.float64)
+    assert (lse - torch.log2(torch.arange(1, 41, dtype=torch.float64))).abs().max() < 1e-12
+
+
+def test_lse_lower_bound():
+    q, k, _, _ = R.make_inputs(2, 50, 10, 2, 128, seed=7, dtype=torch.float64)
+    lse = R.lse2(q, k, True, 5, torch.float64)
+    smax = R.scores(q, k, True, 5, torch.float64).amax(-1) * R.LOG2E
+    assert (lse - smax).min() >= 0
+
+
+def test_causal_no_leak_and_batch_permutation():
+    q, k, v, _ = R.make_inputs(2, 33, 10, 2, 128, seed=8, dtype=torch.float64)
+    o = R.attention(q, k, v, True, 5, torch.float64)
+    q2, k2, v2 = q.clone(), k.clone(), v.clone()
+    q2[:, -1] += 10
+    k2[:, -1] -= 3
+    v2[:, -1] *= 7
+    o2 = R.attention(q2, k2, v2, True, 5, torch.float64)
+    assert torch.equal(o[:, :-1], o2[:, :-1])
+    perm = torch.tensor([1, 0])
+    assert torch.equal(R.attention(q[perm], k[perm], v[perm], True, 5, torch.float64), o[perm])
+
+
+def test_identical_heads_in_a_group_give_identical_outputs():
+    q, k, v, _ = R.make_inputs(1, 20, 10, 2, 128, seed=9, dtype=torch.float64)
+    q[:, :, 1] = q[:, :, 0]
+    q[:, :, 7] = q[:, :, 0]  # head 7 reads KV head 1: different output
+    o = R.attention(q, k, v, True, 5, torch.float64)
+    assert torch.equal(o[:, :, 1], o[:, :, 0])
+    assert not torch.allclose(o[:, :, 7], o[:, :, 0])
+
+
+def test_delta_closed_form():
+    q, k, v, do = R.make_inputs(1, 16, 10, 2, 128, seed=10)
+    o = R.attention(q, k, v, True, 5)
+    d = R.delta(o, do)
+    want = torch.einsum("bshd,bshd->bhs", o.float(), do.float())
+    assert (d - want).abs().max() < 1e-5
+
+
+def test_golden_fixtures_reproduce():
+    cases = load_cases()
+    assert set(cases) == set(CASES)
+    for name, c in cases.items():
+        B, S, H, Hkv, causal = c["meta"]
+        G = H // Hkv
+        o = R.attention(c["q"], c["k"], c["v"], causal, G, cast=False)
+        assert (o - c["o"]).abs().max() < 1e-5, name
+        assert (R.lse2(c["q"], c["k"], causal, G) - c["lse2"]).abs().max() < 1e-5, name
+        for got, key in zip(R.grads(c["q"], c["k"], c["v"], c["do"], causal, G), ("dq", "dk", "dv")):
+            assert (got - c[key]).abs().max() < 1e-4, (name, key)
+
+
+def test_config_input_recipe():
+    q, k, v, do = R.make_inputs(1, 64, 10, 2, 128, seed=0)
+    q2, *_ = R.make_inputs(1, 64, 10, 2, 128, seed=0)
+    assert torch.equal(q, q2) and q.dtype == torch.bfloat16
+    # config 4: sigma-scaled, RoPE-rotated Q/K; rotation preserves per-vector norms
+    qr, kr, _, _ = R.make_inputs(1, 64, 10, 2, 128, seed=0, rope_sigma=True, dtype=torch.float32)
+    gen = torch.Generator().manual_seed(0)
+    raw_q = torch.randn(1, 64, 10, 128, generator=gen)
+    ratio = qr.norm(dim=-1) / raw_q.norm(dim=-1)
+    per_head = ratio.mean(dim=(0, 1))
+    assert (ratio - per_head).abs().max() < 1e-4      # one sigma per head
+    assert per_head.min() >= 0.5 and per_head.max() <= 3.0
+
+
+def test_rope_matches_rotation_of_pairs():
+    x = torch.randn(1, 12, 2, 128, dtype=torch.float64)
+    y = R.rope(x, 10_000.0)
+    i, pos = 5, 9
+    ang = pos * 10_000.0 ** (-2 * i / 128)
+    a, b = x[0, pos, 0, i], x[0, pos, 0, i + 64]
+    assert abs(y[0, pos, 0, i] - (a * math.cos(ang) - b * math.sin(ang))) < 1e-12
+    assert abs(y[0, pos, 0, i + 64] - (a * math.sin(ang) + b * math.cos(ang))) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# Planted mistakes: a wrong oracle must fail the pins above.
+def test_planted_wrong_gqa_mapping_is_caught(monkeypatch):
+    q, k, v, _ = R.make_inputs(1, 9, 10, 2, 128, seed=11, dtype=torch.float64)
+    o_ref, _ = brute.fwd(_np(q), _np(k), _np(v), True)
+    # query head h reading KV head h % Hkv instead of h // groups
+    monkeypatch.setattr(R, "_expand_kv", lambda t, g: t.repeat(1, 1, g, 1))
+    o = R.attention(q, k, v, True, 5, torch.float64)
+    assert np.abs(_np(o) - o_ref).max() > 1e-3
+
+
+def test_planted_strict_causal_mask_is_caught():
+    q, k, v, _ = R.make_inputs(1, 9, 10, 2, 128, seed=12, dtype=torch.float64)
+    o_ref, _ = brute.fwd(_np(q), _np(k), _np(v), True)
+    s = R.scores(q, k, False, 5, torch.float64)
+    wrong = s.masked_fill(~torch.ones(9, 9, dtype=torch.bool).tril(-1), float("-inf"))
+    p = wrong.softmax(-1).nan_to_num(0.0)
+    o = torch.matmul(p, v.repeat_interleave(5, dim=2).permute(0, 2, 1, 3)).permute(0, 2, 1, 3)
+    assert np.abs(_np(o) - o_ref).max() > 1e-3
+
+
+def test_planted_missing_group_sum_is_caught():
+    q, k, v, do = R.make_inputs(1, 9, 10, 2, 128, seed=13, dtype=torch.float64)
+    _, dk_ref, _ = brute.bwd(_np(q), _np(k), _np(v), _np(do), True)
+    _, dk, _ = R.grads_analytic(q, k, v, do, True, 5, torch.float64)
+    # keep only the first query head of each group instead of summing all five
+    dk_one = R.grads_analytic(q[:, :, ::5].contiguous(), k, v, do[:, :, ::5].contiguous(),
+                              True, 1, torch.float64)[1]
+    assert np.abs(_np(dk) - dk_ref).max() < 1e-11
+    assert np.abs(_np(dk_one) - dk_ref).max() > 1e-3
+
+
+def test_planted_lse_natural_log_is_caught():
+    q, k, v, _ = R.make_inputs(1, 9, 10, 2, 128, seed=14, dtype=torch.float64)
+    _, lse_ref = brute.fwd(_np(q), _np(k), _np(v), True)
+    wrong = torch.logsumexp(R.scores(q, k, True, 5, torch.float64), dim=-1)  # missing log2(e)
+    assert np.abs(_np(wrong) - lse_ref).max() > 1e-3
