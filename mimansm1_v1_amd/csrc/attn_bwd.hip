@@ -18,7 +18,8 @@
 //   * attn_dkdv_kernel    : key-stationary, one workgroup per (128-key tile,
 //     query head).  Each wave keeps 32 keys of K and V in registers and dK/dV
 //     accumulators in registers while it walks the head's query tiles, which
-//     are staged in LDS both row-major and transposed.  With G > 1 the
+//     arrive in LDS by DMA (row-major; transposed operands are read with the
+//     LDS transpose read).  With G > 1 the
 //     per-head partial sums go to an fp32 workspace [G][B][S][Hkv][D] and
 //     attn_dkdv_reduce_kernel adds the G heads of each group and rounds once.
 //   * attn_dq_kernel      : query-stationary over the packed GQA row space
@@ -57,16 +58,19 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 
 // ---------------------------------------------------------------------------
 // dK, dV: one workgroup per (128-key tile, query head); 4 waves x 32 keys.
+// Query tiles (Q, dO row-major; lse2, Delta) arrive by LDS DMA in a two-stage
+// ring; the transposed operands of dV^T = dO^T P and dK^T = Q^T dS are read
+// from the same row-major tiles with the LDS transpose read.
 template <bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_dkdv_kernel(
+__global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     float* __restrict__ ws_dk, float* __restrict__ ws_dv,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale) {
   constexpr int BQ = TILE_ROWS;                      // query positions per iteration
-  constexpr int BUF = 4 * TILE_BYTES + 2 * BQ * 4;   // Q, Q^T, dO, dO^T, lse2, delta
-  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
+  constexpr int BUF = 2 * TILE_BYTES + 2 * BQ * 4;   // Q, dO, lse2, delta
+  __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int nbh = B * H;
@@ -77,22 +81,6 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(
   const int kw0 = kt * 128 + 32 * w;      // this wave's first key
   const int key = kw0 + l32;
 
-  // K and V rows of this lane's key as B operands (B[k=d][n=key]).
-  bf16x8 kreg[8], vreg[8];
-  {
-    const long off = ((long)(b * S + key) * Hkv + g) * HD + 8 * h;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      if (key < S) {
-        kreg[ks] = *reinterpret_cast<const bf16x8*>(k + off + 16 * ks);
-        vreg[ks] = *reinterpret_cast<const bf16x8*>(v + off + 16 * ks);
-      } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) { kreg[ks][t] = (__bf16)0.f; vreg[ks][t] = (__bf16)0.f; }
-      }
-    }
-  }
-
   const int q_begin = CAUSAL ? kt * 128 : 0;
   const int n_qt = (S - q_begin + BQ - 1) / BQ;
   const long qstride = (long)H * HD;
@@ -101,50 +89,44 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(
   const float* lse_row = lse2 + ((long)b * H + hq) * S;
   const float* dl_row = delta + ((long)b * H + hq) * S;
 
-  TileRegs qr, dr;
-  float lse_pre = 0.f, dl_pre = 0.f;
-  auto load_tile = [&](int p0) {
-    tile_load(qr, qbase + (long)p0 * qstride, qstride, S - p0, tid);
-    tile_load(dr, dobase + (long)p0 * qstride, qstride, S - p0, tid);
-    if (tid < BQ) {
-      const int p = p0 + tid;
-      lse_pre = p < S ? lse_row[p] : INFINITY;   // padded rows give P = 0
-      dl_pre = p < S ? dl_row[p] : 0.f;
-    }
+  auto issue_tile = [&](char* buf, int p0) {
+    tile_dma<4>(buf, qbase + (long)p0 * qstride, qstride, S - p0, tid);
+    tile_dma<4>(buf + TILE_BYTES, dobase + (long)p0 * qstride, qstride, S - p0, tid);
+    if (w == 0) vec64_dma(buf + 2 * TILE_BYTES, lse_row + p0, S - p0, lane);
+    if (w == 1) vec64_dma(buf + 2 * TILE_BYTES + BQ * 4, dl_row + p0, S - p0, lane);
   };
-  auto store_tile = [&](char* buf) {
-    tile_store_rows(qr, buf, tid);
-    tile_store_tr(qr, buf + TILE_BYTES, tid);
-    tile_store_rows(dr, buf + 2 * TILE_BYTES, tid);
-    tile_store_tr(dr, buf + 3 * TILE_BYTES, tid);
-    if (tid < BQ) {
-      reinterpret_cast<float*>(buf + 4 * TILE_BYTES)[tid] = lse_pre;
-      reinterpret_cast<float*>(buf + 4 * TILE_BYTES + BQ * 4)[tid] = dl_pre;
-    }
-  };
+  issue_tile(smem, q_begin);
 
-  load_tile(q_begin);
-  store_tile(smem);
-  __syncthreads();
+  // K and V rows of this lane's key as B operands (B[k=d][n=key]).
+  bf16x8 kreg[8], vreg[8];
+  {
+    const int kk = min(key, S - 1);
+    const long off = ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      kreg[ks] = *reinterpret_cast<const bf16x8*>(k + off + 16 * ks);
+      vreg[ks] = *reinterpret_cast<const bf16x8*>(v + off + 16 * ks);
+    }
+  }
 
   f32x16 dkacc[4], dvacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) { dkacc[db] = zero16(); dvacc[db] = zero16(); }
+  wait_dma();
+  __syncthreads();
 
   for (int it = 0; it < n_qt; ++it) {
     const char* buf = smem + (it & 1) * BUF;
     const char* ql = buf;
-    const char* qtl = buf + TILE_BYTES;
-    const char* dol = buf + 2 * TILE_BYTES;
-    const char* dotl = buf + 3 * TILE_BYTES;
-    const float* lsel = reinterpret_cast<const float*>(buf + 4 * TILE_BYTES);
+    const char* dol = buf + TILE_BYTES;
+    const float* lsel = reinterpret_cast<const float*>(buf + 2 * TILE_BYTES);
     const float* dll = lsel + BQ;
     const int p0 = q_begin + it * BQ;
-    const bool has_next = it + 1 < n_qt;
-    if (has_next) load_tile(p0 + BQ);
+    if (it + 1 < n_qt) issue_tile(smem + ((it + 1) & 1) * BUF, p0 + BQ);
 
     if (!CAUSAL || p0 + BQ - 1 >= kw0) {
-      const bool need_mask = CAUSAL && (p0 < kw0 + 31);
+      // causal diagonal, or a last tile with rows past the sequence end
+      const bool need_mask = (CAUSAL && p0 < kw0 + 31) || (p0 + BQ > S);
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         f32x16 s = zero16(), dp = zero16();
@@ -164,7 +146,10 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(
           for (int c = 0; c < 4; ++c) {
             const int r = 4 * a4 + c;
             float p = exp2_fast(fmaf(s[r], scale2, -lse4[c]));
-            if (need_mask && key > p0 + i0 + c) p = 0.f;
+            if (need_mask) {
+              const int qp = p0 + i0 + c;
+              if ((CAUSAL && key > qp) || qp >= S) p = 0.f;
+            }
             pv[r] = p;
             dsv[r] = p * (dp[r] - dl4[c]);
           }
@@ -175,13 +160,13 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(
           const bf16x8 sb = pack8(dsv, 8 * ks);
 #pragma unroll
           for (int db = 0; db < 4; ++db) {
-            dvacc[db] = mfma32(lds_a_tr(dotl, db, 2 * qb + ks, lane), pb, dvacc[db]);
-            dkacc[db] = mfma32(lds_a_tr(qtl, db, 2 * qb + ks, lane), sb, dkacc[db]);
+            dvacc[db] = mfma32(lds_a_tr(dol, db, 2 * qb + ks, lane), pb, dvacc[db]);
+            dkacc[db] = mfma32(lds_a_tr(ql, db, 2 * qb + ks, lane), sb, dkacc[db]);
           }
         }
       }
     }
-    if (has_next) store_tile(smem + ((it + 1) & 1) * BUF);
+    wait_dma();
     __syncthreads();
   }
 
@@ -248,18 +233,19 @@ __global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dQ: one workgroup per 128 packed query rows (4 waves x 32); K/V tiles of 64
-// keys staged in LDS (K row-major and transposed, V row-major).
+// dQ: one workgroup per 128 packed query rows (4 waves x 32); K and V tiles of
+// 64 keys arrive by LDS DMA (row-major); K^T for dQ^T = K^T dS^T is read
+// transposed from the same K tile.
 template <bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_dq_kernel(
+__global__ __launch_bounds__(256, 2) void attn_dq_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     __bf16* __restrict__ dq,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles) {
   constexpr int BM = 128;
   constexpr int BN = TILE_ROWS;
-  constexpr int BUF = 3 * TILE_BYTES;   // K, K^T, V
-  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
+  constexpr int BUF = 2 * TILE_BYTES;   // K, V
+  __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int nbg = B * Hkv;
@@ -271,6 +257,12 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(
   const int r0 = tile * BM;
   const int rw0 = r0 + 32 * w;
   const bool wave_active = rw0 < R;
+
+  const long kvstride = (long)Hkv * HD;
+  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
+  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
+  tile_dma<4>(smem, kbase, kvstride, S, tid);
+  tile_dma<4>(smem + TILE_BYTES, vbase, kvstride, S, tid);
 
   const int rr = rw0 + l32;
   const int qp = rr / G;
@@ -301,72 +293,53 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(
   const int pw_lo = rw0 / G;
   const int pw_hi = wave_active ? min(S - 1, (min(rw0 + 32, R) - 1) / G) : -1;
 
-  const long kvstride = (long)Hkv * HD;
-  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
-  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
-
-  TileRegs kr, vr;
-  tile_load(kr, kbase, kvstride, S, tid);
-  tile_load(vr, vbase, kvstride, S, tid);
-  tile_store_rows(kr, smem, tid);
-  tile_store_tr(kr, smem + TILE_BYTES, tid);
-  tile_store_rows(vr, smem + 2 * TILE_BYTES, tid);
-  __syncthreads();
-
   f32x16 dqacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) dqacc[db] = zero16();
+  wait_dma();
+  __syncthreads();
 
   for (int kt = 0; kt < n_kt; ++kt) {
     const char* kl = smem + (kt & 1) * BUF;
-    const char* ktl = kl + TILE_BYTES;
-    const char* vl = kl + 2 * TILE_BYTES;
-    const bool has_next = kt + 1 < n_kt;
-    if (has_next) {
+    const char* vl = kl + TILE_BYTES;
+    if (kt + 1 < n_kt) {
+      char* nb = smem + ((kt + 1) & 1) * BUF;
       const int nk = (kt + 1) * BN;
-      tile_load(kr, kbase + (long)nk * kvstride, kvstride, S - nk, tid);
-      tile_load(vr, vbase + (long)nk * kvstride, kvstride, S - nk, tid);
+      tile_dma<4>(nb, kbase + (long)nk * kvstride, kvstride, S - nk, tid);
+      tile_dma<4>(nb + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, tid);
     }
     const int k0 = kt * BN;
     if (wave_active && (!CAUSAL || k0 <= pw_hi)) {
-      f32x16 s[2], dp[2];
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) { s[jb] = zero16(); dp[jb] = zero16(); }
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          s[jb] = mfma32(lds_a_rows(kl, jb, ks, lane), qreg[ks], s[jb]);
-          dp[jb] = mfma32(lds_a_rows(vl, jb, ks, lane), doreg[ks], dp[jb]);
-        }
-      }
       const bool need_mask = CAUSAL ? (k0 + BN - 1 > pw_lo) : (k0 + BN > S);
+      // one 32-key block at a time keeps S^T/dP^T at 32 registers
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          s = mfma32(lds_a_rows(kl, jb, ks, lane), qreg[ks], s);
+          dp = mfma32(lds_a_rows(vl, jb, ks, lane), doreg[ks], dp);
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float p = exp2_fast(fmaf(s[jb][r], scale2, -lse_i));
+          float p = exp2_fast(fmaf(s[r], scale2, -lse_i));
           if (need_mask) {
             const int key = k0 + 32 * jb + 8 * (r >> 2) + 4 * h + (r & 3);
             const bool masked = CAUSAL ? (key > qp) : (key >= S);
             if (masked) p = 0.f;
           }
-          s[jb][r] = p * (dp[jb][r] - dl_i);   // dS^T
+          s[r] = p * (dp[r] - dl_i);   // dS^T
+        }
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const bf16x8 sb = pack8(s, 8 * kh);
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+            dqacc[db] = mfma32(lds_a_tr(kl, db, 2 * jb + kh, lane), sb, dqacc[db]);
         }
       }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 sb = pack8(s[ks >> 1], 8 * (ks & 1));
-#pragma unroll
-        for (int db = 0; db < 4; ++db) dqacc[db] = mfma32(lds_a_tr(ktl, db, ks, lane), sb, dqacc[db]);
-      }
     }
-    if (has_next) {
-      char* nb = smem + ((kt + 1) & 1) * BUF;
-      tile_store_rows(kr, nb, tid);
-      tile_store_tr(kr, nb + TILE_BYTES, tid);
-      tile_store_rows(vr, nb + 2 * TILE_BYTES, tid);
-    }
+    wait_dma();
     __syncthreads();
   }
 

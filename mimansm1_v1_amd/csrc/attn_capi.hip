@@ -1,6 +1,7 @@
 // extern "C" entry points: argument checks, then the kernel launchers.
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "../../include/mm1_attn.h"
 #include "mm1_common.h"
@@ -38,6 +39,17 @@ int check_shape(int B, int S, int H, int Hkv, int D) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Forward tile variant: query rows per wave (64: one wave per SIMD; 32: two).
+// MM1_FWD_ROWS_PER_WAVE overrides the default for tile experiments.
+int fwd_rows_per_wave() {
+  static const int v = [] {
+    const char* e = getenv("MM1_FWD_ROWS_PER_WAVE");
+    const int x = e ? atoi(e) : 0;
+    return (x == 32 || x == 64) ? x : 32;
+  }();
+  return v;
+}
+
 int from_hip(hipError_t e) { return e == hipSuccess ? MM1_OK : static_cast<int>(e); }
 
 }  // namespace
@@ -54,7 +66,7 @@ int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
   if (rc) return rc;
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MM1_E_ALIGN;
-  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale, 64,
+  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale, fwd_rows_per_wave(),
                                   static_cast<hipStream_t>(stream)));
 }
 

@@ -13,15 +13,22 @@
 //     queries on N), so every lane owns one query column: the row max needs a
 //     single cross-half exchange and P^T feeds the next product as a B operand
 //     straight from the accumulator registers (pi order, see mm1_common.h).
-//   * O^T = V^T P^T keeps the same one-query-per-lane layout for the rescale.
-//   * K tiles are stored row-major (XOR swizzled), V tiles transposed, in a
-//     two-stage LDS ring with one barrier per key tile.
+//   * O^T = V^T P^T keeps the same one-query-per-lane layout for the rescale;
+//     V^T is read transposed from the row-major V tile.
+//   * K and V tiles arrive by LDS DMA into a two-stage ring, one barrier per
+//     key tile; no staging registers.
+//   * The running max is only moved (and O, l rescaled) when a row's max
+//     grows by more than 2^8 (log2 units); otherwise P = exp2(s - m_old) <= 256
+//     stays exact in fp32 and bf16, and the final normalisation uses the same
+//     frame, so the result is unchanged.
 #include "mm1_common.h"
 
 namespace mm1 {
 
+constexpr float kRescaleThreshold = 8.0f;   // log2 units
+
 template <int QW, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(
+__global__ __launch_bounds__(256, (QW == 32 ? 2 : 1)) void attn_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     __bf16* __restrict__ o, float* __restrict__ lse2,
     int B, int S, int H, int Hkv, int G, float scale2, int n_tiles) {
@@ -29,7 +36,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
   constexpr int BM = 4 * QW;      // packed rows per workgroup
   constexpr int BN = TILE_ROWS;   // keys per iteration
   constexpr int BUF = 2 * TILE_BYTES;
-  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
+  __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
   const int nbg = B * Hkv;
@@ -41,6 +48,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
   const int r0 = tile * BM;
   const int rw0 = r0 + w * QW;
   const bool wave_active = rw0 < R;
+
+  const long kvstride = (long)Hkv * HD;
+  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
+  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
+  tile_dma<4>(smem, kbase, kvstride, S, tid);
+  tile_dma<4>(smem + TILE_BYTES, vbase, kvstride, S, tid);
 
   // Query operands (B of S^T = K Q^T), loaded once.
   bf16x8 qreg[NQB][8];
@@ -69,17 +82,6 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
   const int pw_lo = rw0 / G;
   const int pw_hi = wave_active ? min(S - 1, (min(rw0 + QW, R) - 1) / G) : -1;
 
-  const long kvstride = (long)Hkv * HD;
-  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
-  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
-
-  TileRegs kr, vr;
-  tile_load(kr, kbase, kvstride, S, tid);
-  tile_load(vr, vbase, kvstride, S, tid);
-  tile_store_rows(kr, smem, tid);
-  tile_store_tr(vr, smem + TILE_BYTES, tid);
-  __syncthreads();
-
   f32x16 oacc[4][NQB];
   float m_run[NQB], l_run[NQB];
 #pragma unroll
@@ -89,15 +91,17 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
 #pragma unroll
     for (int db = 0; db < 4; ++db) oacc[db][qb] = zero16();
   }
+  wait_dma();
+  __syncthreads();
 
   for (int kt = 0; kt < n_kt; ++kt) {
     const char* kl = smem + (kt & 1) * BUF;
     const char* vl = kl + TILE_BYTES;
-    const bool has_next = kt + 1 < n_kt;
-    if (has_next) {
+    if (kt + 1 < n_kt) {
+      char* nb = smem + ((kt + 1) & 1) * BUF;
       const int nk = (kt + 1) * BN;
-      tile_load(kr, kbase + (long)nk * kvstride, kvstride, S - nk, tid);
-      tile_load(vr, vbase + (long)nk * kvstride, kvstride, S - nk, tid);
+      tile_dma<4>(nb, kbase + (long)nk * kvstride, kvstride, S - nk, tid);
+      tile_dma<4>(nb + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, tid);
     }
     const int k0 = kt * BN;
     if (wave_active && (!CAUSAL || k0 <= pw_hi)) {
@@ -131,6 +135,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
           }
         }
       }
+      // Row max of this tile; move the running max only when it grows by
+      // more than the threshold (any lane of the wave -> whole wave rescales).
+      float mnew[NQB];
+      bool grow = false;
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
         float mx = -INFINITY;
@@ -140,10 +148,24 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[jb][qb][r]);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run[qb], mx);
-        const bool none = (m_new == -INFINITY);
-        const float alpha = none ? 1.f : exp2_fast((m_run[qb] - m_new) * scale2);
-        const float ms = none ? 0.f : m_new * scale2;
+        mnew[qb] = fmaxf(m_run[qb], mx);
+        grow |= !((mnew[qb] - m_run[qb]) * scale2 <= kRescaleThreshold);
+      }
+      if (__any(grow)) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+          const float m_new = mnew[qb];
+          const bool none = (m_new == -INFINITY);
+          const float alpha = none ? 1.f : exp2_fast((m_run[qb] - m_new) * scale2);
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < 4; ++db) oacc[db][qb] *= alpha;
+          m_run[qb] = m_new;
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        const float ms = (m_run[qb] == -INFINITY) ? 0.f : m_run[qb] * scale2;
         float sum = 0.f;
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
@@ -154,10 +176,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
             sum += p;
           }
         }
-        l_run[qb] = l_run[qb] * alpha + sum;
-        m_run[qb] = m_new;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) oacc[db][qb] *= alpha;
+        l_run[qb] += sum;
       }
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -172,11 +191,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
         }
       }
     }
-    if (has_next) {
-      char* nb = smem + ((kt + 1) & 1) * BUF;
-      tile_store_rows(kr, nb, tid);
-      tile_store_tr(vr, nb + TILE_BYTES, tid);
-    }
+    wait_dma();
     __syncthreads();
   }
 

@@ -14,7 +14,19 @@
 //   C/D (32 x 32 fp32, 16 regs): lane l holds column (l & 31); register r
 //   holds row 8*(r/4) + 4*(l/32) + (r%4).
 // A D tile read as a B operand of the next product therefore pairs slot t of
-// k-step s with row 16*s + 8*(t/4) + 4*(l/32) + (t%4): the "pi" order below.
+// k-step s with row 16*s + 8*(t/4) + 4*(l/32) + (t%4): the "pi" order.  A
+// operands that meet such a B operand are read in the same pi order.
+//
+// LDS tiles are 64 rows x 128 bf16 (256 B per row, 16 KiB), row-major, with
+// the sixteen 16-byte chunks of row r permuted by chunk ^ swz(r).  They are
+// filled straight from global memory by the LDS DMA path
+// (global_load_lds_dwordx4: lane L of a wave lands at base + 16*L), and read
+// either row-wise (ds_read_b128: a row of 8 k values per lane) or transposed
+// (two ds_read_b64_tr_b16: a column of 8 rows per lane).  swz() is chosen so
+// that both read patterns touch each bank once per 16-lane phase:
+//   * row reads: 16 consecutive rows at one logical chunk -> 16 chunks;
+//   * transposed reads: 4 consecutive rows (aligned to 4) x 4 consecutive
+//     8-byte columns -> 16 different chunk slots.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -25,8 +37,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define MM1_LDS __attribute__((address_space(3)))
+#define MM1_GLOBAL __attribute__((address_space(1)))
 
 constexpr int HD = 128;            // head_dim supported by the kernels
 constexpr int TILE_ROWS = 64;      // rows in one LDS tile
@@ -45,8 +58,8 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-// Eight consecutive accumulator registers (base, base+1, ..., base+7) as a
-// bf16 MFMA operand (round to nearest even).
+// Eight consecutive accumulator registers (base .. base+7) as a bf16 MFMA
+// operand (round to nearest even).
 __device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
   bf16x8 r;
 #pragma unroll
@@ -54,81 +67,69 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
   return r;
 }
 
-// ---------------------------------------------------------------------------
-// LDS tile layouts (byte offsets inside one 16 KiB tile).
-//
-// Row tile: [64 rows][128 cols] bf16, 256 B per row; 16-byte chunk c of row
-// r lives at chunk c ^ (r & 15) so that 16 consecutive rows read at one
-// logical chunk hit 16 different bank groups.
+// Wait until this wave's outstanding global->LDS copies have landed.
+__device__ __forceinline__ void wait_dma() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
+
+// Byte offset of logical 16-byte chunk `chunk` (0..15) of `row`.
 __device__ __forceinline__ int row_off(int row, int chunk) {
-  return row * 256 + ((chunk ^ (row & 15)) << 4);
+  return row * 256 + ((chunk ^ swz(row)) << 4);
 }
 
-// Transposed tile: [128 cols][64 rows] bf16, 128 B per column, rows inside
-// each 16-block stored in pi order (bits 2 and 3 of the row swapped) so that
-// one 16-byte read returns the eight rows a lane needs for one k-step.
-// Chunks are XOR-swizzled by a function of the column that keeps both the
-// 32-lane column reads and the tile writes spread over the banks.
-__device__ __forceinline__ int pi_pos(int j) {
-  return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
-}
-__device__ __forceinline__ int tr_off(int col, int jp) {
-  const int swz = ((col >> 1) ^ (col >> 3)) & 7;
-  return col * 128 + ((((jp >> 3) ^ swz)) << 4) + ((jp & 7) << 1);
-}
-
-// 256 threads stage a 64 x 128 bf16 tile through registers: thread t owns
-// rows 4*(t>>4) .. +3 and columns 8*(t&15) .. +7.  Rows at or beyond
-// `nvalid` read as zero.
-struct TileRegs {
-  u32x4 r[4];
-};
-
-__device__ __forceinline__ void tile_load(TileRegs& t, const __bf16* __restrict__ base,
-                                          long stride, int nvalid, int tid) {
-  const int rg = tid >> 4, c = tid & 15;
+// Copy a 64 x 128 bf16 tile into LDS with the DMA path.  Row r of the tile is
+// at base + r*stride elements; rows at or beyond nvalid re-read row nvalid-1
+// (finite data the kernels mask out).  NW waves share the 16 row quads.
+template <int NW>
+__device__ __forceinline__ void tile_dma(char* lds, const __bf16* base, long stride, int nvalid,
+                                         int tid) {
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int L = tid & 63;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * rg + i;
-    if (row < nvalid) {
-      t.r[i] = *reinterpret_cast<const u32x4*>(base + (long)row * stride + 8 * c);
-    } else {
-      t.r[i] = u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int i = 0; i < 16 / NW; ++i) {
+    const int rq = i * NW + w;                 // row quad: rows 4rq .. 4rq+3
+    const int row = 4 * rq + (L >> 4);
+    const int chunk = (L & 15) ^ swz(row);     // logical chunk this lane's slot holds
+    const int grow = min(row, nvalid - 1);
+    const __bf16* src = base + (long)grow * stride + 8 * chunk;
+    __builtin_amdgcn_global_load_lds((const MM1_GLOBAL void*)src, (MM1_LDS void*)(lds + rq * 1024),
+                                     16, 0, 0);
   }
 }
 
-__device__ __forceinline__ void tile_store_rows(const TileRegs& t, char* lds, int tid) {
-  const int rg = tid >> 4, c = tid & 15;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<u32x4*>(lds + row_off(4 * rg + i, c)) = t.r[i];
-  }
+// Copy 64 consecutive floats (elements >= nvalid re-read element nvalid-1)
+// into LDS; issued by one whole wave.
+__device__ __forceinline__ void vec64_dma(char* lds, const float* base, int nvalid, int lane) {
+  const float* src = base + min(lane, nvalid - 1);
+  __builtin_amdgcn_global_load_lds((const MM1_GLOBAL void*)src, (MM1_LDS void*)lds, 4, 0, 0);
 }
 
-__device__ __forceinline__ void tile_store_tr(const TileRegs& t, char* lds, int tid) {
-  const int rg = tid >> 4, c = tid & 15;
-  const int jp0 = pi_pos(4 * rg);
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const uint32_t w0 = t.r[0][m], w1 = t.r[1][m], w2 = t.r[2][m], w3 = t.r[3][m];
-    const u32x2 lo = {(w0 & 0xffffu) | (w1 << 16), (w2 & 0xffffu) | (w3 << 16)};
-    const u32x2 hi = {(w0 >> 16) | (w1 & 0xffff0000u), (w2 >> 16) | (w3 & 0xffff0000u)};
-    const int col = 8 * c + 2 * m;
-    *reinterpret_cast<u32x2*>(lds + tr_off(col, jp0)) = lo;
-    *reinterpret_cast<u32x2*>(lds + tr_off(col + 1, jp0)) = hi;
-  }
-}
-
-// A operand from a row tile: rows 32*blk + (lane&31), k-step ks (16 columns).
+// A operand from a tile whose rows are the MFMA M axis: rows 32*blk + (lane&31),
+// k-step ks = columns 16*ks .. +15 (natural order).
 __device__ __forceinline__ bf16x8 lds_a_rows(const char* lds, int blk, int ks, int lane) {
   return *reinterpret_cast<const bf16x8*>(lds + row_off(32 * blk + (lane & 31), 2 * ks + (lane >> 5)));
 }
 
-// A operand from a transposed tile: columns 32*blk + (lane&31), rows of k-step
-// ks (16 rows) in pi order.
+// A operand from a tile whose rows are the k axis (read transposed): M index
+// (column of the tile) 32*blk + (lane&31), k-step ks = tile rows 16*ks .. +15
+// in pi order.  Within each 16-lane group, ds_read_b64_tr_b16 gives lane i
+// element (i & 3) of the 8-byte chunks addressed by lanes 4t + (i >> 2),
+// t = 0..3; lane j of the group therefore addresses row
+// 16ks + 8r + 4h + (j >> 2), columns 4(j & 3) .. +3 of its 16-column strip.
 __device__ __forceinline__ bf16x8 lds_a_tr(const char* lds, int blk, int ks, int lane) {
-  return *reinterpret_cast<const bf16x8*>(lds + tr_off(32 * blk + (lane & 31), 16 * ks + 8 * (lane >> 5)));
+  const int h = lane >> 5, g = (lane >> 4) & 1, j = lane & 15;
+  const int col = 32 * blk + 16 * g + 4 * (j & 3);
+  const int chunk = col >> 3, half = (col >> 2) & 1;
+  bf16x8 out;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int row = 16 * ks + 8 * r + 4 * h + (j >> 2);
+    const char* p = lds + row * 256 + ((chunk ^ swz(row)) << 4) + 8 * half;
+    const bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MM1_LDS bf16x4*)p);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) out[4 * r + t] = v[t];
+  }
+  return out;
 }
 
 }  // namespace mm1

@@ -7,10 +7,13 @@ same bf16 inputs:
     that rounding the exact answer to bf16 already costs (dK/dV sum over up to
     G*S query rows, so at large magnitude one bf16 half-ulp exceeds 2e-2);
   * fp32 lse2: max-abs <= 1e-3;
-    plus, where given, alg_floor = max|emulated reference-kernel arithmetic -
-    ref|: the backward rounds P and dS to bf16 before its products exactly as
-    the reference's TileLang kernel does (AT:306, :310-314), which with peaky
-    softmax (config 4, logits std up to ~9) alone exceeds 2e-2 on dQ/dK;
+    plus, where given, the error of the reference kernel's own arithmetic:
+    alg = max|emulated - ref| (and alg_rel = relative L2 of emulated - ref) for
+    the backward, whose P and dS are rounded to bf16 before their products
+    exactly as the reference's TileLang kernel does (AT:306, :310-314).  With
+    peaky softmax (config 4, logits std up to ~9) that rounding alone exceeds
+    2e-2 max-abs on dQ/dK, and on tiny peaky cases 5e-3 relative L2; the gates
+    then read max_abs <= 2e-2 + floor + alg and rel_l2 <= 5e-3 + alg_rel;
   * the reference harness's own metric max|d| / max|ref| < 2e-2 (AT:664-669),
     applied where max|ref| >= 1e-3 (it is undefined for an exactly-zero
     reference such as dQ at S = 1, where the max-abs gate still holds).
@@ -42,14 +45,16 @@ def metrics(got: torch.Tensor, want: torch.Tensor) -> dict:
 
 def assert_bf16_close(name: str, got, want, log=print, emulated=None):
     m = metrics(got, want)
-    alg = 0.0
+    alg = alg_rel = 0.0
     if emulated is not None:
-        alg = (emulated.detach().float().cpu() - want.detach().float().cpu()).abs().max().item()
-    m["alg_floor"] = alg
+        e = metrics(emulated, want)
+        alg, alg_rel = e["max_abs"], e["rel_l2"]
+    m["alg_floor"], m["alg_rel"] = alg, alg_rel
     log(f"    {name:4s} max_abs {m['max_abs']:.3e} (floor {m['floor']:.3e}, alg {alg:.3e})  "
-        f"rel_l2 {m['rel_l2']:.3e}  ref_rel {m['ref_rel']:.3e}")
+        f"rel_l2 {m['rel_l2']:.3e} (alg {alg_rel:.3e})  ref_rel {m['ref_rel']:.3e}")
     assert m["finite"], f"{name}: non-finite values"
-    assert m["rel_l2"] <= REL_L2, f"{name}: rel L2 {m['rel_l2']:.3e} > {REL_L2}"
+    assert m["rel_l2"] <= REL_L2 + alg_rel, (
+        f"{name}: rel L2 {m['rel_l2']:.3e} > {REL_L2} + alg {alg_rel:.3e}")
     assert m["max_abs"] <= MAX_ABS + m["floor"] + alg, (
         f"{name}: max abs {m['max_abs']:.3e} > {MAX_ABS} + floor {m['floor']:.3e} + alg {alg:.3e}")
     if m["ref_max"] >= 1e-3:
