@@ -7,6 +7,7 @@ raises -- there is no fallback implementation.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
@@ -40,7 +41,9 @@ class LibraryMissing(RuntimeError):
 
 
 def library_path() -> Path:
-    return _build.library_path()
+    """The in-tree build, or the file MM1_ATTN_LIB names (to compare builds)."""
+    override = os.environ.get("MM1_ATTN_LIB")
+    return Path(override).resolve() if override else _build.library_path()
 
 
 def load() -> ctypes.CDLL:

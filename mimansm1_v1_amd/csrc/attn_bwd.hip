@@ -25,6 +25,8 @@
 //   * attn_dq_kernel      : query-stationary over the packed GQA row space
 //     (as in the forward): K/V tiles in LDS serve all G heads of a group and
 //     dQ is written once in bf16 -- no fp32 scratch and no un-swizzle pass.
+#include <type_traits>
+
 #include "mm1_common.h"
 
 namespace mm1 {
@@ -57,28 +59,47 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV: one workgroup per (128-key tile, query head); 4 waves x 32 keys.
+// dK, dV: one workgroup per (128-key tile, query head), 8 waves in 4 pairs.
+// Pair i owns keys kt*128 + 32i .. +31 and splits the work by role:
+//   P wave  (wave i):     S = Q K^T, P = exp2(S*scale2 - lse2), dV^T += dO^T P;
+//                         keeps K (B operand) and the dV^T accumulators;
+//   dS wave (wave i + 4): dP = dO V^T, dS = P (dP - Delta), dK^T += Q^T dS;
+//                         keeps V and the dK^T accumulators.
+// P goes from the P wave to the dS wave through a two-slot fp32 LDS mailbox,
+// one barrier per 32-query block.  Both waves of a pair sit on one SIMD, so
+// one wave's softmax VALU work overlaps the other's MFMAs, and each needs
+// about half the registers of a wave doing both (two waves per SIMD fit).
 // Query tiles (Q, dO row-major; lse2, Delta) arrive by LDS DMA in a two-stage
-// ring; the transposed operands of dV^T = dO^T P and dK^T = Q^T dS are read
-// from the same row-major tiles with the LDS transpose read.
+// ring; the transposed operands of dV^T and dK^T are read with the LDS
+// transpose read.
 template <bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
+__global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     float* __restrict__ ws_dk, float* __restrict__ ws_dv,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale) {
-  constexpr int BQ = TILE_ROWS;                      // query positions per iteration
+  constexpr int BQ = TILE_ROWS;                      // query positions per tile
   constexpr int BUF = 2 * TILE_BYTES + 2 * BQ * 4;   // Q, dO, lse2, delta
-  __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
+  constexpr int MBOX = 32 * 32 * 4;                  // one 32 x 32 fp32 P block
+  constexpr int NSTAGE = 3;
+  // LDS DMA instructions one wave issues per query tile: two row quads of Q
+  // and two of dO (waves 0 and 1 add one vector copy each and so wait for
+  // one copy more than needed, which is safe).
+  constexpr int kDmaPerTile = 2 * (16 / 8);
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + 4 * 2 * MBOX];
+  char* mbox_base = smem + NSTAGE * BUF;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
+  const int pair = w & 3;
+  const bool pwave = w < 4;
   const int nbh = B * H;
   const int kt = blockIdx.x / nbh;        // heaviest key tiles first
   const int bh = blockIdx.x % nbh;
   const int b = bh / H, hq = bh % H;
   const int g = hq / G, hh = hq % G;
-  const int kw0 = kt * 128 + 32 * w;      // this wave's first key
+  const int kw0 = kt * 128 + 32 * pair;   // this pair's first key
   const int key = kw0 + l32;
 
   const int q_begin = CAUSAL ? kt * 128 : 0;
@@ -89,125 +110,158 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_kernel(
   const float* lse_row = lse2 + ((long)b * H + hq) * S;
   const float* dl_row = delta + ((long)b * H + hq) * S;
 
+  // Query tiles are walked from the sequence end down to q_begin, so the
+  // workgroups of one head that start together read the same tiles together.
+  auto tile_p0 = [&](int it) { return q_begin + (n_qt - 1 - it) * BQ; };
+  const uint32_t dma_off = tile_lane_off(qstride, tid);
   auto issue_tile = [&](char* buf, int p0) {
-    tile_dma<4>(buf, qbase + (long)p0 * qstride, qstride, S - p0, tid);
-    tile_dma<4>(buf + TILE_BYTES, dobase + (long)p0 * qstride, qstride, S - p0, tid);
+    tile_dma<8>(buf, qbase + (long)p0 * qstride, qstride, S - p0, dma_off, tid);
+    tile_dma<8>(buf + TILE_BYTES, dobase + (long)p0 * qstride, qstride, S - p0, dma_off, tid);
     if (w == 0) vec64_dma(buf + 2 * TILE_BYTES, lse_row + p0, S - p0, lane);
     if (w == 1) vec64_dma(buf + 2 * TILE_BYTES + BQ * 4, dl_row + p0, S - p0, lane);
   };
-  issue_tile(smem, q_begin);
+  issue_tile(smem, tile_p0(0));
+  if (n_qt > 1) issue_tile(smem + BUF, tile_p0(1));
 
-  // K and V rows of this lane's key as B operands (B[k=d][n=key]).
-  bf16x8 kreg[8], vreg[8];
+  // This lane's key row of K (P wave) or V (dS wave) as the B operand.
+  bf16x8 breg[8];
   {
     const int kk = min(key, S - 1);
-    const long off = ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
+    const __bf16* src = (pwave ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      kreg[ks] = *reinterpret_cast<const bf16x8*>(k + off + 16 * ks);
-      vreg[ks] = *reinterpret_cast<const bf16x8*>(v + off + 16 * ks);
-    }
+    for (int ks = 0; ks < 8; ++ks) breg[ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) pin(breg[ks]);
   }
 
-  f32x16 dkacc[4], dvacc[4];
+  f32x16 acc[4];   // dV^T (P wave) or dK^T (dS wave)
 #pragma unroll
-  for (int db = 0; db < 4; ++db) { dkacc[db] = zero16(); dvacc[db] = zero16(); }
+  for (int db = 0; db < 4; ++db) acc[db] = zero16();
+  const LdsBases lb = make_lds_bases(lane);
   wait_dma();
   __syncthreads();
 
-  for (int it = 0; it < n_qt; ++it) {
-    const char* buf = smem + (it & 1) * BUF;
-    const char* ql = buf;
-    const char* dol = buf + TILE_BYTES;
-    const float* lsel = reinterpret_cast<const float*>(buf + 2 * TILE_BYTES);
+  // One query tile; the loop below runs it NSTAGE times per trip so the ring
+  // slot (and every LDS offset) is a compile-time constant.
+  auto step = [&](auto slot, int it) {
+    constexpr int P = decltype(slot)::value;
+    const char* ql = smem + P * BUF;
+    const char* dol = ql + TILE_BYTES;
+    const float* lsel = reinterpret_cast<const float*>(ql + 2 * TILE_BYTES);
     const float* dll = lsel + BQ;
-    const int p0 = q_begin + it * BQ;
-    if (it + 1 < n_qt) issue_tile(smem + ((it + 1) & 1) * BUF, p0 + BQ);
+    const int p0 = tile_p0(it);
+    if (it + 2 < n_qt) issue_tile(smem + ((P + 2) % NSTAGE) * BUF, tile_p0(it + 2));
+    // pairs whose keys all lie after this tile skip it (causal); the
+    // barriers are still taken by every wave
+    const bool active = !CAUSAL || p0 + BQ - 1 >= kw0;
+    const bool need_mask = (CAUSAL && p0 < kw0 + 31) || (p0 + BQ > S);
 
-    if (!CAUSAL || p0 + BQ - 1 >= kw0) {
-      // causal diagonal, or a last tile with rows past the sequence end
-      const bool need_mask = (CAUSAL && p0 < kw0 + 31) || (p0 + BQ > S);
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        f32x16 s = zero16(), dp = zero16();
+    for (int qb = 0; qb < 2; ++qb) {
+      // D layout: register r holds query 32*qb + 8*(r/4) + 4*h + (r%4) of the tile.
+      // mailbox layout [register group a4][lane] x 4 floats: each 16-byte access
+      // of a wave is one contiguous 1 KiB row (no bank conflicts)
+      float* mbox = reinterpret_cast<float*>(mbox_base + (pair * 2 + qb) * MBOX) + lane * 4;
+      f32x16 sv;
+      if (active) {
+        const char* arows = pwave ? ql : dol;
+        sv = zero16();
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-          s = mfma32(lds_a_rows(ql, qb, ks, lane), kreg[ks], s);
-          dp = mfma32(lds_a_rows(dol, qb, ks, lane), vreg[ks], dp);
-        }
-        // D layout: register r holds query 32*qb + 8*(r/4) + 4*h + (r%4) of this tile.
-        f32x16 pv, dsv;
+        for (int ks = 0; ks < 8; ++ks) sv = mfma32(rows_a(arows, lb, qb, ks), breg[ks], sv);
+        if (pwave) {
 #pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-          const int i0 = 32 * qb + 8 * a4 + 4 * h;
-          const f32x4 lse4 = *reinterpret_cast<const f32x4*>(lsel + i0);
-          const f32x4 dl4 = *reinterpret_cast<const f32x4*>(dll + i0);
+          for (int a4 = 0; a4 < 4; ++a4) {
+            const int i0 = 32 * qb + 8 * a4 + 4 * h;
+            const f32x4 lse4 = *reinterpret_cast<const f32x4*>(lsel + i0);
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const int r = 4 * a4 + c;
-            float p = exp2_fast(fmaf(s[r], scale2, -lse4[c]));
-            if (need_mask) {
-              const int qp = p0 + i0 + c;
-              if ((CAUSAL && key > qp) || qp >= S) p = 0.f;
+            for (int c = 0; c < 4; ++c) {
+              const int r = 4 * a4 + c;
+              float pr = exp2_fast(fmaf(sv[r], scale2, -lse4[c]));
+              if (need_mask) {
+                const int qpos = p0 + i0 + c;
+                if ((CAUSAL && key > qpos) || qpos >= S) pr = 0.f;
+              }
+              sv[r] = pr;
             }
-            pv[r] = p;
-            dsv[r] = p * (dp[r] - dl4[c]);
+          }
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4) {
+            f32x4 v4;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v4[c] = sv[4 * a4 + c];
+            *reinterpret_cast<f32x4*>(mbox + 256 * a4) = v4;
           }
         }
+      }
+      lds_barrier();   // P of this block is in the mailbox
+      if (active) {
+        if (pwave) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const bf16x8 pb = pack8(pv, 8 * ks);
-          const bf16x8 sb = pack8(dsv, 8 * ks);
+          for (int kh = 0; kh < 2; ++kh) {
+            const bf16x8 pb = pack8(sv, 8 * kh);
 #pragma unroll
-          for (int db = 0; db < 4; ++db) {
-            dvacc[db] = mfma32(lds_a_tr(dol, db, 2 * qb + ks, lane), pb, dvacc[db]);
-            dkacc[db] = mfma32(lds_a_tr(ql, db, 2 * qb + ks, lane), sb, dkacc[db]);
+            for (int db = 0; db < 4; ++db) acc[db] = mfma32(tr_a(dol, lb, db, 2 * qb + kh), pb, acc[db]);
+          }
+        } else {
+          f32x16 dsv;
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4) {
+            const int i0 = 32 * qb + 8 * a4 + 4 * h;
+            const f32x4 dl4 = *reinterpret_cast<const f32x4*>(dll + i0);
+            const f32x4 p4 = *reinterpret_cast<const f32x4*>(mbox + 256 * a4);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) dsv[4 * a4 + c] = p4[c] * (sv[4 * a4 + c] - dl4[c]);
+          }
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh) {
+            const bf16x8 sb = pack8(dsv, 8 * kh);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] = mfma32(tr_a(ql, lb, db, 2 * qb + kh), sb, acc[db]);
           }
         }
       }
     }
-    wait_dma();
-    __syncthreads();
+    // the next tile must have landed; the one after it stays in flight
+    if (it + 2 < n_qt) {
+      __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");
+    } else {
+      wait_dma();
+    }
+    lds_barrier();
+  };
+  for (int it = 0; it < n_qt; it += NSTAGE) {
+    step(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < n_qt) step(std::integral_constant<int, 1>{}, it + 1);
+    if (it + 2 < n_qt) step(std::integral_constant<int, 2>{}, it + 2);
   }
 
   if (key >= S) return;
   // D layout of dK^T / dV^T: register r of block db holds column
   // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
+  const float scale_out = pwave ? 1.f : sm_scale;
   if (G == 1) {
-    __bf16* dkrow = dk + ((long)(b * S + key) * Hkv + g) * HD;
-    __bf16* dvrow = dv + ((long)(b * S + key) * Hkv + g) * HD;
+    __bf16* row = (pwave ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int a4 = 0; a4 < 4; ++a4) {
-        bf16x4 kv4, vv4;
+        bf16x4 o4;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          kv4[c] = (__bf16)(dkacc[db][4 * a4 + c] * sm_scale);
-          vv4[c] = (__bf16)(dvacc[db][4 * a4 + c]);
-        }
-        const int d = 32 * db + 8 * a4 + 4 * h;
-        *reinterpret_cast<bf16x4*>(dkrow + d) = kv4;
-        *reinterpret_cast<bf16x4*>(dvrow + d) = vv4;
+        for (int c = 0; c < 4; ++c) o4[c] = (__bf16)(acc[db][4 * a4 + c] * scale_out);
+        *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
       }
     }
   } else {
     const long slot = (long)hh * B * S * Hkv * HD;
-    float* dkrow = ws_dk + slot + ((long)(b * S + key) * Hkv + g) * HD;
-    float* dvrow = ws_dv + slot + ((long)(b * S + key) * Hkv + g) * HD;
+    float* row = (pwave ? ws_dv : ws_dk) + slot + ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int a4 = 0; a4 < 4; ++a4) {
-        f32x4 kv4, vv4;
+        f32x4 o4;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          kv4[c] = dkacc[db][4 * a4 + c] * sm_scale;
-          vv4[c] = dvacc[db][4 * a4 + c];
-        }
-        const int d = 32 * db + 8 * a4 + 4 * h;
-        *reinterpret_cast<f32x4*>(dkrow + d) = kv4;
-        *reinterpret_cast<f32x4*>(dvrow + d) = vv4;
+        for (int c = 0; c < 4; ++c) o4[c] = acc[db][4 * a4 + c] * scale_out;
+        *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
       }
     }
   }
@@ -247,7 +301,8 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(
   constexpr int BUF = 2 * TILE_BYTES;   // K, V
   __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int nbg = B * Hkv;
   int tile = blockIdx.x / nbg;
   if (CAUSAL) tile = n_tiles - 1 - tile;
@@ -261,8 +316,9 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(
   const long kvstride = (long)Hkv * HD;
   const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
   const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
-  tile_dma<4>(smem, kbase, kvstride, S, tid);
-  tile_dma<4>(smem + TILE_BYTES, vbase, kvstride, S, tid);
+  const uint32_t dma_off = tile_lane_off(kvstride, tid);
+  tile_dma<4>(smem, kbase, kvstride, S, dma_off, tid);
+  tile_dma<4>(smem + TILE_BYTES, vbase, kvstride, S, dma_off, tid);
 
   const int rr = rw0 + l32;
   const int qp = rr / G;
@@ -280,6 +336,9 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(
     const long li = ((long)b * H + g * G + hh) * S + qp;
     lse_i = lse2[li];
     dl_i = delta[li];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) { pin(qreg[ks]); pin(doreg[ks]); }
+    __asm__ volatile("" : "+v"(lse_i), "+v"(dl_i));
   } else {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -305,8 +364,8 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(
     if (kt + 1 < n_kt) {
       char* nb = smem + ((kt + 1) & 1) * BUF;
       const int nk = (kt + 1) * BN;
-      tile_dma<4>(nb, kbase + (long)nk * kvstride, kvstride, S - nk, tid);
-      tile_dma<4>(nb + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, tid);
+      tile_dma<4>(nb, kbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
+      tile_dma<4>(nb + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
     }
     const int k0 = kt * BN;
     if (wave_active && (!CAUSAL || k0 <= pw_hi)) {
@@ -391,10 +450,10 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
   const int n_ktiles = (S + 127) / 128;
   dim3 grid(n_ktiles * B * H);
   if (causal)
-    hipLaunchKernelGGL(attn_dkdv_kernel<true>, grid, dim3(256), 0, stream, qp, kp, vp, dop, lse2, delta,
+    hipLaunchKernelGGL(attn_dkdv_kernel<true>, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta,
                        ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale);
   else
-    hipLaunchKernelGGL(attn_dkdv_kernel<false>, grid, dim3(256), 0, stream, qp, kp, vp, dop, lse2, delta,
+    hipLaunchKernelGGL(attn_dkdv_kernel<false>, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta,
                        ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale);
   return hipGetLastError();
 }

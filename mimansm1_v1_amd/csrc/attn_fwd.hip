@@ -38,7 +38,8 @@ __global__ __launch_bounds__(256, (QW == 32 ? 2 : 1)) void attn_fwd_kernel(
   constexpr int BUF = 2 * TILE_BYTES;
   __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int nbg = B * Hkv;
   int tile = blockIdx.x / nbg;
   if (CAUSAL) tile = n_tiles - 1 - tile;   // longest rows first
@@ -52,8 +53,9 @@ __global__ __launch_bounds__(256, (QW == 32 ? 2 : 1)) void attn_fwd_kernel(
   const long kvstride = (long)Hkv * HD;
   const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
   const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
-  tile_dma<4>(smem, kbase, kvstride, S, tid);
-  tile_dma<4>(smem + TILE_BYTES, vbase, kvstride, S, tid);
+  const uint32_t dma_off = tile_lane_off(kvstride, tid);
+  tile_dma<4>(smem, kbase, kvstride, S, dma_off, tid);
+  tile_dma<4>(smem + TILE_BYTES, vbase, kvstride, S, dma_off, tid);
 
   // Query operands (B of S^T = K Q^T), loaded once.
   bf16x8 qreg[NQB][8];
@@ -68,6 +70,8 @@ __global__ __launch_bounds__(256, (QW == 32 ? 2 : 1)) void attn_fwd_kernel(
       const __bf16* src = q + ((long)(b * S + p) * H + g * G + hh) * HD + 8 * h;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) qreg[qb][ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) pin(qreg[qb][ks]);
     } else {
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
@@ -100,8 +104,8 @@ __global__ __launch_bounds__(256, (QW == 32 ? 2 : 1)) void attn_fwd_kernel(
     if (kt + 1 < n_kt) {
       char* nb = smem + ((kt + 1) & 1) * BUF;
       const int nk = (kt + 1) * BN;
-      tile_dma<4>(nb, kbase + (long)nk * kvstride, kvstride, S - nk, tid);
-      tile_dma<4>(nb + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, tid);
+      tile_dma<4>(nb, kbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
+      tile_dma<4>(nb + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
     }
     const int k0 = kt * BN;
     if (wave_active && (!CAUSAL || k0 <= pw_hi)) {

@@ -67,8 +67,22 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
   return r;
 }
 
-// Wait until this wave's outstanding global->LDS copies have landed.
+// Wait until all of this wave's outstanding global loads, LDS DMA copies
+// included, have landed.  Inline assembly on purpose: the compiler does not
+// see the DMA copies, so it would treat a builtin s_waitcnt as redundant and
+// drop it.
 __device__ __forceinline__ void wait_dma() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Workgroup barrier that orders LDS traffic only: unlike __syncthreads() it
+// does not wait for outstanding global loads (LDS DMA prefetches keep
+// flying).  Copies a wave needs before the barrier are waited for explicitly.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Materialise a loaded operand here: the compiler may not sink the load into
+// a loop, where its wait would also drain the LDS DMA copies in flight.
+__device__ __forceinline__ void pin(bf16x8& x) { __asm__ volatile("" : "+v"(x)); }
 
 __device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 
@@ -77,31 +91,78 @@ __device__ __forceinline__ int row_off(int row, int chunk) {
   return row * 256 + ((chunk ^ swz(row)) << 4);
 }
 
+// LDS DMA: every lane of the wave copies `bytes` (16 or 4) from its global
+// address to lds_base + bytes * lane.  Issued as inline assembly so that the
+// compiler does not track the copy: it would otherwise wait for all
+// outstanding copies (vmcnt(0)) before any LDS read it cannot prove disjoint
+// from the copy target, which serialises the prefetch ring.  The kernels wait
+// for the copies themselves (wait_dma / explicit vmcnt) before the barrier
+// that publishes a tile; compiler-generated vmcnt waits for other loads can
+// only over-wait because of the extra copies in flight.  lds_base must be
+// wave-uniform.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const MM1_LDS void*)p;
+}
+
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+  __asm__ volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                   :: "v"(src), "s"(lds_base) : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds_base) {
+  __asm__ volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                   :: "v"(src), "s"(lds_base) : "memory", "m0");
+}
+
 // Copy a 64 x 128 bf16 tile into LDS with the DMA path.  Row r of the tile is
 // at base + r*stride elements; rows at or beyond nvalid re-read row nvalid-1
-// (finite data the kernels mask out).  NW waves share the 16 row quads.
+// (finite data the kernels mask out).  NW waves share the 16 row quads; wave
+// w copies quads w, w + NW, ...
+//
+// Lane L of wave w fills LDS slot (row 4*rq + L/16, chunk L%16), i.e. logical
+// chunk (L%16) ^ swz(row).  Since swz(row) = 4*(L/16) + (rq & 3) and
+// rq & 3 == w & 3 for every quad of the wave (NW is a multiple of 4), a lane's
+// byte offset inside its row quad is the same for every quad and every tile:
+// tile_lane_off() computes it once, and a full tile is copied with a scalar
+// base per quad and no per-lane address arithmetic.
+__device__ __forceinline__ uint32_t tile_lane_off(long stride, int tid) {
+  const int lane = tid & 63, w = tid >> 6;
+  const int rr = lane >> 4;
+  const int chunk = (lane & 15) ^ ((rr << 2) | (w & 3));
+  return (uint32_t)((rr * stride + 8 * chunk) * 2);
+}
+
 template <int NW>
 __device__ __forceinline__ void tile_dma(char* lds, const __bf16* base, long stride, int nvalid,
-                                         int tid) {
+                                         uint32_t lane_off, int tid) {
+  static_assert(NW % 4 == 0, "row-quad swizzle needs a multiple of 4 waves");
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int L = tid & 63;
+  const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  if (nvalid >= TILE_ROWS) {
 #pragma unroll
-  for (int i = 0; i < 16 / NW; ++i) {
-    const int rq = i * NW + w;                 // row quad: rows 4rq .. 4rq+3
-    const int row = 4 * rq + (L >> 4);
-    const int chunk = (L & 15) ^ swz(row);     // logical chunk this lane's slot holds
-    const int grow = min(row, nvalid - 1);
-    const __bf16* src = base + (long)grow * stride + 8 * chunk;
-    __builtin_amdgcn_global_load_lds((const MM1_GLOBAL void*)src, (MM1_LDS void*)(lds + rq * 1024),
-                                     16, 0, 0);
+    for (int i = 0; i < 16 / NW; ++i) {
+      const int rq = i * NW + w;
+      const char* sbase = reinterpret_cast<const char*>(base) + (long)(4 * rq) * stride * 2;
+      __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                       :: "v"(lane_off), "s"(sbase), "s"(l0 + rq * 1024) : "memory", "m0");
+    }
+  } else {
+    const int L = tid & 63;
+#pragma unroll
+    for (int i = 0; i < 16 / NW; ++i) {
+      const int rq = i * NW + w;                 // row quad: rows 4rq .. 4rq+3
+      const int row = 4 * rq + (L >> 4);
+      const int chunk = (L & 15) ^ swz(row);     // logical chunk this lane's slot holds
+      const int grow = min(row, nvalid - 1);
+      dma16(base + (long)grow * stride + 8 * chunk, l0 + rq * 1024);
+    }
   }
 }
 
 // Copy 64 consecutive floats (elements >= nvalid re-read element nvalid-1)
 // into LDS; issued by one whole wave.
 __device__ __forceinline__ void vec64_dma(char* lds, const float* base, int nvalid, int lane) {
-  const float* src = base + min(lane, nvalid - 1);
-  __builtin_amdgcn_global_load_lds((const MM1_GLOBAL void*)src, (MM1_LDS void*)lds, 4, 0, 0);
+  dma4(base + min(lane, nvalid - 1), __builtin_amdgcn_readfirstlane(lds_addr(lds)));
 }
 
 // A operand from a tile whose rows are the MFMA M axis: rows 32*blk + (lane&31),
@@ -126,6 +187,50 @@ __device__ __forceinline__ bf16x8 lds_a_tr(const char* lds, int blk, int ks, int
     const int row = 16 * ks + 8 * r + 4 * h + (j >> 2);
     const char* p = lds + row * 256 + ((chunk ^ swz(row)) << 4) + 8 * half;
     const bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MM1_LDS bf16x4*)p);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) out[4 * r + t] = v[t];
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Precomputed per-lane LDS addressing.  Every operand read of a tile is one of
+// a few per-lane byte offsets plus a compile-time constant, so loops need no
+// address arithmetic and the constants fold into the ds_read offset field.
+//
+// Row reads (lds_a_rows): offset = blk*8192 + (row_base ^ 32*ks), with
+//   row_base = (lane&31)*256 + 16*((lane>>5) ^ swz(lane&31)).
+// Transposed reads (lds_a_tr): offset = 4096*ks + tr_base[blk][r], r = 0, 1.
+struct LdsBases {
+  int row;
+  int tr[4][2];
+};
+
+__device__ __forceinline__ LdsBases make_lds_bases(int lane) {
+  LdsBases b;
+  const int l32 = lane & 31, h = lane >> 5;
+  b.row = l32 * 256 + 16 * (h ^ swz(l32));
+  const int g = (lane >> 4) & 1, j = lane & 15, jj = j >> 2;
+  const int x = 2 * g + ((j & 3) >> 1), half = j & 1;
+  const int p0 = (4 * h + jj) * 256 + 8 * half + 64 * jj + 16 * (x ^ h);
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) b.tr[blk][r] = (p0 ^ (64 * blk + 32 * r)) + 2048 * r;
+  }
+  return b;
+}
+
+__device__ __forceinline__ bf16x8 rows_a(const char* tile, const LdsBases& lb, int blk, int ks) {
+  return *reinterpret_cast<const bf16x8*>(tile + blk * 8192 + (lb.row ^ (32 * ks)));
+}
+
+__device__ __forceinline__ bf16x8 tr_a(const char* tile, const LdsBases& lb, int blk, int ks) {
+  bf16x8 out;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (MM1_LDS bf16x4*)(tile + 4096 * ks + lb.tr[blk][r]));
 #pragma unroll
     for (int t = 0; t < 4; ++t) out[4 * r + t] = v[t];
   }
