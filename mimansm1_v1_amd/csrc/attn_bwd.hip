@@ -287,19 +287,20 @@ __global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dQ: one workgroup per 128 packed query rows (4 waves x 32); K and V tiles of
-// 64 keys arrive by LDS DMA (row-major); K^T for dQ^T = K^T dS^T is read
-// transposed from the same K tile.
-template <bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void attn_dq_kernel(
+// dQ: one workgroup per NW*32 packed query rows (32 per wave); K and V tiles
+// of 64 keys arrive by LDS DMA (row-major) in an NSTAGE-deep ring; K^T for
+// dQ^T = K^T dS^T is read transposed from the same K tile.
+template <int NW, int NSTAGE, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     __bf16* __restrict__ dq,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles) {
-  constexpr int BM = 128;
+  constexpr int BM = NW * 32;
   constexpr int BN = TILE_ROWS;
   constexpr int BUF = 2 * TILE_BYTES;   // K, V
-  __shared__ __attribute__((aligned(1024))) char smem[2 * BUF];
+  constexpr int DMA_PER_TILE = 2 * (16 / NW);
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF];
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
@@ -313,12 +314,23 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(
   const int rw0 = r0 + 32 * w;
   const bool wave_active = rw0 < R;
 
+  const int last_row_wg = min(r0 + BM, R) - 1;
+  const int n_kt = CAUSAL ? (min(S - 1, last_row_wg / G) / BN + 1) : (S + BN - 1) / BN;
+  const int pw_lo = rw0 / G;
+  const int pw_hi = wave_active ? min(S - 1, (min(rw0 + 32, R) - 1) / G) : -1;
+
   const long kvstride = (long)Hkv * HD;
   const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
   const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
   const uint32_t dma_off = tile_lane_off(kvstride, tid);
-  tile_dma<4>(smem, kbase, kvstride, S, dma_off, tid);
-  tile_dma<4>(smem + TILE_BYTES, vbase, kvstride, S, dma_off, tid);
+  auto issue_tile = [&](char* buf, int kt) {
+    const int nk = kt * BN;
+    tile_dma<NW>(buf, kbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
+    tile_dma<NW>(buf + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
+  };
+#pragma unroll
+  for (int st = 0; st < NSTAGE - 1; ++st)
+    if (st < n_kt) issue_tile(smem + st * BUF, st);
 
   const int rr = rw0 + l32;
   const int qp = rr / G;
@@ -347,59 +359,63 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(
     }
   }
 
-  const int last_row_wg = min(r0 + BM, R) - 1;
-  const int n_kt = CAUSAL ? (min(S - 1, last_row_wg / G) / BN + 1) : (S + BN - 1) / BN;
-  const int pw_lo = rw0 / G;
-  const int pw_hi = wave_active ? min(S - 1, (min(rw0 + 32, R) - 1) / G) : -1;
-
   f32x16 dqacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) dqacc[db] = zero16();
+  const LdsBases lb = make_lds_bases(lane);
   wait_dma();
   __syncthreads();
 
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const char* kl = smem + (kt & 1) * BUF;
+  auto step = [&](auto slot, int kt) {
+    constexpr int P = decltype(slot)::value;
+    const char* kl = smem + P * BUF;
     const char* vl = kl + TILE_BYTES;
-    if (kt + 1 < n_kt) {
-      char* nb = smem + ((kt + 1) & 1) * BUF;
-      const int nk = (kt + 1) * BN;
-      tile_dma<4>(nb, kbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
-      tile_dma<4>(nb + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
-    }
+    const bool prefetch = kt + NSTAGE - 1 < n_kt;
+    if (prefetch) issue_tile(smem + ((P + NSTAGE - 1) % NSTAGE) * BUF, kt + NSTAGE - 1);
     const int k0 = kt * BN;
     if (wave_active && (!CAUSAL || k0 <= pw_hi)) {
       const bool need_mask = CAUSAL ? (k0 + BN - 1 > pw_lo) : (k0 + BN > S);
       // one 32-key block at a time keeps S^T/dP^T at 32 registers
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
-        f32x16 s = zero16(), dp = zero16();
+        f32x16 sv = zero16(), dp = zero16();
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-          s = mfma32(lds_a_rows(kl, jb, ks, lane), qreg[ks], s);
-          dp = mfma32(lds_a_rows(vl, jb, ks, lane), doreg[ks], dp);
+          sv = mfma32(rows_a(kl, lb, jb, ks), qreg[ks], sv);
+          dp = mfma32(rows_a(vl, lb, jb, ks), doreg[ks], dp);
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float p = exp2_fast(fmaf(s[r], scale2, -lse_i));
+          float pr = exp2_fast(fmaf(sv[r], scale2, -lse_i));
           if (need_mask) {
             const int key = k0 + 32 * jb + 8 * (r >> 2) + 4 * h + (r & 3);
             const bool masked = CAUSAL ? (key > qp) : (key >= S);
-            if (masked) p = 0.f;
+            if (masked) pr = 0.f;
           }
-          s[r] = p * (dp[r] - dl_i);   // dS^T
+          sv[r] = pr * (dp[r] - dl_i);   // dS^T
         }
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-          const bf16x8 sb = pack8(s, 8 * kh);
+          const bf16x8 sb = pack8(sv, 8 * kh);
 #pragma unroll
           for (int db = 0; db < 4; ++db)
-            dqacc[db] = mfma32(lds_a_tr(kl, db, 2 * jb + kh, lane), sb, dqacc[db]);
+            dqacc[db] = mfma32(tr_a(kl, lb, db, 2 * jb + kh), sb, dqacc[db]);
         }
       }
     }
-    wait_dma();
-    __syncthreads();
+    if (NSTAGE > 2 && prefetch) {
+      __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PER_TILE * (NSTAGE - 2)) : "memory");
+    } else {
+      wait_dma();
+    }
+    lds_barrier();
+  };
+  for (int kt = 0; kt < n_kt; kt += NSTAGE) {
+    step(std::integral_constant<int, 0>{}, kt);
+    if (kt + 1 < n_kt) step(std::integral_constant<int, 1>{}, kt + 1);
+    if constexpr (NSTAGE > 2) {
+      if (kt + 2 < n_kt) step(std::integral_constant<int, 2>{}, kt + 2);
+    }
   }
 
   if (!row_valid) return;
@@ -471,25 +487,38 @@ hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, i
   return hipGetLastError();
 }
 
+template <int NW, int NSTAGE>
+static void launch_dq_t(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* dO,
+                        const float* lse2, const float* delta, __bf16* dq, int B, int S, int H,
+                        int Hkv, bool causal, float scale2, float sm_scale, hipStream_t stream) {
+  const int G = H / Hkv;
+  const int BM = NW * 32;
+  const int n_qtiles = (G * S + BM - 1) / BM;
+  dim3 grid(n_qtiles * B * Hkv), block(NW * 64);
+  if (causal)
+    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, true>), grid, block, 0, stream, q, k, v, dO, lse2, delta, dq,
+                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles);
+  else
+    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, false>), grid, block, 0, stream, q, k, v, dO, lse2, delta, dq,
+                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles);
+}
+
+// variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
+//          1 = 8 waves x 3-stage ring (one workgroup per CU).
 hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                          const float* lse2, const float* delta, void* dq,
-                         int B, int S, int H, int Hkv, bool causal, float sm_scale,
+                         int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                          hipStream_t stream) {
-  const int G = H / Hkv;
   const float scale2 = sm_scale * 1.4426950408889634f;
   auto qp = static_cast<const __bf16*>(q);
   auto kp = static_cast<const __bf16*>(k);
   auto vp = static_cast<const __bf16*>(v);
   auto dop = static_cast<const __bf16*>(dO);
   auto dqp = static_cast<__bf16*>(dq);
-  const int n_qtiles = (G * S + 127) / 128;
-  dim3 grid(n_qtiles * B * Hkv);
-  if (causal)
-    hipLaunchKernelGGL(attn_dq_kernel<true>, grid, dim3(256), 0, stream, qp, kp, vp, dop, lse2, delta, dqp,
-                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles);
+  if (variant == 1)
+    launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, stream);
   else
-    hipLaunchKernelGGL(attn_dq_kernel<false>, grid, dim3(256), 0, stream, qp, kp, vp, dop, lse2, delta, dqp,
-                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles);
+    launch_dq_t<4, 2>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, stream);
   return hipGetLastError();
 }
 

@@ -8,7 +8,7 @@
 
 namespace mm1 {
 hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
-                      int B, int S, int H, int Hkv, bool causal, float sm_scale, int qw,
+                      int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                       hipStream_t stream);
 hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int S, int H,
                         hipStream_t stream);
@@ -21,7 +21,7 @@ hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, i
                              hipStream_t stream);
 hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                          const float* lse2, const float* delta, void* dq,
-                         int B, int S, int H, int Hkv, bool causal, float sm_scale,
+                         int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                          hipStream_t stream);
 }  // namespace mm1
 
@@ -39,14 +39,18 @@ int check_shape(int B, int S, int H, int Hkv, int D) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Forward tile variant: query rows per wave (64: one wave per SIMD; 32: two).
-// MM1_FWD_ROWS_PER_WAVE overrides the default for tile experiments.
-int fwd_rows_per_wave() {
-  static const int v = [] {
-    const char* e = getenv("MM1_FWD_ROWS_PER_WAVE");
-    const int x = e ? atoi(e) : 0;
-    return (x == 32 || x == 64) ? x : 32;
-  }();
+// Kernel variants (see launch_fwd / launch_bwd_dq).  MM1_FWD_VARIANT and
+// MM1_DQ_VARIANT override the defaults for tile experiments.
+int env_variant(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : dflt;
+}
+int fwd_variant() {
+  static const int v = env_variant("MM1_FWD_VARIANT", 0);
+  return v;
+}
+int dq_variant() {
+  static const int v = env_variant("MM1_DQ_VARIANT", 0);
   return v;
 }
 
@@ -66,7 +70,7 @@ int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
   if (rc) return rc;
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MM1_E_ALIGN;
-  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale, fwd_rows_per_wave(),
+  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale, fwd_variant(),
                                   static_cast<hipStream_t>(stream)));
 }
 
@@ -127,7 +131,7 @@ int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq))
     return MM1_E_ALIGN;
   return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, B, S, H, Hkv, causal != 0,
-                                     sm_scale, static_cast<hipStream_t>(stream)));
+                                     sm_scale, dq_variant(), static_cast<hipStream_t>(stream)));
 }
 
 int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
