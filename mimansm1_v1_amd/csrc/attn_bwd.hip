@@ -165,25 +165,37 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
       f32x16 sv;
       if (active) {
         const char* arows = pwave ? ql : dol;
+        // lse2 (P wave) rows of this block, read ahead of the products
+        f32x4 lse4[4];
+        if (pwave) {
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4)
+            lse4[a4] = *reinterpret_cast<const f32x4*>(lsel + 32 * qb + 8 * a4 + 4 * h);
+        }
         sv = zero16();
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) sv = mfma32(rows_a(arows, lb, qb, ks), breg[ks], sv);
         if (pwave) {
+          // P = exp2(S*scale2 - lse2); masked (causal or past the end) only in
+          // the tiles that need it, as separate straight-line code
+          auto softmax = [&](auto masked) {
 #pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-            const int i0 = 32 * qb + 8 * a4 + 4 * h;
-            const f32x4 lse4 = *reinterpret_cast<const f32x4*>(lsel + i0);
+            for (int a4 = 0; a4 < 4; ++a4) {
+              const int i0 = 32 * qb + 8 * a4 + 4 * h;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const int r = 4 * a4 + c;
-              float pr = exp2_fast(fmaf(sv[r], scale2, -lse4[c]));
-              if (need_mask) {
-                const int qpos = p0 + i0 + c;
-                if ((CAUSAL && key > qpos) || qpos >= S) pr = 0.f;
+              for (int c = 0; c < 4; ++c) {
+                const int r = 4 * a4 + c;
+                float pr = exp2_fast(fmaf(sv[r], scale2, -lse4[a4][c]));
+                if constexpr (decltype(masked)::value) {
+                  const int qpos = p0 + i0 + c;
+                  pr = ((CAUSAL && key > qpos) || qpos >= S) ? 0.f : pr;
+                }
+                sv[r] = pr;
               }
-              sv[r] = pr;
             }
-          }
+          };
+          if (need_mask) softmax(std::true_type{});
+          else softmax(std::false_type{});
 #pragma unroll
           for (int a4 = 0; a4 < 4; ++a4) {
             f32x4 v4;
@@ -384,16 +396,21 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
           sv = mfma32(rows_a(kl, lb, jb, ks), qreg[ks], sv);
           dp = mfma32(rows_a(vl, lb, jb, ks), doreg[ks], dp);
         }
+        // dS^T = P^T (dP^T - Delta), masked only in the tiles that need it,
+        // as separate straight-line code
+        auto dscore = [&](auto masked) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float pr = exp2_fast(fmaf(sv[r], scale2, -lse_i));
-          if (need_mask) {
-            const int key = k0 + 32 * jb + 8 * (r >> 2) + 4 * h + (r & 3);
-            const bool masked = CAUSAL ? (key > qp) : (key >= S);
-            if (masked) pr = 0.f;
+          for (int r = 0; r < 16; ++r) {
+            float pr = exp2_fast(fmaf(sv[r], scale2, -lse_i));
+            if constexpr (decltype(masked)::value) {
+              const int key = k0 + 32 * jb + 8 * (r >> 2) + 4 * h + (r & 3);
+              pr = (CAUSAL ? (key > qp) : (key >= S)) ? 0.f : pr;
+            }
+            sv[r] = pr * (dp[r] - dl_i);
           }
-          sv[r] = pr * (dp[r] - dl_i);   // dS^T
-        }
+        };
+        if (need_mask) dscore(std::true_type{});
+        else dscore(std::false_type{});
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
           const bf16x8 sb = pack8(sv, 8 * kh);

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
           for (int r = 0; r < 16; ++r) {
             const int key = k0 + 32 * jb + 8 * (r >> 2) + 4 * h + (r & 3);
             const bool masked = CAUSAL ? (key > qpos) : (key >= S);
-            if (masked) sacc[jb][r] = -INFINITY;
+            sacc[jb][r] = masked ? -INFINITY : sacc[jb][r];
           }
         }
       }
