@@ -143,8 +143,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
 
   // One query tile; the loop below runs it NSTAGE times per trip so the ring
   // slot (and every LDS offset) is a compile-time constant.
-  auto step = [&](auto slot, int it) {
+  auto step = [&](auto slot, int it, auto role) {
     constexpr int P = decltype(slot)::value;
+    constexpr bool PW = decltype(role)::value;   // P wave (else dS wave)
     const char* ql = smem + P * BUF;
     const char* dol = ql + TILE_BYTES;
     const float* lsel = reinterpret_cast<const float*>(ql + 2 * TILE_BYTES);
@@ -164,10 +165,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
       float* mbox = reinterpret_cast<float*>(mbox_base + (pair * 2 + qb) * MBOX) + lane * 4;
       f32x16 sv;
       if (active) {
-        const char* arows = pwave ? ql : dol;
+        const char* arows = PW ? ql : dol;
         // lse2 (P wave) rows of this block, read ahead of the products
         f32x4 lse4[4];
-        if (pwave) {
+        if constexpr (PW) {
 #pragma unroll
           for (int a4 = 0; a4 < 4; ++a4)
             lse4[a4] = *reinterpret_cast<const f32x4*>(lsel + 32 * qb + 8 * a4 + 4 * h);
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
         sv = zero16();
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) sv = mfma32(rows_a(arows, lb, qb, ks), breg[ks], sv);
-        if (pwave) {
+        if constexpr (PW) {
           // P = exp2(S*scale2 - lse2); masked (causal or past the end) only in
           // the tiles that need it, as separate straight-line code
           auto softmax = [&](auto masked) {
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
       }
       lds_barrier();   // P of this block is in the mailbox
       if (active) {
-        if (pwave) {
+        if constexpr (PW) {
 #pragma unroll
           for (int kh = 0; kh < 2; ++kh) {
             const bf16x8 pb = pack8(sv, 8 * kh);
@@ -241,11 +242,16 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
     }
     lds_barrier();
   };
-  for (int it = 0; it < n_qt; it += NSTAGE) {
-    step(std::integral_constant<int, 0>{}, it);
-    if (it + 1 < n_qt) step(std::integral_constant<int, 1>{}, it + 1);
-    if (it + 2 < n_qt) step(std::integral_constant<int, 2>{}, it + 2);
-  }
+  // each role runs its own specialised copy of the loop (same barriers)
+  auto run = [&](auto role) {
+    for (int it = 0; it < n_qt; it += NSTAGE) {
+      step(std::integral_constant<int, 0>{}, it, role);
+      if (it + 1 < n_qt) step(std::integral_constant<int, 1>{}, it + 1, role);
+      if (it + 2 < n_qt) step(std::integral_constant<int, 2>{}, it + 2, role);
+    }
+  };
+  if (pwave) run(std::true_type{});
+  else run(std::false_type{});
 
   if (key >= S) return;
   // D layout of dK^T / dV^T: register r of block db holds column
