@@ -15,12 +15,12 @@
 //
 // The decomposition here is atomic-free and deterministic:
 //   * attn_delta_kernel   : Delta, one 16-lane group per (b, s, h) row.
-//   * attn_dkdv_kernel    : key-stationary, one workgroup per (128-key tile,
-//     query head).  Each wave keeps 32 keys of K and V in registers and dK/dV
-//     accumulators in registers while it walks the head's query tiles, which
-//     arrive in LDS by DMA (row-major; transposed operands are read with the
-//     LDS transpose read).  With G > 1 the
-//     per-head partial sums go to an fp32 workspace [G][B][S][Hkv][D] and
+//   * attn_dkdv_pipe_kernel (default) / attn_dkdv_kernel : key-stationary,
+//     one workgroup per (128-key tile, query head).  Each wave pair keeps 32
+//     keys of K and V and their dK/dV accumulators in registers while it
+//     walks the head's query tiles, which arrive in LDS by DMA (row-major;
+//     transposed operands are read with the LDS transpose read).  With G > 1
+//     the per-head partial sums go to an fp32 workspace [G][B][S][Hkv][D] and
 //     attn_dkdv_reduce_kernel adds the G heads of each group and rounds once.
 //   * attn_dq_kernel      : query-stationary over the packed GQA row space
 //     (as in the forward): K/V tiles in LDS serve all G heads of a group and
@@ -285,6 +285,298 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
   }
 }
 
+// Calls f(integral_constant<J>) for J = 0 .. N-1 while it returns true.
+template <int J, int N, class F>
+__device__ __forceinline__ void unroll_while(F&& f) {
+  if constexpr (J < N) {
+    if (f(std::integral_constant<int, J>{})) unroll_while<J + 1, N>(f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV, software-pipelined across the two roles of a pair.
+//
+// Same decomposition and roles as attn_dkdv_kernel (one workgroup per
+// (128-key tile, query head), pair i owns keys kt*128 + 32i .. +31, P wave
+// keeps K and dV^T, dS wave keeps V and dK^T), but the query tiles are 32
+// rows and the work on a tile is spread over four segments:
+//   segment s, P wave : S(s+1) = Q(s+1) K^T | P(s) = exp2(S(s) scale2 - lse2) -> mailbox | dV^T += dO(s-1)^T P(s-1)
+//   segment s, dS wave: dP(s) = dO(s) V^T   | dS(s-1) = P(s-1) (dP(s-1) - Delta)          | dK^T += Q(s-2)^T dS(s-2)
+// Within a segment each wave's VALU work (middle column) depends on no
+// product of the same segment, so it runs under the wave's own 16 products
+// and the other wave's, and the pair meets at one barrier per segment, which
+// also publishes the DMA ring.  S(s+1), P(s-1) (bf16) stay in the P wave's
+// registers, dP(s-1) and dS(s-2) (bf16) in the dS wave's.
+//
+// Tile x of the ring lives in slot x % NSTAGE; it is first read in segment
+// x-1 and last in segment x+2, so segment s refills slot (s-3) % NSTAGE with
+// tile s + NSTAGE - 3 and waits for tile s+2 before its barrier (NSTAGE - 5
+// segments of lead).  Tiles whose queries all precede a pair's keys (causal)
+// are computed with the mask (P = 0): the pair would otherwise only wait at
+// the barrier.
+template <int NSTAGE, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
+    float* __restrict__ ws_dk, float* __restrict__ ws_dv,
+    __bf16* __restrict__ dk, __bf16* __restrict__ dv,
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale) {
+  static_assert(NSTAGE >= 6, "ring depth: at least 6");
+  constexpr int BQ = 32;                  // query positions per tile
+  constexpr int QT = BQ * HD * 2;         // one 32 x 128 bf16 operand tile
+  constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse2 x 32 | Delta x 32], 1 KiB aligned
+  constexpr int MBOX = 32 * 32 * 4;       // one 32 x 32 fp32 P block
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + 4 * 2 * MBOX];
+
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
+  const int pair = w & 3;
+  const bool pwave = w < 4;
+  const int nbh = B * H;
+  const int kt = blockIdx.x / nbh;        // heaviest key tiles first
+  const int bh = blockIdx.x % nbh;
+  const int b = bh / H, hq = bh % H;
+  const int g = hq / G, hh = hq % G;
+  const int kw0 = kt * 128 + 32 * pair;   // this pair's first key
+  const int key = kw0 + l32;
+  // mailbox of this pair, two slots; [register group a4][lane] x 4 floats so
+  // each 16-byte access of a wave is one contiguous 1 KiB row
+  float* const mbox = reinterpret_cast<float*>(smem + NSTAGE * BUF + pair * 2 * MBOX) + lane * 4;
+
+  const int q_begin = CAUSAL ? kt * 128 : 0;
+  const int n_qt = (S - q_begin + BQ - 1) / BQ;
+  const long qstride = (long)H * HD;
+  const __bf16* qbase = q + ((long)b * S * H + hq) * HD;
+  const __bf16* dobase = dO + ((long)b * S * H + hq) * HD;
+  const float* lse_row = lse2 + ((long)b * H + hq) * S;
+  const float* dl_row = delta + ((long)b * H + hq) * S;
+
+  // Query tiles are walked from the sequence end down to q_begin, so the
+  // workgroups of one head that start together read the same tiles together.
+  // Only the first tile walked (it = 0) can be partial (S % 32 != 0).
+  auto tile_p0 = [&](int it) { return q_begin + (n_qt - 1 - it) * BQ; };
+  // LDS DMA, per wave and tile: row quad w of Q and of dO; wave 0 adds the
+  // lse2 | Delta vector (lanes 0-31 lse2, lanes 32-63 Delta).
+  const uint32_t dma_off = tile_lane_off(qstride, tid);
+  const uint32_t lds_smem = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  const uint32_t lds_quad = lds_smem + w * 1024;       // this wave's row quad in slot 0
+  const long quad_rows = (long)(4 * w) * qstride;      // its first row, in elements
+  const float* vec_src = (h ? dl_row : lse_row) + l32;
+  auto issue_full = [&](int slot, int p0) {
+    const uint32_t l = lds_quad + slot * BUF;
+    dma16_sbase(dma_off, qbase + (long)p0 * qstride + quad_rows, l);
+    dma16_sbase(dma_off, dobase + (long)p0 * qstride + quad_rows, l + QT);
+    if (w == 0) dma4(vec_src + p0, lds_smem + slot * BUF + 2 * QT);
+  };
+  for (int it = 0; it < NSTAGE - 3 && it < n_qt; ++it) {
+    const int p0 = tile_p0(it);
+    if (p0 + BQ <= S) {
+      issue_full(it, p0);
+    } else {
+      tile32_dma(smem + it * BUF, qbase + (long)p0 * qstride, qstride, S - p0, dma_off, tid);
+      tile32_dma(smem + it * BUF + QT, dobase + (long)p0 * qstride, qstride, S - p0, dma_off, tid);
+      if (w == 0) dma4((h ? dl_row : lse_row) + min(p0 + l32, S - 1), lds_smem + it * BUF + 2 * QT);
+    }
+  }
+
+  // This lane's key row of K (P wave) or V (dS wave) as the B operand.
+  bf16x8 breg[8];
+  {
+    const int kk = min(key, S - 1);
+    const __bf16* src = (pwave ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) breg[ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) pin(breg[ks]);
+  }
+
+  f32x16 acc[4];   // dV^T (P wave) or dK^T (dS wave)
+#pragma unroll
+  for (int db = 0; db < 4; ++db) acc[db] = zero16();
+  bf16x8 pb[2];    // P wave: P(s-1) as the B operand of dV^T
+  f32x16 snext;    // P wave: S(s), computed one segment ahead
+  f32x16 dpp;      // dS wave: dP(s-1)
+  bf16x8 sbp[2];   // dS wave: dS(s-2) as the B operand of dK^T
+  const LdsBases lb = make_lds_bases(lane);
+  wait_dma();
+  __syncthreads();
+  // S = Q K^T / dP = dO V^T of one tile (D layout: register r holds query
+  // 8*(r/4) + 4*h + (r%4) of the tile, lane l32 holds key kw0 + l32)
+  auto product = [&](const char* t) {
+    f32x16 sacc = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) sacc = mfma32(rows_a(t, lb, 0, ks), breg[ks], sacc);
+    return sacc;
+  };
+  if (pwave) snext = product(smem);
+
+  // Segment s.  tn, tc, tp, tp2: ring slots of tiles s+1, s, s-1, s-2.
+  // CUR: s < n_qt; PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a
+  // later segment reads what this one publishes (mailbox, ring).  In the last
+  // segment with CUR, S(s+1) reads a slot holding another tile (or nothing
+  // yet) and is discarded: every read stays inside the ring.
+  auto segment = [&](const char* tn, const char* tc, const char* tp, const char* tp2, int refill,
+                     int s, auto role, auto cur, auto prev, auto prev2, auto sync) {
+    constexpr bool PW = decltype(role)::value;
+    constexpr bool CUR = decltype(cur)::value, PREV = decltype(prev)::value;
+    constexpr bool PREV2 = decltype(prev2)::value, SYNC = decltype(sync)::value;
+    if (CUR && s + NSTAGE - 3 < n_qt) issue_full(refill, tile_p0(s + NSTAGE - 3));
+    if constexpr (PW) {
+      f32x16 sv;
+      if constexpr (CUR) {
+        const float* lsel = reinterpret_cast<const float*>(tc + 2 * QT);
+        f32x4 lse4[4];
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) lse4[a4] = *reinterpret_cast<const f32x4*>(lsel + 8 * a4 + 4 * h);
+        sv = snext;
+        snext = product(tn);
+        // P = exp2(S*scale2 - lse2)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sv[4 * a4 + c] = exp2_fast(fmaf(sv[4 * a4 + c], scale2, -lse4[a4][c]));
+        }
+      }
+      if constexpr (PREV) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) acc[db] = mfma32(tr_a(tp + QT, lb, db, kh), pb[kh], acc[db]);
+        }
+      }
+      if constexpr (CUR) {
+        // causal / past-the-end mask, only in the tiles that need it
+        const int p0 = tile_p0(s);
+        if ((CAUSAL && p0 < kw0 + 31) || p0 + BQ > S) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int qpos = p0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            sv[r] = ((CAUSAL && key > qpos) || qpos >= S) ? 0.f : sv[r];
+          }
+        }
+        float* mb = mbox + (s & 1) * (MBOX / 4);
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          f32x4 v4;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v4[c] = sv[4 * a4 + c];
+          *reinterpret_cast<f32x4*>(mb + 256 * a4) = v4;
+        }
+        pb[0] = pack8(sv, 0);
+        pb[1] = pack8(sv, 8);
+        // keep the conversion in this segment (it would otherwise sink to
+        // its first use, in the next one, where it runs before any product)
+        pin(pb[0]);
+        pin(pb[1]);
+      }
+    } else {
+      f32x16 dpn;
+      if constexpr (CUR) dpn = product(tc + QT);
+      if constexpr (PREV2) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) acc[db] = mfma32(tr_a(tp2, lb, db, kh), sbp[kh], acc[db]);
+        }
+      }
+      if constexpr (PREV) {
+        const float* mb = mbox + ((s - 1) & 1) * (MBOX / 4);
+        const float* dll = reinterpret_cast<const float*>(tp + 2 * QT) + BQ;
+        f32x16 dsv;
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          const f32x4 dl4 = *reinterpret_cast<const f32x4*>(dll + 8 * a4 + 4 * h);
+          const f32x4 p4 = *reinterpret_cast<const f32x4*>(mb + 256 * a4);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) dsv[4 * a4 + c] = p4[c] * (dpp[4 * a4 + c] - dl4[c]);
+        }
+        sbp[0] = pack8(dsv, 0);
+        sbp[1] = pack8(dsv, 8);
+        // keep dS in this segment, under the products (see above)
+        pin(sbp[0]);
+        pin(sbp[1]);
+      }
+      if constexpr (CUR) dpp = dpn;
+    }
+    if constexpr (SYNC) {
+      // tile s+2 must have landed; the newer prefetches stay in flight
+      if (s + NSTAGE - 3 < n_qt) {
+        if (w == 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (NSTAGE - 5)) : "memory");
+        else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (NSTAGE - 5)) : "memory");
+      } else {
+        wait_dma();
+      }
+      lds_barrier();
+    }
+  };
+
+  // Each role runs its own specialised copy of the loop (same barriers).
+  // Segments 2 .. n_qt-1 are unrolled NSTAGE at a time so that every ring
+  // slot, and so every LDS offset, is a compile-time constant.
+  using T = std::true_type;
+  using F = std::false_type;
+  auto slot = [&](int c) { return smem + c * BUF; };
+  auto run = [&](auto role) {
+    const char* s0p = slot(0);
+    const char* s1p = slot(1);
+    if (n_qt == 1) {
+      segment(s1p, s0p, s0p, s0p, NSTAGE - 3, 0, role, T{}, F{}, F{}, T{});
+      segment(s0p, s0p, s0p, s0p, 0, 1, role, F{}, T{}, F{}, F{});
+      segment(s0p, s0p, s0p, s0p, 0, 2, role, F{}, F{}, T{}, F{});
+      return;
+    }
+    segment(s1p, s0p, s0p, s0p, NSTAGE - 3, 0, role, T{}, F{}, F{}, T{});
+    segment(slot(2), s1p, s0p, s0p, NSTAGE - 2, 1, role, T{}, T{}, F{}, T{});
+    for (int b0 = 2; b0 < n_qt; b0 += NSTAGE) {
+      unroll_while<0, NSTAGE>([&](auto j) {
+        constexpr int C = (2 + decltype(j)::value) % NSTAGE;
+        const int s = b0 + decltype(j)::value;
+        if (s >= n_qt) return false;
+        segment(slot((C + 1) % NSTAGE), slot(C), slot((C + NSTAGE - 1) % NSTAGE),
+                slot((C + NSTAGE - 2) % NSTAGE), (C + NSTAGE - 3) % NSTAGE, s, role, T{}, T{}, T{}, T{});
+        return true;
+      });
+    }
+    const char* tl = slot((n_qt - 1) % NSTAGE);
+    const char* tl2 = slot((n_qt - 2) % NSTAGE);
+    segment(tl, tl, tl, tl2, 0, n_qt, role, F{}, T{}, T{}, F{});
+    segment(tl, tl, tl, tl, 0, n_qt + 1, role, F{}, F{}, T{}, F{});
+  };
+  if (pwave) run(std::true_type{});
+  else run(std::false_type{});
+
+  if (key >= S) return;
+  // D layout of dK^T / dV^T: register r of block db holds column
+  // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
+  const float scale_out = pwave ? 1.f : sm_scale;
+  if (G == 1) {
+    __bf16* row = (pwave ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        bf16x4 o4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o4[c] = (__bf16)(acc[db][4 * a4 + c] * scale_out);
+        *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+      }
+    }
+  } else {
+    const long slot = (long)hh * B * S * Hkv * HD;
+    float* row = (pwave ? ws_dv : ws_dk) + slot + ((long)(b * S + key) * Hkv + g) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        f32x4 o4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o4[c] = acc[db][4 * a4 + c] * scale_out;
+        *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+      }
+    }
+  }
+}
+
 // Sum the G per-head partials of dK and dV and round to bf16 once.
 __global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(
     const float* __restrict__ ws_dk, const float* __restrict__ ws_dv,
@@ -471,10 +763,12 @@ size_t bwd_workspace_bytes(int B, int S, int H, int Hkv) {
   return (size_t)2 * G * B * S * Hkv * HD * sizeof(float);
 }
 
+// variant: 0 = attn_dkdv_pipe_kernel (7-slot ring of 32-query tiles),
+//          1 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries).
 hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
                            const float* lse2, const float* delta, void* dk, void* dv,
                            void* workspace, int B, int S, int H, int Hkv, bool causal,
-                           float sm_scale, hipStream_t stream) {
+                           float sm_scale, int variant, hipStream_t stream) {
   const int G = H / Hkv;
   const float scale2 = sm_scale * 1.4426950408889634f;
   const long n_kv = (long)B * S * Hkv * HD;
@@ -488,12 +782,17 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
   auto dvp = static_cast<__bf16*>(dv);
   const int n_ktiles = (S + 127) / 128;
   dim3 grid(n_ktiles * B * H);
-  if (causal)
-    hipLaunchKernelGGL(attn_dkdv_kernel<true>, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta,
-                       ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale);
-  else
-    hipLaunchKernelGGL(attn_dkdv_kernel<false>, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta,
-                       ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale);
+#define MM1_DKDV_LAUNCH(KERNEL)                                                               \
+  hipLaunchKernelGGL(KERNEL, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta, ws_dk, \
+                     ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale)
+  if (variant == 1) {
+    if (causal) MM1_DKDV_LAUNCH(attn_dkdv_kernel<true>);
+    else MM1_DKDV_LAUNCH(attn_dkdv_kernel<false>);
+  } else {
+    if (causal) MM1_DKDV_LAUNCH((attn_dkdv_pipe_kernel<7, true>));
+    else MM1_DKDV_LAUNCH((attn_dkdv_pipe_kernel<7, false>));
+  }
+#undef MM1_DKDV_LAUNCH
   return hipGetLastError();
 }
 

@@ -16,7 +16,7 @@ size_t bwd_workspace_bytes(int B, int S, int H, int Hkv);
 hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
                            const float* lse2, const float* delta, void* dk, void* dv,
                            void* workspace, int B, int S, int H, int Hkv, bool causal,
-                           float sm_scale, hipStream_t stream);
+                           float sm_scale, int variant, hipStream_t stream);
 hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
                              hipStream_t stream);
 hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
@@ -39,8 +39,9 @@ int check_shape(int B, int S, int H, int Hkv, int D) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Kernel variants (see launch_fwd / launch_bwd_dq).  MM1_FWD_VARIANT and
-// MM1_DQ_VARIANT override the defaults for tile experiments.
+// Kernel variants (see launch_fwd / launch_bwd_dkdv / launch_bwd_dq).
+// MM1_FWD_VARIANT, MM1_DKDV_VARIANT and MM1_DQ_VARIANT override the defaults
+// for tile experiments.
 int env_variant(const char* name, int dflt) {
   const char* e = getenv(name);
   return e ? atoi(e) : dflt;
@@ -51,6 +52,10 @@ int fwd_variant() {
 }
 int dq_variant() {
   static const int v = env_variant("MM1_DQ_VARIANT", 0);
+  return v;
+}
+int dkdv_variant() {
+  static const int v = env_variant("MM1_DKDV_VARIANT", 0);
   return v;
 }
 
@@ -103,7 +108,7 @@ int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* d
       !aligned16(dv) || (need > 0 && !aligned16(workspace)))
     return MM1_E_ALIGN;
   return from_hip(mm1::launch_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, need > 0 ? workspace : nullptr,
-                                       B, S, H, Hkv, causal != 0, sm_scale,
+                                       B, S, H, Hkv, causal != 0, sm_scale, dkdv_variant(),
                                        static_cast<hipStream_t>(stream)));
 }
 

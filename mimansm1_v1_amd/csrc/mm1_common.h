@@ -114,6 +114,13 @@ __device__ __forceinline__ void dma4(const void* src, uint32_t lds_base) {
                    :: "v"(src), "s"(lds_base) : "memory", "m0");
 }
 
+// Same copy with a wave-uniform global base (scalar register pair) and a
+// per-lane byte offset.
+__device__ __forceinline__ void dma16_sbase(uint32_t lane_off, const void* sbase, uint32_t lds_base) {
+  __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                   :: "v"(lane_off), "s"(sbase), "s"(lds_base) : "memory", "m0");
+}
+
 // Copy a 64 x 128 bf16 tile into LDS with the DMA path.  Row r of the tile is
 // at base + r*stride elements; rows at or beyond nvalid re-read row nvalid-1
 // (finite data the kernels mask out).  NW waves share the 16 row quads; wave
@@ -156,6 +163,25 @@ __device__ __forceinline__ void tile_dma(char* lds, const __bf16* base, long str
       const int grow = min(row, nvalid - 1);
       dma16(base + (long)grow * stride + 8 * chunk, l0 + rq * 1024);
     }
+  }
+}
+
+// Copy a 32 x 128 bf16 tile (the layout of the first 32 rows of a 64-row
+// tile) with the LDS DMA path; issued by all 8 waves, wave w copies row quad
+// w (so swz(row) = 4*(L/16) + (w & 3) and tile_lane_off() applies as above).
+__device__ __forceinline__ void tile32_dma(char* lds, const __bf16* base, long stride, int nvalid,
+                                           uint32_t lane_off, int tid) {
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + w * 1024;
+  if (nvalid >= 32) {
+    const char* sbase = reinterpret_cast<const char*>(base) + (long)(4 * w) * stride * 2;
+    __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                     :: "v"(lane_off), "s"(sbase), "s"(l0) : "memory", "m0");
+  } else {
+    const int L = tid & 63;
+    const int row = 4 * w + (L >> 4);
+    const int chunk = (L & 15) ^ swz(row);
+    dma16(base + (long)min(row, nvalid - 1) * stride + 8 * chunk, l0);
   }
 }
 
