@@ -11,7 +11,6 @@ import os
 import threading
 from pathlib import Path
 
-from . import build as _build
 
 # Every symbol include/mm1_attn.h declares, with its ctypes signature.
 _c_int, _c_float, _c_size, _vp = ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
@@ -43,7 +42,10 @@ class LibraryMissing(RuntimeError):
 def library_path() -> Path:
     """The in-tree build, or the file MM1_ATTN_LIB names (to compare builds)."""
     override = os.environ.get("MM1_ATTN_LIB")
-    return Path(override).resolve() if override else _build.library_path()
+    if override:
+        return Path(override).resolve()
+    from . import build   # imported here: `python -m mimansm1_v1_amd.build` must not find it loaded
+    return build.library_path()
 
 
 def load() -> ctypes.CDLL:
