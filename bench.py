@@ -299,7 +299,7 @@ def main(argv=None):
         "reference_flop_count_tflops": round(main_res["tflops"] * 5 / 7, 2),
         "roofline": {
             "bound": "mfma",
-            "kernel": {"fwd": "attn_fwd_kernel", "dkdv": "attn_dkdv_kernel",
+            "kernel": {"fwd": "attn_fwd_kernel", "dkdv": "attn_dkdv_pipe_kernel",
                        "dq": "attn_dq_kernel"}[dom],
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,

@@ -1,0 +1,100 @@
+"""Summarise rocprofv3 output of a bench.py run (kernel times and HBM traffic).
+
+    python -m mimansm1_v1_amd.profsum --trace DIR/prof_trace/trace_results.db \\
+        --fetch DIR/pmc_fetch/fetch_counter_collection.csv \\
+        --write DIR/pmc_write/write_counter_collection.csv \\
+        --copy-fetch DIR/pmc_copy_fetch/cf_counter_collection.csv \\
+        --copy-write DIR/pmc_copy_write/cw_counter_collection.csv \\
+        --copy-bytes 1073741824 [--json profiles/traffic_config3.json]
+
+Kernel times come from the ``top_kernels`` view of the ``--kernel-trace
+--stats`` database.  FETCH_SIZE / WRITE_SIZE (KiB per dispatch, averaged over a
+kernel's dispatches) are scaled by the factors that make the same counters read
+``--copy-bytes`` for the plain device copy of that many bytes (the largest
+dispatch of the calibration runs).
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import sqlite3
+from collections import defaultdict
+
+SHORT = {
+    "attn_fwd_kernel": "fwd",
+    "attn_dkdv_pipe_kernel": "dkdv",
+    "attn_dkdv_kernel": "dkdv",
+    "attn_dq_kernel": "dq",
+    "attn_dkdv_reduce_kernel": "reduce",
+    "attn_delta_kernel": "delta",
+}
+
+
+def kernel_key(name: str) -> str:
+    base = name.replace("void ", "").split("(")[0].split("<")[0]
+    return base.split("::")[-1]
+
+
+def trace_table(db: str):
+    con = sqlite3.connect(db)
+    rows = con.execute("select name, total_calls, average, percentage from top_kernels").fetchall()
+    return [(kernel_key(n), n.split("(")[0].replace("void ", ""), c, avg, pct) for n, c, avg, pct in rows]
+
+
+def counter_means(path: str):
+    vals = defaultdict(list)
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            vals[kernel_key(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in vals.items()}
+
+
+def copy_kib(path: str) -> float:
+    with open(path, newline="") as f:
+        return max(float(r["Counter_Value"]) for r in csv.DictReader(f))
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--trace")
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--copy-fetch")
+    ap.add_argument("--copy-write")
+    ap.add_argument("--copy-bytes", type=int, default=1 << 30)
+    ap.add_argument("--json", help="write {short kernel name: HBM bytes per launch} here")
+    args = ap.parse_args(argv)
+
+    if args.trace:
+        print("| kernel | calls | avg µs | share |\n|---|---:|---:|---:|")
+        for _, full, calls, avg, pct in trace_table(args.trace):
+            print(f"| `{full}` | {calls} | {avg:.1f} | {pct:.1f}% |")
+        print()
+    if args.fetch and args.write and args.copy_fetch and args.copy_write:
+        kib = args.copy_bytes / 1024
+        f_scale = kib / copy_kib(args.copy_fetch)
+        w_scale = kib / copy_kib(args.copy_write)
+        fetch, write = counter_means(args.fetch), counter_means(args.write)
+        print(f"calibration: FETCH_SIZE x {f_scale:.4f}, WRITE_SIZE x {w_scale:.4f} "
+              f"(copy of {args.copy_bytes} bytes)\n")
+        print("| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes/launch (scaled) |\n|---|---:|---:|---:|")
+        traffic = {}
+        for k in sorted(fetch):
+            if k not in SHORT or k not in write:
+                continue
+            total = (fetch[k] * f_scale + write[k] * w_scale) * 1024
+            traffic[SHORT[k]] = int(round(total))
+            print(f"| `{k}` | {fetch[k]:,.0f} | {write[k]:,.0f} | {total / 1e6:,.1f} MB |")
+        if args.json:
+            traffic["_note"] = (f"HBM-side bytes per launch: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                                f"(KiB per dispatch, mean over dispatches) scaled by {f_scale:.4f} and "
+                                f"{w_scale:.4f}, the factors that make the same counters read "
+                                f"{args.copy_bytes} bytes for a device copy of that size")
+            with open(args.json, "w") as f:
+                json.dump(traffic, f, indent=1)
+                f.write("\n")
+
+
+if __name__ == "__main__":
+    main()

@@ -108,3 +108,29 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_profsum_tables(tmp_path, capsys):
+    """profsum reads rocprofv3 outputs: trace view and calibrated PMC means."""
+    import sqlite3
+    from mimansm1_v1_amd import profsum
+    db = tmp_path / "t.db"
+    con = sqlite3.connect(db)
+    con.execute("create table top_kernels (name, total_calls, total_duration, average, percentage)")
+    con.execute("insert into top_kernels values ('void mm1::attn_fwd_kernel<4, 2, true>(int)', 3, 30.0, 10.0, 100.0)")
+    con.commit()
+    con.close()
+    hdr = "Kernel_Name,Counter_Name,Counter_Value\n"
+    (tmp_path / "f.csv").write_text(hdr + '"void mm1::attn_fwd_kernel<4, 2, true>(int)",FETCH_SIZE,10\n'
+                                    '"void mm1::attn_fwd_kernel<4, 2, true>(int)",FETCH_SIZE,30\n')
+    (tmp_path / "w.csv").write_text(hdr + '"void mm1::attn_fwd_kernel<4, 2, true>(int)",WRITE_SIZE,4\n')
+    (tmp_path / "cf.csv").write_text(hdr + '"copyBuffer",FETCH_SIZE,512\n"copyBuffer",FETCH_SIZE,2\n')
+    (tmp_path / "cw.csv").write_text(hdr + '"copyBuffer",WRITE_SIZE,1024\n')
+    out = tmp_path / "traffic.json"
+    profsum.main(["--trace", str(db), "--fetch", str(tmp_path / "f.csv"), "--write", str(tmp_path / "w.csv"),
+                  "--copy-fetch", str(tmp_path / "cf.csv"), "--copy-write", str(tmp_path / "cw.csv"),
+                  "--copy-bytes", str(1 << 20), "--json", str(out)])
+    text = capsys.readouterr().out
+    assert "attn_fwd_kernel<4, 2, true>" in text and "| 3 | 10.0 |" in text
+    # mean fetch 20 KiB x 2 (copy read 512 KiB for 1 MiB) + 4 KiB writes x 1
+    assert json.loads(out.read_text())["fwd"] == (20 * 2 + 4) * 1024
