@@ -7,7 +7,7 @@ A step is one forward + backward of the attention op over one batch of the
 BASELINE.json workload (default config 3: batch 2, seq 8192, 10 query heads,
 2 KV heads, head_dim 128, causal, bf16, synthetic N(0,1) inputs resident in
 HBM).  The step runs exactly the kernels ``FlashAttention`` runs -- forward,
-Delta, dK/dV, dK/dV group reduce, dQ -- through the library's C ABI, with HIP
+Delta, dK/dV, dQ with the dK/dV group sum in its tail -- through the library's C ABI, with HIP
 events between them on the launch stream so every kernel's average duration
 is measured live over the timed region.
 
@@ -86,7 +86,7 @@ class Workload:
         self.scale = DIM ** -0.5
         self.stream = torch.cuda.current_stream(device)
 
-    STAGES = ("fwd", "delta", "dkdv", "reduce", "dq")
+    STAGES = ("fwd", "delta", "dkdv", "dq")
 
     def step(self, marks=None):
         """One fwd+bwd; if `marks` is given, records an event after each stage."""
@@ -109,14 +109,14 @@ class Workload:
                                 B, S, H, Hkv, D, 1, self.scale, sp), "dkdv")
         if marks is not None:
             marks[2].record(self.stream)
-        chk(L.mm1_attn_bwd_dkdv_reduce(p(self.ws), self.ws_bytes, p(self.dk), p(self.dv),
-                                       B, S, H, Hkv, D, sp), "reduce")
+        # dQ, with the dK/dV group sum folded into the same launch (what
+        # mm1_attn_bwd runs after mm1_attn_bwd_dkdv)
+        chk(L.mm1_attn_bwd_dq_reduce(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
+                                     p(self.delta), p(self.dq), p(self.dk), p(self.dv),
+                                     p(self.ws), self.ws_bytes, B, S, H, Hkv, D, 1, self.scale, sp),
+            "dq")
         if marks is not None:
             marks[3].record(self.stream)
-        chk(L.mm1_attn_bwd_dq(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
-                              p(self.delta), p(self.dq), B, S, H, Hkv, D, 1, self.scale, sp), "dq")
-        if marks is not None:
-            marks[4].record(self.stream)
 
 
 def time_workload(wl, steps, warmup):

@@ -68,14 +68,19 @@ int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                  void* stream);
 
-/* The three stages mm1_attn_bwd runs, in order, for callers that schedule or
- * time them separately (same arguments and checks as mm1_attn_bwd).
+/* The stages of the backward, for callers that schedule or time them
+ * separately (same arguments and checks as mm1_attn_bwd).  mm1_attn_bwd runs
+ * mm1_attn_bwd_dkdv then mm1_attn_bwd_dq_reduce; mm1_attn_bwd_dkdv_reduce
+ * followed by mm1_attn_bwd_dq is the same result in two launches.
  *  - mm1_attn_bwd_dkdv: dK/dV.  With H == Hkv it writes bf16 dk, dv directly;
  *    otherwise it writes the per-query-head fp32 partial sums into `workspace`
  *    ([2][G][B][S][Hkv][D], G = H / Hkv) and leaves dk/dv untouched.
  *  - mm1_attn_bwd_dkdv_reduce: sums the G partials of each KV head and writes
  *    bf16 dk, dv (no-op when H == Hkv).
  *  - mm1_attn_bwd_dq: bf16 dq.
+ *  - mm1_attn_bwd_dq_reduce: bf16 dq, and the group sum of
+ *    mm1_attn_bwd_dkdv_reduce done by the tail of the same launch (must run
+ *    after mm1_attn_bwd_dkdv on the same stream).
  * Together they replace flash_bwd + flash_unswizzle + casts
  * (attention_tilelang.py:242-323, :385-389); no counterpart as separate calls. */
 int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
@@ -89,6 +94,11 @@ int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                     const float* lse2, const float* delta, void* dq,
                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                     void* stream);
+int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const void* dO,
+                           const float* lse2, const float* delta, void* dq, void* dk, void* dv,
+                           const void* workspace, size_t workspace_bytes,
+                           int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                           void* stream);
 
 /* Static description of a return code. */
 const char* mm1_attn_strerror(int code);

@@ -577,12 +577,11 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   }
 }
 
-// Sum the G per-head partials of dK and dV and round to bf16 once.
-__global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(
-    const float* __restrict__ ws_dk, const float* __restrict__ ws_dv,
-    __bf16* __restrict__ dk, __bf16* __restrict__ dv, long n, int G) {
-  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i >= n) return;
+// Sum the G per-head partials of dK and dV (workspace [G][n]) at element i
+// .. i+3 and round to bf16 once; the sum runs in head order, so the result
+// does not depend on which thread or kernel does it.
+__device__ __forceinline__ void reduce4(const float* __restrict__ ws_dk, const float* __restrict__ ws_dv,
+                                        __bf16* __restrict__ dk, __bf16* __restrict__ dv, long n, int G, long i) {
   f32x4 sk = *reinterpret_cast<const f32x4*>(ws_dk + i);
   f32x4 sv = *reinterpret_cast<const f32x4*>(ws_dv + i);
   for (int j = 1; j < G; ++j) {
@@ -596,6 +595,28 @@ __global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(
   *reinterpret_cast<bf16x4*>(dv + i) = ov;
 }
 
+__global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(
+    const float* __restrict__ ws_dk, const float* __restrict__ ws_dv,
+    __bf16* __restrict__ dk, __bf16* __restrict__ dv, long n, int G) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  reduce4(ws_dk, ws_dv, dk, dv, n, G, i);
+}
+
+// Where the dQ kernel folds the dK/dV group sum in: the last n_red workgroups
+// of its grid each reduce one contiguous slice of the n elements after their
+// own work (with n_red = the grid size, a small slice per workgroup, spread
+// over the whole launch).
+struct TailReduce {
+  const float* ws_dk;
+  const float* ws_dv;
+  __bf16* dk;
+  __bf16* dv;
+  long n;
+  int G;
+  int n_red;   // 0: no reduction in this launch
+};
+
 // ---------------------------------------------------------------------------
 // dQ: one workgroup per NW*32 packed query rows (32 per wave); K and V tiles
 // of 64 keys arrive by LDS DMA (row-major) in an NSTAGE-deep ring; K^T for
@@ -605,7 +626,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     __bf16* __restrict__ dq,
-    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles) {
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles, TailReduce red) {
   constexpr int BM = NW * 32;
   constexpr int BN = TILE_ROWS;
   constexpr int BUF = 2 * TILE_BYTES;   // K, V
@@ -733,17 +754,27 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     }
   }
 
-  if (!row_valid) return;
-  __bf16* dst = dq + roff;
+  if (row_valid) {
+    __bf16* dst = dq + roff;
 #pragma unroll
-  for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
-    for (int a4 = 0; a4 < 4; ++a4) {
-      bf16x4 val;
+      for (int a4 = 0; a4 < 4; ++a4) {
+        bf16x4 val;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) val[c] = (__bf16)(dqacc[db][4 * a4 + c] * sm_scale);
-      *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * a4 + 4 * h) = val;
+        for (int c = 0; c < 4; ++c) val[c] = (__bf16)(dqacc[db][4 * a4 + c] * sm_scale);
+        *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * a4 + 4 * h) = val;
+      }
     }
+  }
+
+  // dK/dV group sum slice (the partials were completed by an earlier launch)
+  const int slice = (int)blockIdx.x - ((int)gridDim.x - red.n_red);
+  if (slice >= 0) {
+    const long per = ((red.n + red.n_red - 1) / red.n_red + 3) & ~3L;
+    const long end = min(red.n, per * (slice + 1));
+    for (long i = per * slice + 4L * tid; i < end; i += 4L * NW * 64)
+      reduce4(red.ws_dk, red.ws_dv, red.dk, red.dv, red.n, red.G, i);
   }
 }
 
@@ -812,23 +843,29 @@ hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, i
 template <int NW, int NSTAGE>
 static void launch_dq_t(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* dO,
                         const float* lse2, const float* delta, __bf16* dq, int B, int S, int H,
-                        int Hkv, bool causal, float scale2, float sm_scale, hipStream_t stream) {
+                        int Hkv, bool causal, float scale2, float sm_scale, TailReduce red,
+                        hipStream_t stream) {
   const int G = H / Hkv;
   const int BM = NW * 32;
   const int n_qtiles = (G * S + BM - 1) / BM;
-  dim3 grid(n_qtiles * B * Hkv), block(NW * 64);
+  const int n_blocks = n_qtiles * B * Hkv;
+  if (red.n_red > 0) red.n_red = min(red.n_red, n_blocks);
+  dim3 grid(n_blocks), block(NW * 64);
   if (causal)
     hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, true>), grid, block, 0, stream, q, k, v, dO, lse2, delta, dq,
-                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles);
+                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red);
   else
     hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, false>), grid, block, 0, stream, q, k, v, dO, lse2, delta, dq,
-                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles);
+                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red);
 }
 
 // variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
 //          1 = 8 waves x 3-stage ring (one workgroup per CU).
+// workspace != nullptr: also sum the G dK/dV partials it holds into dk, dv
+// (what launch_bwd_reduce does), in the dQ grid's tail.
 hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                          const float* lse2, const float* delta, void* dq,
+                         const void* workspace, void* dk, void* dv,
                          int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                          hipStream_t stream) {
   const float scale2 = sm_scale * 1.4426950408889634f;
@@ -837,10 +874,20 @@ hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void
   auto vp = static_cast<const __bf16*>(v);
   auto dop = static_cast<const __bf16*>(dO);
   auto dqp = static_cast<__bf16*>(dq);
+  const int G = H / Hkv;
+  TailReduce red{nullptr, nullptr, nullptr, nullptr, 0, G, 0};
+  if (workspace && G > 1) {
+    red.n = (long)B * S * Hkv * HD;
+    red.ws_dk = static_cast<const float*>(workspace);
+    red.ws_dv = red.ws_dk + (long)G * red.n;
+    red.dk = static_cast<__bf16*>(dk);
+    red.dv = static_cast<__bf16*>(dv);
+    red.n_red = 1 << 30;   // every workgroup of the grid takes a slice
+  }
   if (variant == 1)
-    launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, stream);
+    launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, stream);
   else
-    launch_dq_t<4, 2>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, stream);
+    launch_dq_t<4, 2>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, stream);
   return hipGetLastError();
 }
 

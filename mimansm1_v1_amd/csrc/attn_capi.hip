@@ -21,6 +21,7 @@ hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, i
                              hipStream_t stream);
 hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                          const float* lse2, const float* delta, void* dq,
+                         const void* workspace, void* dk, void* dv,
                          int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                          hipStream_t stream);
 }  // namespace mm1
@@ -40,24 +41,16 @@ int check_shape(int B, int S, int H, int Hkv, int D) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Kernel variants (see launch_fwd / launch_bwd_dkdv / launch_bwd_dq).
-// MM1_FWD_VARIANT, MM1_DKDV_VARIANT and MM1_DQ_VARIANT override the defaults
-// for tile experiments.
-int env_variant(const char* name, int dflt) {
+// MM1_FWD_VARIANT, MM1_DKDV_VARIANT and MM1_DQ_VARIANT select alternative
+// tilings with the same results (tuning, tests); read on every call, so a
+// process can switch between launches.
+int env_variant(const char* name) {
   const char* e = getenv(name);
-  return e ? atoi(e) : dflt;
+  return e ? atoi(e) : 0;
 }
-int fwd_variant() {
-  static const int v = env_variant("MM1_FWD_VARIANT", 0);
-  return v;
-}
-int dq_variant() {
-  static const int v = env_variant("MM1_DQ_VARIANT", 0);
-  return v;
-}
-int dkdv_variant() {
-  static const int v = env_variant("MM1_DKDV_VARIANT", 0);
-  return v;
-}
+int fwd_variant() { return env_variant("MM1_FWD_VARIANT"); }
+int dq_variant() { return env_variant("MM1_DQ_VARIANT"); }
+int dkdv_variant() { return env_variant("MM1_DKDV_VARIANT"); }
 
 int from_hip(hipError_t e) { return e == hipSuccess ? MM1_OK : static_cast<int>(e); }
 
@@ -135,8 +128,28 @@ int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq))
     return MM1_E_ALIGN;
-  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, B, S, H, Hkv, causal != 0,
-                                     sm_scale, dq_variant(), static_cast<hipStream_t>(stream)));
+  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, nullptr, nullptr, nullptr,
+                                     B, S, H, Hkv, causal != 0, sm_scale, dq_variant(),
+                                     static_cast<hipStream_t>(stream)));
+}
+
+int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const void* dO,
+                           const float* lse2, const float* delta, void* dq, void* dk, void* dv,
+                           const void* workspace, size_t workspace_bytes,
+                           int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                           void* stream) {
+  if (!q || !k || !v || !dO || !lse2 || !delta || !dq || !dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
+  const size_t need = mm1::bwd_workspace_bytes(B, S, H, Hkv);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return MM1_E_WORKSPACE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) ||
+      !aligned16(dk) || !aligned16(dv) || (need > 0 && !aligned16(workspace)))
+    return MM1_E_ALIGN;
+  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, need > 0 ? workspace : nullptr,
+                                     dk, dv, B, S, H, Hkv, causal != 0, sm_scale, dq_variant(),
+                                     static_cast<hipStream_t>(stream)));
 }
 
 int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
@@ -149,9 +162,8 @@ int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
   int rc = mm1_attn_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes,
                              B, S, H, Hkv, D, causal, sm_scale, stream);
   if (rc) return rc;
-  rc = mm1_attn_bwd_dkdv_reduce(workspace, workspace_bytes, dk, dv, B, S, H, Hkv, D, stream);
-  if (rc) return rc;
-  return mm1_attn_bwd_dq(q, k, v, dO, lse2, delta, dq, B, S, H, Hkv, D, causal, sm_scale, stream);
+  return mm1_attn_bwd_dq_reduce(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes,
+                                B, S, H, Hkv, D, causal, sm_scale, stream);
 }
 
 const char* mm1_attn_strerror(int code) {

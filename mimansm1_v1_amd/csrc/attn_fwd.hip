@@ -199,6 +199,219 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   }
 }
 
+// Ping-pong forward: one workgroup of 8 waves per CU over 256 packed query
+// rows.  Group A (waves 0-3) owns rows 0-127, group B (waves 4-7) rows
+// 128-255, and the waves of the two groups pair up on the four SIMDs.  The
+// work on a 64-key tile is split into
+//   part 1: S^T = K Q^T, row max, lazy rescale, P = exp2(..), row sums;
+//   part 2: O^T += V^T P^T,
+// and group B runs half a tile behind group A, so in every phase (one
+// barrier each) one wave of a SIMD runs part 1 while the other runs part 2:
+// the SIMD sees 16 products from each wave, and the softmax VALU work of one
+// wave runs under the other wave's products.
+//   phase 2t  : A part 1 of tile t,  B part 2 of tile t-1
+//   phase 2t+1: A part 2 of tile t,  B part 1 of tile t
+// K(t) is read in phases 2t and 2t+1, V(t) in 2t+1 and 2t+2.  Two-slot rings
+// for each: the group running part 2 issues the copies of the phase (B
+// refills K(t+2) in phase 2t+2, A refills V(t+2) in phase 2t+3) and waits for
+// them at the end of the next phase, two phases ahead of their first use.
+template <bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    __bf16* __restrict__ o, float* __restrict__ lse2,
+    int B, int S, int H, int Hkv, int G, float scale2, int n_tiles) {
+  constexpr int BM = 256;         // packed rows per workgroup
+  constexpr int BN = TILE_ROWS;   // keys per tile
+  __shared__ __attribute__((aligned(1024))) char smem[4 * TILE_BYTES];   // K slots 0, 1; V slots 0, 1
+
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
+  const int grp = w >> 2;                                    // 0 = A, 1 = B
+  const int nbg = B * Hkv;
+  int tile = blockIdx.x / nbg;
+  if (CAUSAL) tile = n_tiles - 1 - tile;   // longest rows first
+  const int bg = blockIdx.x % nbg;
+  const int b = bg / Hkv, g = bg % Hkv;
+  const int R = G * S;
+  const int r0 = tile * BM;
+  const int rw0 = r0 + w * 32;
+  const bool wave_active = rw0 < R;
+
+  const int last_row_wg = min(r0 + BM, R) - 1;
+  const int n_kt = CAUSAL ? (min(S - 1, last_row_wg / G) / BN + 1) : (S + BN - 1) / BN;
+  const int pw_lo = rw0 / G;
+
+  const long kvstride = (long)Hkv * HD;
+  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
+  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
+  const uint32_t dma_off = tile_lane_off(kvstride, tid);
+  auto kslot = [&](int j) { return smem + j * TILE_BYTES; };
+  auto vslot = [&](int j) { return smem + (2 + j) * TILE_BYTES; };
+  // all 8 waves (prologue) or the 4 waves of one group (in the loop; the
+  // quad a wave copies depends on w & 3 only, as tile_dma<4> requires)
+  auto copy8 = [&](char* dst, const __bf16* base, int kt) {
+    const int nk = kt * BN;
+    tile_dma<8>(dst, base + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
+  };
+  auto copy4 = [&](char* dst, const __bf16* base, int kt) {
+    const int nk = kt * BN;
+    tile_dma<4>(dst, base + (long)nk * kvstride, kvstride, S - nk, dma_off, tid & 255);
+  };
+  copy8(kslot(0), kbase, 0);
+  copy8(vslot(0), vbase, 0);
+  if (n_kt > 1) {
+    copy8(kslot(1), kbase, 1);
+    copy8(vslot(1), vbase, 1);
+  }
+
+  // Query operands (B of S^T = K Q^T), loaded once.
+  bf16x8 qreg[8];
+  const int rr = rw0 + l32;
+  const int qpos = rr / G;
+  const int hq = rr - qpos * G;
+  if (rr < R) {
+    const __bf16* src = q + ((long)(b * S + qpos) * H + g * G + hq) * HD + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) pin(qreg[ks]);
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) qreg[ks][t] = (__bf16)0.f;
+    }
+  }
+
+  f32x16 oacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) oacc[db] = zero16();
+  float m_run = -INFINITY, l_run = 0.f;
+  bf16x8 pb[4];   // P(t) of part 1, the B operand of part 2
+  const LdsBases lb = make_lds_bases(lane);
+  wait_dma();
+  __syncthreads();
+
+  // part 1 of tile kt from K slot J
+  auto part1 = [&](auto jslot, int kt) {
+    constexpr int J = decltype(jslot)::value;
+    const char* kl = kslot(J);
+    const int k0 = kt * BN;
+    f32x16 sacc[2];
+    sacc[0] = zero16();
+    sacc[1] = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) sacc[jb] = mfma32(rows_a(kl, lb, jb, ks), qreg[ks], sacc[jb]);
+    }
+    if (CAUSAL ? (k0 + BN - 1 > pw_lo) : (k0 + BN > S)) {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 32 * jb + 8 * (r >> 2) + 4 * h + (r & 3);
+          sacc[jb][r] = (CAUSAL ? (key > qpos) : (key >= S)) ? -INFINITY : sacc[jb][r];
+        }
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[jb][r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    if (__any(!((m_new - m_run) * scale2 <= kRescaleThreshold))) {
+      const float alpha = (m_new == -INFINITY) ? 1.f : exp2_fast((m_run - m_new) * scale2);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+      m_run = m_new;
+    }
+    const float ms = (m_run == -INFINITY) ? 0.f : m_run * scale2;
+    float sum = 0.f;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = exp2_fast(fmaf(sacc[jb][r], scale2, -ms));
+        sacc[jb][r] = pr;
+        sum += pr;
+      }
+    }
+    l_run += sum;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) pb[ks] = pack8(sacc[ks >> 1], 8 * (ks & 1));
+  };
+  // part 2 of a tile from V slot J
+  auto part2 = [&](auto jslot) {
+    constexpr int J = decltype(jslot)::value;
+    const char* vl = vslot(J);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] = mfma32(tr_a(vl, lb, db, ks), pb[ks], oacc[db]);
+    }
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  if (grp == 0) {
+    // phase 2t: part 1 (t); phase 2t+1: part 2 (t), refill V(t+1) when t >= 1
+    // (V(0), V(1) come from the prologue); the refill is waited for at the
+    // end of phase 2t+2.
+    auto tile_a = [&](auto jslot, int t) {
+      part1(jslot, t);
+      if (t >= 2) wait_dma();          // V(t) refilled in phase 2t-1
+      lds_barrier();
+      if (t >= 1 && t + 1 < n_kt) copy4(vslot(decltype(jslot)::value ^ 1), vbase, t + 1);
+      part2(jslot);
+      lds_barrier();
+    };
+    for (int t = 0; t < n_kt; t += 2) {
+      tile_a(I0{}, t);
+      if (t + 1 < n_kt) tile_a(I1{}, t + 1);
+    }
+  } else {
+    // phase 2t+1: part 1 (t); phase 2t+2: part 2 (t), refill K(t+2) (its slot
+    // was last read in phase 2t+1), waited for at the end of phase 2t+3.
+    lds_barrier();   // phase 0
+    auto tile_b = [&](auto jslot, int t) {
+      part1(jslot, t);
+      if (t >= 1) wait_dma();          // K(t+1) refilled in phase 2t
+      lds_barrier();
+      if (t + 2 < n_kt) copy4(kslot(decltype(jslot)::value), kbase, t + 2);
+      part2(jslot);
+      if (t + 1 < n_kt) lds_barrier();
+    };
+    for (int t = 0; t < n_kt; t += 2) {
+      tile_b(I0{}, t);
+      if (t + 1 < n_kt) tile_b(I1{}, t + 1);
+    }
+  }
+  wait_dma();
+
+  if (!wave_active) return;
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.f / l_tot;
+  if (rr < R) {
+    __bf16* dst = o + ((long)(b * S + qpos) * H + g * G + hq) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        bf16x4 val;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) val[c] = (__bf16)(oacc[db][4 * a4 + c] * inv);
+        *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * a4 + 4 * h) = val;
+      }
+    }
+    if (h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
+  }
+}
+
 template <int NW, int NSTAGE>
 static void launch_fwd_t(const __bf16* q, const __bf16* k, const __bf16* v, __bf16* o, float* lse2,
                          int B, int S, int H, int Hkv, bool causal, float scale2, hipStream_t stream) {
@@ -213,7 +426,8 @@ static void launch_fwd_t(const __bf16* q, const __bf16* k, const __bf16* v, __bf
 }
 
 // variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
-//          1 = 8 waves x 3-stage ring (one workgroup per CU).
+//          1 = 8 waves x 3-stage ring (one workgroup per CU),
+//          2 = attn_fwd_pp_kernel (8 waves, two groups half a tile apart).
 hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
                       int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                       hipStream_t stream) {
@@ -222,7 +436,15 @@ hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, floa
   auto kp = static_cast<const __bf16*>(k);
   auto vp = static_cast<const __bf16*>(v);
   auto op = static_cast<__bf16*>(o);
-  if (variant == 1)
+  if (variant == 2) {
+    const int G = H / Hkv;
+    const int n_tiles = (G * S + 255) / 256;
+    dim3 grid(n_tiles * B * Hkv), block(512);
+    if (causal)
+      hipLaunchKernelGGL(attn_fwd_pp_kernel<true>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles);
+    else
+      hipLaunchKernelGGL(attn_fwd_pp_kernel<false>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles);
+  } else if (variant == 1)
     launch_fwd_t<8, 3>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, stream);
   else
     launch_fwd_t<4, 2>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, stream);

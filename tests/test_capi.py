@@ -97,6 +97,12 @@ def test_bwd_argument_errors(lib):
     assert bwd(ws=FAKE + 4) == -6
     assert lib.mm1_attn_bwd_dq(FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE,
                                1, 64, 10, 2, 128, 1, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE,
+                                      FAKE, need, 2, 100, 10, 2, 128, 1, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                      None, 0, 2, 100, 10, 2, 128, 1, 0.1, None) == -4
+    assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                      FAKE + 4, need, 2, 100, 10, 2, 128, 1, 0.1, None) == -6
     assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 10, 2, 128, None) == -4
     # nothing to reduce without groups: success without a device call
     assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 4, 4, 128, None) == 0

@@ -71,6 +71,28 @@ def test_small_shapes_vs_cpu_oracle(hip_device, shape, causal):
     assert_bf16_close("dV", dv, wv, log)
 
 
+VARIANTS = [("MM1_FWD_VARIANT", 1), ("MM1_FWD_VARIANT", 2), ("MM1_DKDV_VARIANT", 1),
+            ("MM1_DQ_VARIANT", 1)]
+
+
+@pytest.mark.parametrize("env,variant", VARIANTS, ids=[f"{e}={v}" for e, v in VARIANTS])
+def test_kernel_variants_vs_cpu_oracle(hip_device, monkeypatch, env, variant):
+    """The alternative tilings (selected per call by environment variable)
+    meet the same gates as the defaults, causal and full, ragged S."""
+    monkeypatch.setenv(env, str(variant))
+    for (B, S, H, Hkv), causal in [((2, 300, 10, 2), True), ((1, 200, 6, 3), False), ((1, 77, 4, 4), True)]:
+        G = H // Hkv
+        log(f"[case] {env}={variant} B={B} S={S} H={H} Hkv={Hkv} causal={causal}")
+        q, k, v, do = R.make_inputs(B, S, H, Hkv, 128, seed=3 * S + H)
+        o, lse, dq, dk, dv = hip_run(q, k, v, do, causal, G, hip_device)
+        wq, wk, wv = R.grads(q, k, v, do, causal, G)
+        assert_bf16_close("O", o, R.attention(q, k, v, causal, G, cast=False), log)
+        assert_lse_close(lse, R.lse2(q, k, causal, G), log)
+        assert_bf16_close("dQ", dq, wq, log)
+        assert_bf16_close("dK", dk, wk, log)
+        assert_bf16_close("dV", dv, wv, log)
+
+
 def test_config1_forward_vs_cpu_oracle(hip_device):
     log("[case] config 1: B1 S512 fwd")
     q, k, v, _ = R.config_inputs(1)
@@ -118,6 +140,46 @@ def test_backward_deterministic(hip_device):
     b = hip_run(q, k, v, do, True, 5, hip_device)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("shape", [(2, 1000, 10, 2, True), (1, 333, 6, 3, False), (1, 256, 4, 4, True)],
+                         ids=["B2S1000G5causal", "B1S333G2full", "B1S256G1causal"])
+def test_backward_stages_match_combined(hip_device, shape):
+    """mm1_attn_bwd (dK/dV, then dQ with the group sum in its tail) and the
+    separate stages (dK/dV, group sum, dQ) write bitwise-identical gradients."""
+    from mimansm1_v1_amd import _lib
+    B, S, H, Hkv, causal = shape
+    log(f"[case] stages vs combined {shape}")
+    lib = _lib.load()
+    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=9))
+    scale = 128 ** -0.5
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, dtype=torch.float32, device=hip_device)
+    delta = torch.empty_like(lse)
+    sp = torch.cuda.current_stream(hip_device).cuda_stream
+    p = lambda t: t.data_ptr()
+    assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), B, S, H, Hkv, 128, int(causal), scale, sp) == 0
+    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+    nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
+    ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=hip_device)
+    outs = []
+    for combined in (True, False):
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        args = (B, S, H, Hkv, 128, int(causal), scale, sp)
+        if combined:
+            rc = lib.mm1_attn_bwd(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk), p(dv),
+                                  p(ws), nws, *args)
+            assert rc == 0
+        else:
+            assert lib.mm1_attn_bwd_dkdv(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dk), p(dv),
+                                         p(ws), nws, *args) == 0
+            assert lib.mm1_attn_bwd_dkdv_reduce(p(ws), nws, p(dk), p(dv), B, S, H, Hkv, 128, sp) == 0
+            assert lib.mm1_attn_bwd_dq(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), *args) == 0
+        torch.cuda.synchronize()
+        outs.append((dq.cpu(), dk.cpu(), dv.cpu()))
+    for name, x, y in zip(("dq", "dk", "dv"), *outs):
+        assert torch.equal(x, y), name
+        assert torch.isfinite(x.float()).all(), name
 
 
 def test_lse_lower_bound_and_rows_sum(hip_device):
