@@ -38,6 +38,7 @@ CONFIGS = {
     4: dict(batch=4, seq=4096),
 }
 HEADS, KV_HEADS, DIM = 10, 2, 128
+SUBLAYER_CONFIG = 5           # the attention sublayer, reported beside
 
 
 def gemm_unit(batch, seq, heads=HEADS, dim=DIM, causal=True):
@@ -51,8 +52,8 @@ def parse(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
-    ap.add_argument("--also", type=int, nargs="*", default=[2],
-                    help="extra configs reported beside the main one")
+    ap.add_argument("--also", type=int, nargs="*", default=[2, 5],
+                    help="extra configs reported beside the main one (5 = the attention sublayer)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-autograd", action="store_true", help="skip the autograd cross-check")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -170,6 +171,120 @@ def time_autograd(batch, seq, device, steps, warmup):
     return t0.elapsed_time(t1) / steps
 
 
+def _timed(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def time_sublayer(batch, seq, device, steps, warmup):
+    """the attention sublayer (d_model 1280, fused QKV
+    projection, QK-norm + RoPE, causal flash attention, wo) forward + backward
+    under bf16 autocast, x ~ N(0,1), weights ~ N(0, 0.02^2).  Besides the whole
+    step, its parts are timed on the same tensors: the attention kernels (fwd +
+    bwd), the hipBLASLt GEMMs (QKV and wo, fwd + both backward products) and the
+    QK-norm + RoPE kernels (fwd + bwd)."""
+    import torch
+    import torch.nn.functional as F
+    from mimansm1_v1_amd import attention as A
+    gen = torch.Generator().manual_seed(0)
+    cfg = A.AttnConfig(max_seq_len=seq)
+    mod = A.Attention(cfg, A.Rotary(cfg.head_dim, seq, cfg.rope_theta))
+    with torch.no_grad():
+        for lin in (mod.wq, mod.wk, mod.wv, mod.wo):
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=gen) * 0.02)
+    mod = mod.to(device)
+    x = torch.randn(batch, seq, cfg.d_model, generator=gen).to(device).requires_grad_(True)
+    dy = torch.randn(batch, seq, cfg.d_model, generator=gen).to(torch.bfloat16).to(device)
+    ac = lambda: torch.autocast("cuda", dtype=torch.bfloat16)
+
+    def full():
+        with ac():
+            y = mod(x)
+        y.backward(dy)
+        x.grad = None
+        mod.zero_grad(set_to_none=True)
+
+    ms_full = _timed(full, steps, warmup)
+    # parts, on tensors of the same shapes and values
+    w_cat = torch.cat((mod.wq.weight, mod.wk.weight, mod.wv.weight), 0).detach().requires_grad_(True)
+    wo = mod.wo.weight.detach().requires_grad_(True)
+    with torch.no_grad(), ac():
+        qkv = F.linear(x, w_cat).contiguous()
+    qkv.requires_grad_(True)
+    qn, kn = (m.weight.detach().requires_grad_(True) for m in (mod.q_norm, mod.k_norm))
+    with torch.no_grad():
+        q, k, v = A.qknorm_rope(qkv, qn, kn, mod.rope.cos, mod.rope.sin, cfg.n_heads, cfg.n_kv_heads,
+                                cfg.norm_eps)
+    g = [torch.randn(t.shape, generator=gen).to(torch.bfloat16).to(device) for t in (q, k, v)]
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    o = torch.randn(batch, seq, cfg.d_model, generator=gen).to(torch.bfloat16).to(device).requires_grad_(True)
+    dqkv = torch.randn(qkv.shape, generator=gen).to(torch.bfloat16).to(device)
+
+    def attention():
+        A.flash_attention(q, k, v, True, cfg.groups).backward(g[0])
+        q.grad = k.grad = v.grad = None
+
+    # the QK-norm + RoPE kernels through the C ABI on preallocated buffers (the
+    # autograd wrapper's allocations would otherwise time the host, not the GPU)
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    qo, ko, vo = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dqkv_o = torch.empty_like(qkv)
+    dwq, dwk = torch.empty(cfg.head_dim, device=device), torch.empty(cfg.head_dim, device=device)
+    ws_bytes = lib.mm1_qknorm_rope_bwd_workspace_size()
+    ws = torch.empty(ws_bytes // 4, device=device)
+    qnf, knf = qn.detach().float().contiguous(), kn.detach().float().contiguous()
+    cos_t, sin_t = mod.rope.cos, mod.rope.sin
+    sp = torch.cuda.current_stream(device).cuda_stream
+    H, Hkv, D, rot = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cos_t.shape[0]
+
+    def norm_rope():
+        _lib.check(lib.mm1_qknorm_rope_fwd(qkv.data_ptr(), qnf.data_ptr(), knf.data_ptr(), cos_t.data_ptr(),
+                                           sin_t.data_ptr(), qo.data_ptr(), ko.data_ptr(), vo.data_ptr(),
+                                           batch, seq, H, Hkv, D, rot, cfg.norm_eps, sp), "qknorm fwd")
+        _lib.check(lib.mm1_qknorm_rope_bwd(qkv.data_ptr(), qnf.data_ptr(), knf.data_ptr(), cos_t.data_ptr(),
+                                           sin_t.data_ptr(), g[0].data_ptr(), g[1].data_ptr(), g[2].data_ptr(),
+                                           dqkv_o.data_ptr(), dwq.data_ptr(), dwk.data_ptr(), ws.data_ptr(),
+                                           ws_bytes, batch, seq, H, Hkv, D, rot, cfg.norm_eps, sp), "qknorm bwd")
+
+    def gemms():
+        with ac():
+            a = F.linear(x, w_cat)
+            b = F.linear(o, wo)
+        torch.autograd.backward((a, b), (dqkv, dy))
+        x.grad = w_cat.grad = o.grad = wo.grad = None
+
+    parts = {"attention": _timed(attention, steps, warmup), "gemm": _timed(gemms, steps, warmup),
+             "qknorm_rope": _timed(norm_rope, steps, warmup)}
+    tokens = batch * seq
+    gemm_flops = 6.0 * tokens * cfg.d_model * (cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim \
+        + 6.0 * tokens * cfg.d_model * cfg.d_model
+    attn_flops = 7 * gemm_unit(batch, seq)
+    return {
+        "batch": batch, "seq_len": seq, "d_model": cfg.d_model,
+        "ms_per_step": round(ms_full, 4),
+        "tflops": round((attn_flops + gemm_flops) / (ms_full * 1e-3) / 1e12, 2),
+        "part_ms": {k: round(v, 4) for k, v in parts.items()},
+        "other_ms": round(ms_full - sum(parts.values()), 4),
+        "attention_tflops": round(attn_flops / (parts["attention"] * 1e-3) / 1e12, 2),
+        "gemm_tflops": round(gemm_flops / (parts["gemm"] * 1e-3) / 1e12, 2),
+        "flops": {"attention": attn_flops, "gemm": gemm_flops},
+        "note": "bf16 autocast; attention = flash_attention fwd+bwd kernels, gemm = QKV (1280->1792) and "
+                "wo (1280->1280) fwd + dX + dW via torch (hipBLASLt), qknorm_rope = fwd+bwd kernels; "
+                "other = casts, weight concatenation and autograd bookkeeping of the whole step",
+    }
+
+
 def cpu_baseline(seq):
     """fp32 reference math (oracle restatement of AT:521-530, autograd backward)
     on one KV group (5 query heads, 1 KV head) of one batch element, full seq."""
@@ -238,6 +353,13 @@ def main(argv=None):
 
     results = {}
     for cfg in [args.config] + [c for c in args.also if c != args.config]:
+        if cfg == SUBLAYER_CONFIG:
+            res = time_sublayer(2, 8192, device, args.steps, args.warmup)
+            results[cfg] = res
+            torch.cuda.empty_cache()
+            print(f"[bench] config 5 (sublayer): {res['ms_per_step']:.3f} ms/step, {res['tflops']:.1f} TFLOP/s, "
+                  f"parts {res['part_ms']}, other {res['other_ms']:.3f}", file=sys.stderr, flush=True)
+            continue
         B, S = CONFIGS[cfg]["batch"], CONFIGS[cfg]["seq"]
         wl = Workload(lib, B, S, device)
         ms, stages = time_workload(wl, args.steps, args.warmup)
@@ -314,6 +436,9 @@ def main(argv=None):
         out["ms_per_step_autograd"] = round(main_res["ms_per_step_autograd"], 4)
     for cfg, res in results.items():
         if cfg == args.config:
+            continue
+        if cfg == SUBLAYER_CONFIG:
+            out["config5"] = res
             continue
         out[f"config{cfg}"] = {
             "batch": CONFIGS[cfg]["batch"], "seq_len": CONFIGS[cfg]["seq"],

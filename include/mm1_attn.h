@@ -100,6 +100,31 @@ int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const vo
                            int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                            void* stream);
 
+/* QK-RMSNorm + RoPE between the fused QKV projection and the attention
+ * kernel.  Replaces, in Attention.forward (attention_tilelang.py:483-487), the
+ * views of wq/wk/wv outputs, q_norm/k_norm (RMSNorm.forward, :423-428) and
+ * apply_rope (:458-461) on Q and K, plus the .contiguous() copies (:492-493).
+ *  - qkv: [B, S, (H + 2*Hkv) * D] bf16, columns = wq | wk | wv outputs;
+ *  - wq, wk: the norm weights [D] fp32, or both NULL for qk_norm = False;
+ *  - cos_t, sin_t: the Rotary tables [rot_len, D] fp32 (rot_len >= S);
+ *  - q [B,S,H,D], k, v [B,S,Hkv,D] bf16 out (v is the copied value slice).
+ * Numerics: the norm in fp32 rounded to bf16, the rotation in bf16 steps, as
+ * the reference under bf16. */
+int mm1_qknorm_rope_fwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
+                        const float* sin_t, void* q, void* k, void* v,
+                        int B, int S, int H, int Hkv, int D, int rot_len, float eps, void* stream);
+
+/* Backward of mm1_qknorm_rope_fwd: given dq, dk, dv (bf16, the attention
+ * backward's outputs) writes dqkv [B, S, (H + 2*Hkv) * D] bf16 and, with the
+ * norm, the weight gradients dwq, dwk [D] fp32 (deterministic two-stage sum;
+ * needs a workspace of mm1_qknorm_rope_bwd_workspace_size() bytes).  Replaces
+ * autograd through :423-428 and :458-461; no counterpart as a separate call. */
+size_t mm1_qknorm_rope_bwd_workspace_size(void);
+int mm1_qknorm_rope_bwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
+                        const float* sin_t, const void* dq, const void* dk, const void* dv,
+                        void* dqkv, float* dwq, float* dwk, void* workspace, size_t workspace_bytes,
+                        int B, int S, int H, int Hkv, int D, int rot_len, float eps, void* stream);
+
 /* Static description of a return code. */
 const char* mm1_attn_strerror(int code);
 

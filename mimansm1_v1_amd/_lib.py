@@ -30,6 +30,12 @@ SIGNATURES = {
                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_attn_bwd_dq_reduce": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
                                         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_qknorm_rope_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_qknorm_rope_bwd_workspace_size": (_c_size, []),
+    "mm1_qknorm_rope_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _c_size, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                     _c_float, _vp]),
     "mm1_attn_strerror": (ctypes.c_char_p, [_c_int]),
 }
 

@@ -10,7 +10,9 @@ Drop-in surface (same names, arguments, layouts and return values):
   ``AUTOTUNE``, ``warmup``, ``flash_delta``                        (AT:94, :192-217, :326-357)
 * ``AttnConfig``, ``RMSNorm``, ``Rotary``, ``rotate_half``, ``apply_rope``,
   ``Attention`` with backends ``"hip"`` (alias ``"tilelang"``), ``"sdpa"``,
-  ``"flex"``, ``"math"``                                          (AT:396-518)
+  ``"flex"``, ``"math"``                                          (AT:396-518);
+  with ``"hip"`` and bf16 activations the projection is one GEMM against
+  wq | wk | wv followed by the QK-norm + RoPE kernel (``qknorm_rope``)
 * harnesses ``reference``, ``rope_reference``, ``check_math``, ``check_gpu``,
   ``benchmark``, ``tune``                                          (AT:521-788)
 
@@ -335,6 +337,73 @@ def apply_rope(x, cos, sin):
 _HIP_BACKENDS = ("hip", "tilelang")
 
 
+class QKNormRope(torch.autograd.Function):
+    """QK-RMSNorm + RoPE of the fused projection on the gfx950 kernels
+    (mm1_qknorm_rope_fwd / _bwd): qkv [B, S, (H + 2*Hkv) * D] bf16 ->
+    (q [B,S,H,D], k [B,S,Hkv,D], v [B,S,Hkv,D]) bf16, the numerics of
+    q_norm / k_norm + apply_rope on the wq / wk / wv outputs (AT:483-487).
+    wq, wk: the RMSNorm weights [D], or None without QK-norm."""
+
+    @staticmethod
+    def forward(ctx, qkv, wq, wk, cos, sin, heads, kv_heads, eps):
+        batch, seq_len, width = qkv.shape
+        dim = width // (heads + 2 * kv_heads)
+        if dim * (heads + 2 * kv_heads) != width:
+            raise ValueError(f"qkv width {width} is not (heads + 2*kv_heads) * head_dim")
+        _require(qkv, "qkv", (batch, seq_len, width))
+        for t, name in ((cos, "cos"), (sin, "sin")):
+            _require(t, name, (t.shape[0], dim), torch.float32)
+        wqf = None if wq is None else wq.detach().float().contiguous()
+        wkf = None if wk is None else wk.detach().float().contiguous()
+        q = torch.empty(batch, seq_len, heads, dim, dtype=DTYPE, device=qkv.device)
+        k = torch.empty(batch, seq_len, kv_heads, dim, dtype=DTYPE, device=qkv.device)
+        v = torch.empty_like(k)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        rc = _lib.load().mm1_qknorm_rope_fwd(
+            qkv.data_ptr(), ptr(wqf), ptr(wkf), cos.data_ptr(), sin.data_ptr(), q.data_ptr(),
+            k.data_ptr(), v.data_ptr(), batch, seq_len, heads, kv_heads, dim, cos.shape[0], eps,
+            _stream(qkv.device))
+        _lib.check(rc, "mm1_qknorm_rope_fwd")
+        ctx.save_for_backward(qkv, wqf, wkf, cos, sin)
+        ctx.meta = (heads, kv_heads, eps, None if wq is None else wq.dtype,
+                    None if wk is None else wk.dtype)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        qkv, wqf, wkf, cos, sin = ctx.saved_tensors
+        heads, kv_heads, eps, wq_dtype, wk_dtype = ctx.meta
+        batch, seq_len, width = qkv.shape
+        dim = width // (heads + 2 * kv_heads)
+        shapes = ((batch, seq_len, heads, dim), (batch, seq_len, kv_heads, dim), (batch, seq_len, kv_heads, dim))
+        grads = []
+        for g, shp in zip((dq, dk, dv), shapes):
+            g = torch.zeros(shp, dtype=DTYPE, device=qkv.device) if g is None else g
+            grads.append(g.to(DTYPE).contiguous())
+        dqkv = torch.empty_like(qkv)
+        lib = _lib.load()
+        norm = wqf is not None
+        dwq = torch.empty(dim, dtype=torch.float32, device=qkv.device) if norm else None
+        dwk = torch.empty_like(dwq) if norm else None
+        ws_bytes = lib.mm1_qknorm_rope_bwd_workspace_size()
+        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=qkv.device)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        rc = lib.mm1_qknorm_rope_bwd(
+            qkv.data_ptr(), ptr(wqf), ptr(wkf), cos.data_ptr(), sin.data_ptr(), grads[0].data_ptr(),
+            grads[1].data_ptr(), grads[2].data_ptr(), dqkv.data_ptr(), ptr(dwq), ptr(dwk),
+            ws.data_ptr(), ws_bytes, batch, seq_len, heads, kv_heads, dim, cos.shape[0], eps,
+            _stream(qkv.device))
+        _lib.check(rc, "mm1_qknorm_rope_bwd")
+        if norm:
+            dwq, dwk = dwq.to(wq_dtype), dwk.to(wk_dtype)
+        return dqkv, dwq, dwk, None, None, None, None, None
+
+
+def qknorm_rope(qkv, wq, wk, cos, sin, heads, kv_heads, eps=1e-5):
+    """The attention kernel's q, k, v from the fused projection (see QKNormRope)."""
+    return QKNormRope.apply(qkv, wq, wk, cos, sin, heads, kv_heads, eps)
+
+
 class Attention(nn.Module):
     """GQA attention sublayer: wq/wk/wv, QK-RMSNorm, RoPE, causal attention, wo
     (AT:464-518).  ``backend`` "hip" (also accepted under the reference's name
@@ -365,11 +434,27 @@ class Attention(nn.Module):
         k = apply_rope(k, self.rope.cos, self.rope.sin)
         return q, k, v
 
+    def project_fused(self, x):
+        """The same q, k, v from one GEMM against wq | wk | wv and the QK-norm +
+        RoPE kernel; None when the projection is not bf16 (fp32 activations
+        outside autocast keep the reference's fp32 norm and rotation)."""
+        batch, seq_len, _ = x.shape
+        cfg = self.cfg
+        w = torch.cat((self.wq.weight, self.wk.weight, self.wv.weight), dim=0)
+        qkv = F.linear(x, w)
+        if qkv.dtype != DTYPE or not qkv.is_cuda or cfg.head_dim != 128:
+            return None
+        qn = self.q_norm.weight if cfg.qk_norm else None
+        kn = self.k_norm.weight if cfg.qk_norm else None
+        return qknorm_rope(qkv.contiguous(), qn, kn, self.rope.cos, self.rope.sin,
+                           cfg.n_heads, cfg.n_kv_heads, cfg.norm_eps)
+
     def forward(self, x, backend=None):
         batch, seq_len, _ = x.shape
         cfg = self.cfg
         backend = backend or cfg.backend
-        q, k, v = self.project(x)
+        fused = self.project_fused(x) if backend in _HIP_BACKENDS and x.is_cuda else None
+        q, k, v = fused if fused is not None else self.project(x)
 
         if backend in _HIP_BACKENDS:
             out = flash_attention(q.to(DTYPE).contiguous(), k.to(DTYPE).contiguous(),

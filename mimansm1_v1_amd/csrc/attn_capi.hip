@@ -24,6 +24,14 @@ hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void
                          const void* workspace, void* dk, void* dv,
                          int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                          hipStream_t stream);
+size_t qknorm_bwd_workspace_bytes();
+hipError_t launch_qknorm_fwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
+                             const float* sin_t, void* q, void* k, void* v, int B, int S, int H, int Hkv,
+                             float eps, hipStream_t stream);
+hipError_t launch_qknorm_bwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
+                             const float* sin_t, const void* dq, const void* dk, const void* dv,
+                             void* dqkv, float* dwq, float* dwk, void* workspace, int B, int S, int H,
+                             int Hkv, float eps, hipStream_t stream);
 }  // namespace mm1
 
 namespace {
@@ -164,6 +172,45 @@ int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
   if (rc) return rc;
   return mm1_attn_bwd_dq_reduce(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes,
                                 B, S, H, Hkv, D, causal, sm_scale, stream);
+}
+
+static int check_qknorm(int B, int S, int H, int Hkv, int D, int rot_len, float eps, bool norm) {
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (S > rot_len) return MM1_E_SHAPE;
+  if (norm && !(eps > 0.f && isfinite(eps))) return MM1_E_SCALE;
+  return MM1_OK;
+}
+
+int mm1_qknorm_rope_fwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
+                        const float* sin_t, void* q, void* k, void* v,
+                        int B, int S, int H, int Hkv, int D, int rot_len, float eps, void* stream) {
+  if (!qkv || !cos_t || !sin_t || !q || !k || !v || (!wq) != (!wk)) return MM1_E_NULL;
+  int rc = check_qknorm(B, S, H, Hkv, D, rot_len, eps, wq != nullptr);
+  if (rc) return rc;
+  if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(cos_t) ||
+      !aligned16(sin_t))
+    return MM1_E_ALIGN;
+  return from_hip(mm1::launch_qknorm_fwd(qkv, wq, wk, cos_t, sin_t, q, k, v, B, S, H, Hkv, eps,
+                                         static_cast<hipStream_t>(stream)));
+}
+
+size_t mm1_qknorm_rope_bwd_workspace_size(void) { return mm1::qknorm_bwd_workspace_bytes(); }
+
+int mm1_qknorm_rope_bwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
+                        const float* sin_t, const void* dq, const void* dk, const void* dv,
+                        void* dqkv, float* dwq, float* dwk, void* workspace, size_t workspace_bytes,
+                        int B, int S, int H, int Hkv, int D, int rot_len, float eps, void* stream) {
+  if (!qkv || !cos_t || !sin_t || !dq || !dk || !dv || !dqkv || (!wq) != (!wk)) return MM1_E_NULL;
+  if (wq && (!dwq || !dwk)) return MM1_E_NULL;
+  int rc = check_qknorm(B, S, H, Hkv, D, rot_len, eps, wq != nullptr);
+  if (rc) return rc;
+  if (wq && (!workspace || workspace_bytes < mm1::qknorm_bwd_workspace_bytes())) return MM1_E_WORKSPACE;
+  if (!aligned16(qkv) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(dqkv) ||
+      !aligned16(cos_t) || !aligned16(sin_t))
+    return MM1_E_ALIGN;
+  return from_hip(mm1::launch_qknorm_bwd(qkv, wq, wk, cos_t, sin_t, dq, dk, dv, dqkv, dwq, dwk,
+                                         workspace, B, S, H, Hkv, eps, static_cast<hipStream_t>(stream)));
 }
 
 const char* mm1_attn_strerror(int code) {

@@ -20,6 +20,11 @@ What it restates (all citations are to /root/reference):
   softmax-attention backward, computed per (batch, head) chunk so that the
   full-size configs fit (usable on a GPU device for the large parity tests).
 * ``rope(x, theta)`` -- explicit pairwise rotation (AT:533-541).
+* ``rope_tables``, ``rmsnorm``, ``apply_rope``, ``qknorm_rope`` -- the
+  sublayer prologue (config 5): the Rotary cos/sin tables (AT:438-444), the
+  QK-RMSNorm in fp32 cast back to the input dtype (AT:423-428), the
+  rotate-half RoPE in the input dtype with the tables cast to it (AT:452-461),
+  applied to the wq | wk | wv outputs as Attention.forward does (AT:483-487).
 * ``make_inputs(config)`` -- the seeded input recipe of BASELINE.json configs
   1-5: CPU ``torch.Generator().manual_seed(seed)``, draws in the order Q, K, V,
   dO (config 4 adds per-head sigma ~ U(0.5, 3) and RoPE in fp32 before the
@@ -164,6 +169,48 @@ def rope(x, theta, dtype=torch.float64):
     xd = x.to(dtype)
     lo, hi = xd[..., :half], xd[..., half:]
     return torch.cat([lo * c - hi * s, lo * s + hi * c], dim=-1)
+
+
+def rope_tables(head_dim, max_seq_len, theta):
+    """fp32 cos/sin tables [max_seq_len, head_dim], halves repeated (AT:438-444)."""
+    freqs = 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+    angles = torch.outer(torch.arange(max_seq_len).float(), freqs)
+    table = torch.cat((angles, angles), dim=-1)
+    return table.cos(), table.sin()
+
+
+def rmsnorm(x, w, eps):
+    """x * rsqrt(mean(x^2) + eps) * w in fp32, cast back to x.dtype (AT:423-428)."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * w.float()).to(x.dtype)
+
+
+def rotate_half(x):
+    left, right = x.chunk(2, dim=-1)
+    return torch.cat((-right, left), dim=-1)
+
+
+def apply_rope(x, cos, sin):
+    """x * cos + rotate_half(x) * sin with the tables cast to x.dtype (AT:452-461)."""
+    seq_len = x.shape[1]
+    c = cos[:seq_len].to(x.dtype).unsqueeze(1)
+    s = sin[:seq_len].to(x.dtype).unsqueeze(1)
+    return x * c + rotate_half(x) * s
+
+
+def qknorm_rope(qkv, wq, wk, cos, sin, heads, kv_heads, eps=1e-5):
+    """The attention kernel's inputs from the fused projection qkv
+    [B, S, (heads + 2*kv_heads) * D] (columns wq | wk | wv outputs), as
+    Attention.forward computes them (AT:483-487); wq = wk = None: no QK-norm."""
+    B, S, _ = qkv.shape
+    D = qkv.shape[-1] // (heads + 2 * kv_heads)
+    q = qkv[..., :heads * D].reshape(B, S, heads, D)
+    k = qkv[..., heads * D:(heads + kv_heads) * D].reshape(B, S, kv_heads, D)
+    v = qkv[..., (heads + kv_heads) * D:].reshape(B, S, kv_heads, D)
+    if wq is not None:
+        q, k = rmsnorm(q, wq, eps), rmsnorm(k, wk, eps)
+    return apply_rope(q, cos, sin).contiguous(), apply_rope(k, cos, sin).contiguous(), v.contiguous()
 
 
 # BASELINE.json configs (index = position in its "configs" list + 1).

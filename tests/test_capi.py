@@ -18,7 +18,7 @@ FAKE = 1 << 20  # aligned, non-null; never dereferenced (calls fail validation f
 
 def declared_functions():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(mm1_attn_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(mm1_\w+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
@@ -36,7 +36,7 @@ def test_exports_every_declared_symbol(lib):
     assert len(names) >= 8
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.library_path())],
                          capture_output=True, text=True, check=True).stdout
-    exported = set(re.findall(r"\bT (mm1_attn_\w+)", out))
+    exported = set(re.findall(r"\bT (mm1_\w+)", out))
     assert set(names) <= exported, set(names) - exported
     assert set(names) == set(_lib.SIGNATURES), "ctypes table and header disagree"
     for n in names:
@@ -113,3 +113,29 @@ def test_bwd_argument_errors(lib):
 def test_python_error_wrapper(lib):
     with pytest.raises(_lib.AttnError, match="head_dim must be 128"):
         _lib.check(-3, "mm1_attn_fwd")
+
+
+def test_qknorm_rope_argument_errors_without_device(lib):
+    """The sublayer prologue entries reject bad arguments before any launch."""
+    fwd = lib.mm1_qknorm_rope_fwd
+    ok = dict(B=1, S=64, H=10, Hkv=2, D=128, rot=64, eps=1e-5)
+
+    def call(qkv=FAKE, wq=FAKE, wk=FAKE, q=FAKE, **kw):
+        a = dict(ok, **kw)
+        return fwd(qkv, wq, wk, FAKE, FAKE, q, FAKE, FAKE, a["B"], a["S"], a["H"], a["Hkv"], a["D"],
+                   a["rot"], a["eps"], None)
+
+    assert call(qkv=None) == -1
+    assert call(wk=None) == -1            # both norm weights or neither
+    assert call(D=64) == -3
+    assert call(H=9) == -2
+    assert call(rot=63) == -2             # tables shorter than the sequence
+    assert call(eps=0.0) == -5
+    assert call(q=FAKE + 8) == -6
+    ws = lib.mm1_qknorm_rope_bwd_workspace_size()
+    assert ws > 0
+    bwd = lib.mm1_qknorm_rope_bwd
+    args = [FAKE] * 11
+    assert bwd(*args, None, ws, 1, 64, 10, 2, 128, 64, 1e-5, None) == -4
+    assert bwd(*args, FAKE, ws - 4, 1, 64, 10, 2, 128, 64, 1e-5, None) == -4
+    assert bwd(*args[:9], None, FAKE, FAKE, ws, 1, 64, 10, 2, 128, 64, 1e-5, None) == -1

@@ -235,3 +235,95 @@ def test_golden_fixtures(hip_device):
                                bf16_products=True, o=o)
         for key, got, e in zip(("dq", "dk", "dv"), (dq, dk, dv), emu):
             assert_bf16_close(key, got, c[key], log, emulated=e)
+
+
+# ---------------------------------------------------------------------------
+# Sublayer prologue (config 5): QK-RMSNorm + RoPE kernel and the full sublayer.
+
+def _qkv_inputs(B, S, H, Hkv, seed, norm=True):
+    gen = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn(B, S, (H + 2 * Hkv) * 128, generator=gen) * 2).to(torch.bfloat16)
+    wq = (1 + 0.3 * torch.randn(128, generator=gen)) if norm else None
+    wk = (1 + 0.3 * torch.randn(128, generator=gen)) if norm else None
+    cos, sin = R.rope_tables(128, S + 5, 10000.0)
+    grads = [torch.randn(B, S, h, 128, generator=gen).to(torch.bfloat16) for h in (H, Hkv, Hkv)]
+    return qkv, wq, wk, cos, sin, grads
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,norm", [(2, 100, 10, 2, True), (1, 257, 6, 3, True), (1, 64, 4, 4, False)],
+                         ids=["B2S100G5", "B1S257G2", "B1S64nonorm"])
+def test_qknorm_rope_kernel_vs_oracle(hip_device, B, S, H, Hkv, norm):
+    """Forward: bf16 Q/K/V of the kernel against the oracle's bf16 chain
+    (near bit-exact: only the fp32 mean-of-squares order and rsqrt may flip a
+    rounding).  Backward: dqkv and the norm-weight gradients against CPU
+    autograd through the same chain."""
+    import mimansm1_v1_amd as mm
+    from mimansm1_v1_amd import attention as A
+    log(f"[case] qknorm_rope B={B} S={S} H={H} Hkv={Hkv} norm={norm}")
+    qkv, wq, wk, cos, sin, (gq, gk, gv) = _qkv_inputs(B, S, H, Hkv, seed=S + H, norm=norm)
+    dev = lambda t: None if t is None else t.to(hip_device)
+    qkv_d = qkv.to(hip_device).requires_grad_(True)
+    wq_d = dev(wq).requires_grad_(True) if norm else None
+    wk_d = dev(wk).requires_grad_(True) if norm else None
+    q, k, v = A.qknorm_rope(qkv_d, wq_d, wk_d, dev(cos), dev(sin), H, Hkv, 1e-5)
+    torch.autograd.backward((q, k, v), (dev(gq), dev(gk), dev(gv)))
+    torch.cuda.synchronize()
+
+    qkv_c = qkv.clone().requires_grad_(True)
+    wq_c = wq.clone().requires_grad_(True) if norm else None
+    wk_c = wk.clone().requires_grad_(True) if norm else None
+    wantq, wantk, wantv = R.qknorm_rope(qkv_c, wq_c, wk_c, cos, sin, H, Hkv, 1e-5)
+    torch.autograd.backward((wantq, wantk, wantv), (gq, gk, gv))
+    for name, got, want in (("Q", q, wantq), ("K", k, wantk)):
+        got = got.detach().cpu()
+        same = (got == want.detach()).float().mean().item()
+        log(f"  {name}: {100 * same:.3f}% bitwise equal")
+        assert same > 0.99, name
+        assert_bf16_close(name, got, want.detach().float(), log)
+    assert torch.equal(v.detach().cpu(), wantv.detach())
+    dqkv = qkv_d.grad.cpu()
+    same = (dqkv == qkv_c.grad).float().mean().item()
+    log(f"  dqkv: {100 * same:.3f}% bitwise equal")
+    assert same > 0.98
+    assert_bf16_close("dqkv", dqkv, qkv_c.grad.float(), log)
+    if norm:
+        for name, got, want in (("dwq", wq_d.grad, wq_c.grad), ("dwk", wk_d.grad, wk_c.grad)):
+            err = ((got.cpu() - want).norm() / want.norm()).item()
+            log(f"  {name}: rel_l2 {err:.2e}")
+            assert err < 2e-3, name
+
+
+def test_sublayer_hip_matches_reference_backend(hip_device):
+    """The config-5 sublayer (fused QKV GEMM, QK-norm + RoPE kernel, flash
+    attention, wo) under bf16 autocast against the same module run with the
+    reference's "math" backend: output and every gradient."""
+    from mimansm1_v1_amd import attention as A
+    log("[case] sublayer B2 S384 hip vs math (bf16 autocast)")
+    torch.manual_seed(0)
+    cfg = A.AttnConfig(max_seq_len=512)
+    mod = A.Attention(cfg, A.Rotary(cfg.head_dim, cfg.max_seq_len, cfg.rope_theta)).to(hip_device)
+    with torch.no_grad():
+        for lin in (mod.wq, mod.wk, mod.wv, mod.wo):
+            lin.weight.normal_(0.0, 0.02)
+        mod.q_norm.weight.uniform_(0.7, 1.3)
+        mod.k_norm.weight.uniform_(0.7, 1.3)
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 384, cfg.d_model, generator=gen).to(hip_device)
+    dy = torch.randn(2, 384, cfg.d_model, generator=gen).to(hip_device)
+    results = {}
+    for backend in ("hip", "math"):
+        mod.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = mod(xi, backend=backend)
+        y.backward(dy.to(y.dtype))
+        torch.cuda.synchronize()
+        results[backend] = [y.detach().float().cpu(), xi.grad.float().cpu()] + [
+            p.grad.float().cpu() for p in (mod.wq.weight, mod.wk.weight, mod.wv.weight, mod.wo.weight,
+                                           mod.q_norm.weight, mod.k_norm.weight)]
+    names = ["y", "dx", "dwq", "dwk", "dwv", "dwo", "dq_norm", "dk_norm"]
+    for name, got, want in zip(names, results["hip"], results["math"]):
+        err = ((got - want).norm() / want.norm()).item()
+        log(f"  {name}: rel_l2 {err:.2e}")
+        assert torch.isfinite(got).all(), name
+        assert err < 1e-2, name

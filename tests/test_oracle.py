@@ -210,3 +210,69 @@ def test_planted_lse_natural_log_is_caught():
     _, lse_ref = brute.fwd(_np(q), _np(k), _np(v), True)
     wrong = torch.logsumexp(R.scores(q, k, True, 5, torch.float64), dim=-1)  # missing log2(e)
     assert np.abs(_np(wrong) - lse_ref).max() > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# Sublayer prologue (config 5): tables, RMSNorm, rotate-half RoPE.
+
+def test_rope_tables_closed_form():
+    """cos/sin at position p, column j: angle p * theta^(-2(j mod D/2)/D);
+    position 0 is the identity rotation."""
+    cos, sin = R.rope_tables(128, 40, 10000.0)
+    assert cos.shape == (40, 128) and cos.dtype == torch.float32
+    assert torch.equal(cos[0], torch.ones(128)) and torch.equal(sin[0], torch.zeros(128))
+    for p, j in [(1, 0), (7, 3), (39, 63), (39, 127), (12, 100)]:
+        ang = p * 10000.0 ** (-2 * (j % 64) / 128)
+        assert abs(cos[p, j].item() - math.cos(ang)) < 2e-6
+        assert abs(sin[p, j].item() - math.sin(ang)) < 2e-6
+
+
+def test_rotate_half_rope_equals_pairwise_rotation():
+    """In fp64 the rotate-half form rotates the pairs (d, d + D/2): it equals
+    the explicit pairwise rotation (an independent formula) and keeps norms."""
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 33, 3, 128, generator=gen, dtype=torch.float64)
+    freqs = 1.0 / (10000.0 ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))
+    ang = torch.outer(torch.arange(33, dtype=torch.float64), freqs)
+    table = torch.cat((ang, ang), dim=-1)
+    got = R.apply_rope(x, table.cos(), table.sin())
+    assert torch.allclose(got, R.rope(x, 10000.0), atol=1e-12)
+    assert torch.allclose(got.norm(dim=-1), x.norm(dim=-1), atol=1e-10)
+    # rotating twice by a half turn of each pair: rotate_half(rotate_half(x)) = -x
+    assert torch.equal(R.rotate_half(R.rotate_half(x)), -x)
+
+
+def test_rmsnorm_closed_forms():
+    """Unit weight: each output row has mean square 1 / (1 + eps / ms); a
+    constant row c maps to sign(c) |c| / sqrt(c^2 + eps); scale invariance."""
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(4, 5, 128, generator=gen) * 3
+    w = torch.ones(128)
+    y = R.rmsnorm(x, w, 1e-5)
+    ms = x.pow(2).mean(-1)
+    assert torch.allclose(y.pow(2).mean(-1), 1 / (1 + 1e-5 / ms), rtol=1e-5)
+    c = torch.full((1, 128), -0.3)
+    assert torch.allclose(R.rmsnorm(c, w, 1e-5), torch.full((1, 128), -0.3 / math.sqrt(0.09 + 1e-5)))
+    assert torch.allclose(R.rmsnorm(5 * x, w, 0.0), R.rmsnorm(x, w, 0.0), atol=1e-6)
+    wv = torch.linspace(0.5, 2, 128)
+    assert torch.allclose(R.rmsnorm(x, wv, 1e-5), y * wv, atol=1e-6)
+    # bf16 in, bf16 out: one rounding of the fp32 result
+    xb = x.to(torch.bfloat16)
+    assert torch.equal(R.rmsnorm(xb, wv, 1e-5), R.rmsnorm(xb.float(), wv, 1e-5).to(torch.bfloat16))
+
+
+def test_qknorm_rope_column_split():
+    """qkv columns are wq | wk | wv outputs: V is the untouched last slice and
+    Q / K are the normalised, rotated first slices (no norm: pure rotation)."""
+    gen = torch.Generator().manual_seed(3)
+    qkv = torch.randn(2, 9, (6 + 2 * 3) * 128, generator=gen)
+    cos, sin = R.rope_tables(128, 16, 10000.0)
+    q, k, v = R.qknorm_rope(qkv, None, None, cos, sin, 6, 3)
+    assert q.shape == (2, 9, 6, 128) and k.shape == (2, 9, 3, 128) and v.shape == (2, 9, 3, 128)
+    assert torch.equal(v.reshape(2, 9, -1), qkv[..., 9 * 128:])
+    assert torch.equal(q[:, 0], qkv[:, 0, :6 * 128].reshape(2, 6, 128))   # position 0: identity
+    assert torch.allclose(k.norm(dim=-1), qkv[..., 6 * 128:9 * 128].reshape(2, 9, 3, 128).norm(dim=-1),
+                          rtol=1e-5)
+    w = torch.ones(128)
+    qn, _, _ = R.qknorm_rope(qkv, w, w, cos, sin, 6, 3)
+    assert torch.allclose(qn.pow(2).mean(-1), torch.ones(2, 9, 6), rtol=1e-3)
