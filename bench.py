@@ -65,6 +65,34 @@ def parse(argv=None):
     return ap.parse_args(argv)
 
 
+# Kernel launched by each tiling index of a stage (mm1_attn_tile_desc order).
+KERNEL_NAMES = {"fwd": ("attn_fwd_kernel", "attn_fwd_kernel", "attn_fwd_pp_kernel"),
+                "dkdv": ("attn_dkdv_pipe_kernel", "attn_dkdv_kernel"),
+                "dq": ("attn_dq_kernel", "attn_dq_kernel")}
+TILE_ENV = {"fwd": "MM1_FWD_VARIANT", "dkdv": "MM1_DKDV_VARIANT", "dq": "MM1_DQ_VARIANT"}
+USER_TILE_ENV = {k: os.environ[v] for k, v in TILE_ENV.items() if v in os.environ}
+
+
+def select_tiles(batch, seq):
+    """The tilings the tile record (this machine's store, then the shipped
+    gfx950 table) holds for this workload -- what get_kernel's handles launch
+    -- applied to the stage calls through their per-call environment switch.
+    A switch the caller set explicitly wins.  Returns {stage: index}."""
+    from mimansm1_v1_amd import attention as A
+    from mimansm1_v1_amd import tuned
+    shape = (batch, HEADS, seq, DIM, True, HEADS // KV_HEADS)
+    fwd_cfg = tuned.lookup("attention_fwd", shape)
+    bwd_cfg = tuned.lookup("attention_bwd", shape)
+    fwd = A.tile_index("fwd", fwd_cfg) if fwd_cfg else None
+    bwd = A.tile_index("bwd", bwd_cfg) if bwd_cfg else None
+    chosen = {"fwd": fwd or 0, "dkdv": (bwd or (0, 0))[0], "dq": (bwd or (0, 0))[1]}
+    for stage, env in TILE_ENV.items():
+        if stage in USER_TILE_ENV:
+            chosen[stage] = int(USER_TILE_ENV[stage])
+        os.environ[env] = str(chosen[stage])
+    return chosen
+
+
 class Workload:
     def __init__(self, lib, batch, seq, device, seed=0):
         import torch
@@ -361,6 +389,7 @@ def main(argv=None):
                   f"parts {res['part_ms']}, other {res['other_ms']:.3f}", file=sys.stderr, flush=True)
             continue
         B, S = CONFIGS[cfg]["batch"], CONFIGS[cfg]["seq"]
+        tiles = select_tiles(B, S)
         wl = Workload(lib, B, S, device)
         ms, stages = time_workload(wl, args.steps, args.warmup)
         unit = gemm_unit(B, S)
@@ -373,6 +402,7 @@ def main(argv=None):
             "bwd_tflops": 5 * unit / ((ms - stages["fwd"]) * 1e-3) / 1e12,
             "kernel_tflops": {k: flops[k] / (stages[k] * 1e-3) / 1e12 for k in flops},
             "kernel_flops": flops,
+            "tiles": tiles,
         }
         if not args.no_autograd:
             res["ms_per_step_autograd"] = time_autograd(B, S, device, args.steps, args.warmup)
@@ -418,11 +448,11 @@ def main(argv=None):
         "fwd_tflops": round(main_res["fwd_tflops"], 2),
         "bwd_tflops": round(main_res["bwd_tflops"], 2),
         "stage_ms": {k: round(v, 4) for k, v in main_res["stage_ms"].items()},
+        "tiles": main_res["tiles"],
         "reference_flop_count_tflops": round(main_res["tflops"] * 5 / 7, 2),
         "roofline": {
             "bound": "mfma",
-            "kernel": {"fwd": "attn_fwd_kernel", "dkdv": "attn_dkdv_pipe_kernel",
-                       "dq": "attn_dq_kernel"}[dom],
+            "kernel": KERNEL_NAMES[dom][main_res["tiles"][dom]],
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MM1_ATTN_VERSION 1
+#define MM1_ATTN_VERSION 2
 
 #define MM1_OK 0
 #define MM1_E_NULL (-1)        /* a required pointer is NULL */
@@ -34,6 +34,12 @@ extern "C" {
 #define MM1_E_WORKSPACE (-4)   /* workspace smaller than mm1_attn_bwd_workspace_size() */
 #define MM1_E_SCALE (-5)       /* sm_scale not a positive finite number */
 #define MM1_E_ALIGN (-6)       /* a tensor pointer is not 16-byte aligned */
+#define MM1_E_TILES (-7)       /* tiling index out of range (see mm1_attn_tile_count) */
+
+/* Kernel kinds for the tiling queries below. */
+#define MM1_TILES_FWD 0
+#define MM1_TILES_DKDV 1
+#define MM1_TILES_DQ 2
 
 /* Library version (MM1_ATTN_VERSION of the build). */
 int mm1_attn_version(void);
@@ -99,6 +105,36 @@ int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const vo
                            const void* workspace, size_t workspace_bytes,
                            int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                            void* stream);
+
+/* Tilings compiled into the library.  The reference autotunes each TileLang
+ * kernel over a space of (block_M, block_N, threads, num_stages)
+ * (attention_tilelang.py:61-98) and remembers the winner per (device, kernel,
+ * shape) (get_kernel, :329-346; CODE/mimans/model/tuned.py:59-74); here the
+ * space is the fixed set of gfx950 tilings built into this library, all with
+ * the same results up to fp32 summation order.
+ *  - mm1_attn_tile_count(kind): number of tilings of MM1_TILES_FWD,
+ *    MM1_TILES_DKDV or MM1_TILES_DQ (0 for another kind);
+ *  - mm1_attn_tile_desc(kind, i): static "key=value ..." description of
+ *    tiling i (block_M, block_N, waves, stages, schedule), NULL if out of range.
+ * Index 0 is each kind's default.  The calls without a tiling argument use
+ * the default unless the environment variable MM1_FWD_VARIANT,
+ * MM1_DKDV_VARIANT or MM1_DQ_VARIANT names another index (read per call). */
+int mm1_attn_tile_count(int kind);
+const char* mm1_attn_tile_desc(int kind, int index);
+
+/* mm1_attn_fwd and mm1_attn_bwd with an explicit tiling: `tiles`,
+ * `dkdv_tiles`, `dq_tiles` index the tilings above (-1 = the default of the
+ * calls without them); MM1_E_TILES for an index out of range.  What a tuned
+ * kernel handle (get_kernel with a remembered config) launches. */
+int mm1_attn_fwd_tiles(const void* q, const void* k, const void* v, void* o, float* lse2,
+                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                       int tiles, void* stream);
+int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* dO,
+                       const float* lse2, const float* delta,
+                       void* dq, void* dk, void* dv,
+                       void* workspace, size_t workspace_bytes,
+                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                       int dkdv_tiles, int dq_tiles, void* stream);
 
 /* QK-RMSNorm + RoPE between the fused QKV projection and the attention
  * kernel.  Replaces, in Attention.forward (attention_tilelang.py:483-487), the

@@ -18,10 +18,17 @@ SIGNATURES = {
     "mm1_attn_version": (_c_int, []),
     "mm1_attn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp,
                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_fwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
+                                    _c_int, _c_int, _c_float, _c_int, _vp]),
+    "mm1_attn_tile_count": (_c_int, [_c_int]),
+    "mm1_attn_tile_desc": (ctypes.c_char_p, [_c_int, _c_int]),
     "mm1_attn_delta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "mm1_attn_bwd_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "mm1_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_bwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
+                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                    _c_int, _c_int, _vp]),
     "mm1_attn_bwd_dkdv": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_attn_bwd_dkdv_reduce": (_c_int, [_vp, _c_size, _vp, _vp,

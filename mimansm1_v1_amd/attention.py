@@ -41,37 +41,72 @@ DTYPE = torch.bfloat16
 LOG2E = 1.4426950408889634
 
 # ---------------------------------------------------------------------------
-# gfx950 tile policy (replaces the NVIDIA shared-memory model of AT:26-98).
+# gfx950 tilings (replace the TileLang search space and shared-memory model of
+# AT:26-98).  The library compiles a fixed set per kernel and describes each
+# (mm1_attn_tile_count / mm1_attn_tile_desc); index 0 is a kernel's default.
+# A config is the parsed description: block_M, block_N, waves, stages,
+# schedule -- for the backward both kernels' fields, prefixed dkdv_ / dq_.
 LDS_PER_CU = 160 * 1024
 WAVE = 64
-TILE_BYTES = 64 * 128 * 2
+TILE_KINDS = {"fwd": 0, "dkdv": 1, "dq": 2}    # MM1_TILES_FWD / _DKDV / _DQ
 
 
-def fwd_lds(rows_per_wave=64, block_n=64, dim=128):
-    """LDS bytes of the forward: two stages of a K tile and a transposed V tile."""
-    return 2 * 2 * block_n * dim * 2
+def _parse_tiles(desc: str) -> dict:
+    out = {}
+    for item in desc.split():
+        key, val = item.split("=", 1)
+        out[key] = int(val) if val.isdigit() else val
+    return out
 
 
-def bwd_lds(dim=128):
-    """LDS bytes of the two backward kernels (dK/dV, dQ), two stages each."""
-    dkdv = 2 * (4 * 64 * dim * 2 + 2 * 64 * 4)
-    dq = 2 * (3 * 64 * dim * 2)
-    return dkdv, dq
+def tile_space(kind):
+    """The tilings of one kernel ("fwd", "dkdv" or "dq") compiled into the library."""
+    lib = _lib.load()
+    code = TILE_KINDS[kind]
+    return [_parse_tiles(lib.mm1_attn_tile_desc(code, i).decode())
+            for i in range(lib.mm1_attn_tile_count(code))]
 
 
 def fwd_configs(dim=128):
-    """Forward tile variants compiled into the library."""
-    return [dict(rows_per_wave=r, waves=4, block_M=4 * r, block_N=64) for r in (64, 32)
-            if fwd_lds(r, 64, dim) <= LDS_PER_CU]
+    """Forward search space (AT:66-71): the compiled forward tilings."""
+    return tile_space("fwd") if dim == 128 else []
 
 
 def bwd_configs(dim=128):
-    return [dict(dkdv_keys=128, dkdv_queries=64, dq_block_M=128, dq_block_N=64, waves=4)]
+    """Backward search space (AT:74-79): every dK/dV tiling with every dQ tiling."""
+    if dim != 128:
+        return []
+    return [{**{f"dkdv_{k}": v for k, v in a.items()}, **{f"dq_{k}": v for k, v in b.items()}}
+            for a in tile_space("dkdv") for b in tile_space("dq")]
+
+
+def tile_index(kind, config):
+    """Library index of a forward config, (dK/dV, dQ) indices of a backward
+    one, or None when the config names no compiled tiling."""
+    config = dict(config)
+    if kind == "fwd":
+        space = tile_space("fwd")
+        return space.index(config) if config in space else None
+    parts = {}
+    for sub in ("dkdv", "dq"):
+        cut = len(sub) + 1
+        mine = {k[cut:]: v for k, v in config.items() if k.startswith(sub + "_")}
+        space = tile_space(sub)
+        if mine not in space:
+            return None
+        parts[sub] = space.index(mine)
+    if len(config) != sum(len(tile_space(sub)[i]) for sub, i in parts.items()):
+        return None
+    return parts["dkdv"], parts["dq"]
 
 
 AUTOTUNE = True
-FWD_TILES = fwd_configs()[0]
-BWD_TILES = bwd_configs()[0]
+# Index 0 of each kernel (the library's defaults), spelled out so that the
+# module imports without the library; the CPU tests check they agree.
+FWD_TILES = dict(block_M=128, block_N=64, waves=4, stages=2, schedule="ring")
+BWD_TILES = dict(dkdv_block_M=128, dkdv_block_N=32, dkdv_waves=8, dkdv_stages=7,
+                 dkdv_schedule="pipelined",
+                 dq_block_M=128, dq_block_N=64, dq_waves=4, dq_stages=2, dq_schedule="ring")
 
 
 # ---------------------------------------------------------------------------
@@ -108,6 +143,10 @@ class _Kernel:
         self.kv_heads = heads // groups
         self.sm_scale = (1.0 / dim) ** 0.5
         _lib.load()
+        self.tiles = tile_index(self.kind, self.config)
+        if self.tiles is None:
+            raise ValueError(f"{self.kind} config {self.config} is not a tiling compiled into "
+                             f"the library")
 
     def __repr__(self):
         return f"<{type(self).__name__} shape={self.shape} config={self.config}>"
@@ -124,10 +163,11 @@ class FwdKernel(_Kernel):
         _require(v, "v", (B, S, Hkv, D))
         out = torch.empty_like(q)
         lse = torch.empty(B, H, S, dtype=torch.float32, device=q.device)
-        rc = _lib.load().mm1_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                      lse.data_ptr(), B, S, H, Hkv, D, int(self.causal),
-                                      self.sm_scale, _stream(q.device))
-        _lib.check(rc, "mm1_attn_fwd")
+        rc = _lib.load().mm1_attn_fwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                            out.data_ptr(), lse.data_ptr(), B, S, H, Hkv, D,
+                                            int(self.causal), self.sm_scale, self.tiles,
+                                            _stream(q.device))
+        _lib.check(rc, "mm1_attn_fwd_tiles")
         return out, lse
 
 
@@ -153,12 +193,13 @@ class BwdKernel(_Kernel):
         ws_bytes = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, D)
         ws = (torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device)
               if ws_bytes else None)
-        rc = lib.mm1_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
-                              lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), dk.data_ptr(),
-                              dv.data_ptr(), ws.data_ptr() if ws is not None else None,
-                              ws_bytes, B, S, H, Hkv, D, int(self.causal), self.sm_scale,
-                              _stream(q.device))
-        _lib.check(rc, "mm1_attn_bwd")
+        rc = lib.mm1_attn_bwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                    grad_out.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+                                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                    ws.data_ptr() if ws is not None else None, ws_bytes,
+                                    B, S, H, Hkv, D, int(self.causal), self.sm_scale,
+                                    *self.tiles, _stream(q.device))
+        _lib.check(rc, "mm1_attn_bwd_tiles")
 
 
 class DeltaKernel:
@@ -186,20 +227,88 @@ def flash_delta(batch, heads, seq_len, dim):
     return DeltaKernel(batch, heads, seq_len, dim)
 
 
+def _median_ms(fn, device, budget_ms=60.0, max_reps=25):
+    """Median duration of fn() on the current stream of `device` (HIP events)."""
+    stream = torch.cuda.current_stream(device)
+    fn()
+    torch.cuda.synchronize(device)
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize(device)
+    first = (time.perf_counter() - t0) * 1e3
+    reps = int(min(max_reps, max(3, budget_ms / max(first, 1e-3))))
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+    for start, end in events:
+        start.record(stream)
+        fn()
+        end.record(stream)
+    torch.cuda.synchronize(device)
+    times = sorted(start.elapsed_time(end) for start, end in events)
+    return times[len(times) // 2]
+
+
+def autotune(kind, shape, device=None, verbose=False):
+    """Time every compiled tiling of `kind` at `shape` on synthetic inputs and
+    return (best config, its median ms, [(ms, config), ...]).  The search the
+    reference's TileLang autotuner runs for a miss (AT:337-343), over this
+    library's tilings; inputs are seeded so that runs are repeatable."""
+    if kind not in ("fwd", "bwd"):
+        raise ValueError(f"unknown kernel kind {kind!r}")
+    batch, heads, seq_len, dim, causal, groups = shape
+    device = torch.device(device or f"cuda:{torch.cuda.current_device()}")
+    gen = torch.Generator(device=device).manual_seed(0)
+    kv_heads = heads // groups
+
+    def rand(*dims):
+        return torch.randn(*dims, device=device, dtype=DTYPE, generator=gen)
+
+    q, k, v = rand(batch, seq_len, heads, dim), rand(batch, seq_len, kv_heads, dim), \
+        rand(batch, seq_len, kv_heads, dim)
+    results = []
+    if kind == "fwd":
+        for config in fwd_configs(dim):
+            handle = FwdKernel(shape, config)
+            results.append((_median_ms(lambda: handle(q, k, v), device), config))
+    else:
+        out, lse = FwdKernel(shape, FWD_TILES)(q, k, v)
+        grad_out = rand(batch, seq_len, heads, dim)
+        delta = DeltaKernel(batch, heads, seq_len, dim)(out, grad_out)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        for config in bwd_configs(dim):
+            handle = BwdKernel(shape, config)
+            results.append((_median_ms(lambda: handle(q, k, v, grad_out, lse, delta, dq, dk, dv),
+                                       device), config))
+    if verbose:
+        for ms, config in results:
+            print(f"    {ms:8.3f} ms  {' '.join(f'{k}={v}' for k, v in config.items())}")
+    best_ms, best = min(results, key=lambda r: r[0])
+    return best, best_ms, results
+
+
 def get_kernel(kind, *shape):
     """Per-shape kernel handle, cached in ``_kernels`` under
     ``(kind, shape, AUTOTUNE)`` (AT:329-346).  Lookup order as in the
-    reference: tile record for this device and shape, then a timed search
-    over the compiled variants when AUTOTUNE is set, else the defaults."""
+    reference: the tile record for this device and shape, then a timed search
+    over the compiled tilings when AUTOTUNE is set and a GPU is present (its
+    winner is recorded), else the defaults.  A record naming a tiling this
+    build does not have is ignored."""
     if kind not in ("fwd", "bwd"):
         raise ValueError(f"unknown kernel kind {kind!r}")
     key = (kind, tuple(shape), AUTOTUNE)
     if key not in _kernels:
         cls = FwdKernel if kind == "fwd" else BwdKernel
         name = f"attention_{kind}"
+        kernel = None
         remembered = tuned.lookup(name, shape)
-        if remembered is not None:
+        if remembered is not None and tile_index(kind, remembered) is not None:
             kernel = cls(shape, remembered)
+        elif AUTOTUNE and torch.cuda.is_available():
+            cls(shape, FWD_TILES if kind == "fwd" else BWD_TILES)   # shape check first
+            config, latency, _ = autotune(kind, shape)
+            kernel = cls(shape, config)
+            kernel.latency = latency
+            tuned.record(name, shape, tuned.config_of(kernel))
         else:
             kernel = cls(shape, FWD_TILES if kind == "fwd" else BWD_TILES)
         _kernels[key] = kernel
@@ -526,15 +635,19 @@ def check_math():
 
     torch.manual_seed(0)
     cfg = AttnConfig(backend="math")
-    kb = 1024
-    print("LDS (gfx950, 160 KiB per CU)")
-    dkdv, dq = bwd_lds()
-    print(f"    forward   {fwd_lds() / kb:6.1f} KiB")
-    print(f"    dK/dV     {dkdv / kb:6.1f} KiB")
-    print(f"    dQ        {dq / kb:6.1f} KiB")
-    check("forward fits", fwd_lds() <= LDS_PER_CU)
-    check("backward fits", max(dkdv, dq) <= LDS_PER_CU)
-    check("forward default is compiled", FWD_TILES in fwd_configs())
+    print("tilings compiled for gfx950")
+    try:
+        fwd_space, bwd_space = fwd_configs(), bwd_configs()
+    except _lib.LibraryMissing as exc:
+        print(f"    (library not built: {exc})")
+    else:
+        print(f"    forward  {len(fwd_space)}, backward {len(bwd_space)}")
+        check("forward default is compiled", FWD_TILES == fwd_space[0])
+        check("backward default is compiled", BWD_TILES == bwd_space[0])
+        check("every config maps back to its index",
+              all(tile_index("fwd", c) == i for i, c in enumerate(fwd_space))
+              and len({tile_index("bwd", c) for c in bwd_space}) == len(bwd_space))
+        check("waves fit a workgroup", all(c["waves"] * WAVE <= 1024 for c in fwd_space))
 
     print("\nrope")
     rope = Rotary(128, 64, 10_000.0)
@@ -689,13 +802,28 @@ def benchmark(batch=8, seq_len=2048, iters=30):
 
 
 def tune(batch=8, seq_len=2048):
-    """Time every compiled tile variant at one shape and record the winner."""
-    print(f"forward variants  {len(fwd_configs())}")
-    print(f"backward variants {len(bwd_configs())}")
-    for c in fwd_configs():
-        print(f"  fwd {c}")
-    for c in bwd_configs():
-        print(f"  bwd {c}")
+    """Search the compiled tilings at one shape and record the winners
+    (AT:751-769); ``python -m mimansm1_v1_amd.tune`` does every run shape."""
+    try:
+        fwd_space, bwd_space = fwd_configs(), bwd_configs()
+    except _lib.LibraryMissing as exc:
+        print(f"library not built: {exc}")
+        return
+    print(f"forward candidates  {len(fwd_space)}")
+    print(f"backward candidates {len(bwd_space)}")
+    if not torch.cuda.is_available():
+        for name, space in (("forward", fwd_space), ("backward", bwd_space)):
+            print(f"\n{name}")
+            for c in space:
+                print(f"  {c}")
+        return
+    cfg = AttnConfig()
+    shape = (batch, cfg.n_heads, seq_len, cfg.head_dim, True, cfg.groups)
+    for kind in ("fwd", "bwd"):
+        config, latency, _ = autotune(kind, shape, verbose=True)
+        tuned.record(f"attention_{kind}", shape, config)
+        _kernels.pop((kind, shape, AUTOTUNE), None)
+        print(f"\n{kind}: {config}\n     {latency:.3f} ms")
 
 
 if __name__ == "__main__":

@@ -48,17 +48,48 @@ int check_shape(int B, int S, int H, int Hkv, int D) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Kernel variants (see launch_fwd / launch_bwd_dkdv / launch_bwd_dq).
-// MM1_FWD_VARIANT, MM1_DKDV_VARIANT and MM1_DQ_VARIANT select alternative
-// tilings with the same results (tuning, tests); read on every call, so a
-// process can switch between launches.
-int env_variant(const char* name) {
-  const char* e = getenv(name);
-  return e ? atoi(e) : 0;
+// Tilings compiled into the library (the `variant` argument of launch_fwd,
+// launch_bwd_dkdv and launch_bwd_dq).  block_M / block_N name the stationary
+// and the streamed block: query rows x key rows for the forward and dQ, key
+// rows x query rows for dK/dV.
+const char* const kFwdTiles[] = {
+    "block_M=128 block_N=64 waves=4 stages=2 schedule=ring",
+    "block_M=256 block_N=64 waves=8 stages=3 schedule=ring",
+    "block_M=256 block_N=64 waves=8 stages=2 schedule=pingpong",
+};
+const char* const kDkdvTiles[] = {
+    "block_M=128 block_N=32 waves=8 stages=7 schedule=pipelined",
+    "block_M=128 block_N=64 waves=8 stages=3 schedule=paired",
+};
+const char* const kDqTiles[] = {
+    "block_M=128 block_N=64 waves=4 stages=2 schedule=ring",
+    "block_M=256 block_N=64 waves=8 stages=3 schedule=ring",
+};
+
+template <size_t N>
+constexpr int count(const char* const (&)[N]) { return static_cast<int>(N); }
+
+int tile_count(int kind) {
+  switch (kind) {
+    case MM1_TILES_FWD: return count(kFwdTiles);
+    case MM1_TILES_DKDV: return count(kDkdvTiles);
+    case MM1_TILES_DQ: return count(kDqTiles);
+    default: return 0;
+  }
 }
-int fwd_variant() { return env_variant("MM1_FWD_VARIANT"); }
-int dq_variant() { return env_variant("MM1_DQ_VARIANT"); }
-int dkdv_variant() { return env_variant("MM1_DKDV_VARIANT"); }
+
+const char* const kTileEnv[] = {"MM1_FWD_VARIANT", "MM1_DKDV_VARIANT", "MM1_DQ_VARIANT"};
+
+// The tiling to launch: `tiles` itself when >= 0, else the default -- the
+// kind's environment variable if set (read on every call, so a process can
+// switch between launches), otherwise 0.  -1 when out of range.
+int pick_tiles(int kind, int tiles) {
+  if (tiles == -1) {
+    const char* e = getenv(kTileEnv[kind]);
+    tiles = e ? atoi(e) : 0;
+  }
+  return (tiles >= 0 && tiles < tile_count(kind)) ? tiles : -1;
+}
 
 int from_hip(hipError_t e) { return e == hipSuccess ? MM1_OK : static_cast<int>(e); }
 
@@ -68,16 +99,35 @@ extern "C" {
 
 int mm1_attn_version(void) { return MM1_ATTN_VERSION; }
 
-int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
-                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                 void* stream) {
+int mm1_attn_fwd_tiles(const void* q, const void* k, const void* v, void* o, float* lse2,
+                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                       int tiles, void* stream) {
   if (!q || !k || !v || !o || !lse2) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
   if (rc) return rc;
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MM1_E_ALIGN;
-  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale, fwd_variant(),
+  const int variant = pick_tiles(MM1_TILES_FWD, tiles);
+  if (variant < 0) return MM1_E_TILES;
+  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale, variant,
                                   static_cast<hipStream_t>(stream)));
+}
+
+int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
+                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                 void* stream) {
+  return mm1_attn_fwd_tiles(q, k, v, o, lse2, B, S, H, Hkv, D, causal, sm_scale, -1, stream);
+}
+
+int mm1_attn_tile_count(int kind) { return tile_count(kind); }
+
+const char* mm1_attn_tile_desc(int kind, int index) {
+  if (index < 0 || index >= tile_count(kind)) return nullptr;
+  switch (kind) {
+    case MM1_TILES_FWD: return kFwdTiles[index];
+    case MM1_TILES_DKDV: return kDkdvTiles[index];
+    default: return kDqTiles[index];
+  }
 }
 
 int mm1_attn_delta(const void* o, const void* dO, float* delta, int B, int S, int H, int D,
@@ -94,11 +144,11 @@ size_t mm1_attn_bwd_workspace_size(int B, int S, int H, int Hkv, int D) {
   return mm1::bwd_workspace_bytes(B, S, H, Hkv);
 }
 
-int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
-                      const float* lse2, const float* delta, void* dk, void* dv,
-                      void* workspace, size_t workspace_bytes,
-                      int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                      void* stream) {
+static int bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
+                    const float* lse2, const float* delta, void* dk, void* dv,
+                    void* workspace, size_t workspace_bytes,
+                    int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                    int tiles, void* stream) {
   if (!q || !k || !v || !dO || !lse2 || !delta || !dk || !dv) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
   if (rc) return rc;
@@ -108,9 +158,44 @@ int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* d
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dk) ||
       !aligned16(dv) || (need > 0 && !aligned16(workspace)))
     return MM1_E_ALIGN;
+  const int variant = pick_tiles(MM1_TILES_DKDV, tiles);
+  if (variant < 0) return MM1_E_TILES;
   return from_hip(mm1::launch_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, need > 0 ? workspace : nullptr,
-                                       B, S, H, Hkv, causal != 0, sm_scale, dkdv_variant(),
+                                       B, S, H, Hkv, causal != 0, sm_scale, variant,
                                        static_cast<hipStream_t>(stream)));
+}
+
+// dq, and with dk/dv the group sum of the dK/dV partials in the same launch.
+static int bwd_dq(const void* q, const void* k, const void* v, const void* dO,
+                  const float* lse2, const float* delta, void* dq, void* dk, void* dv,
+                  const void* workspace, size_t workspace_bytes, bool reduce,
+                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                  int tiles, void* stream) {
+  if (!q || !k || !v || !dO || !lse2 || !delta || !dq) return MM1_E_NULL;
+  if (reduce && (!dk || !dv)) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
+  const size_t need = reduce ? mm1::bwd_workspace_bytes(B, S, H, Hkv) : 0;
+  if (need > 0 && (!workspace || workspace_bytes < need)) return MM1_E_WORKSPACE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) ||
+      (reduce && (!aligned16(dk) || !aligned16(dv))) || (need > 0 && !aligned16(workspace)))
+    return MM1_E_ALIGN;
+  const int variant = pick_tiles(MM1_TILES_DQ, tiles);
+  if (variant < 0) return MM1_E_TILES;
+  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, need > 0 ? workspace : nullptr,
+                                     reduce ? dk : nullptr, reduce ? dv : nullptr,
+                                     B, S, H, Hkv, causal != 0, sm_scale, variant,
+                                     static_cast<hipStream_t>(stream)));
+}
+
+int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
+                      const float* lse2, const float* delta, void* dk, void* dv,
+                      void* workspace, size_t workspace_bytes,
+                      int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                      void* stream) {
+  return bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes, B, S, H, Hkv, D,
+                  causal, sm_scale, -1, stream);
 }
 
 int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
@@ -130,15 +215,8 @@ int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                     const float* lse2, const float* delta, void* dq,
                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                     void* stream) {
-  if (!q || !k || !v || !dO || !lse2 || !delta || !dq) return MM1_E_NULL;
-  int rc = check_shape(B, S, H, Hkv, D);
-  if (rc) return rc;
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq))
-    return MM1_E_ALIGN;
-  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, nullptr, nullptr, nullptr,
-                                     B, S, H, Hkv, causal != 0, sm_scale, dq_variant(),
-                                     static_cast<hipStream_t>(stream)));
+  return bwd_dq(q, k, v, dO, lse2, delta, dq, nullptr, nullptr, nullptr, 0, false, B, S, H, Hkv, D,
+                causal, sm_scale, -1, stream);
 }
 
 int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const void* dO,
@@ -146,18 +224,26 @@ int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const vo
                            const void* workspace, size_t workspace_bytes,
                            int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                            void* stream) {
-  if (!q || !k || !v || !dO || !lse2 || !delta || !dq || !dk || !dv) return MM1_E_NULL;
-  int rc = check_shape(B, S, H, Hkv, D);
+  return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
+                D, causal, sm_scale, -1, stream);
+}
+
+int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* dO,
+                       const float* lse2, const float* delta,
+                       void* dq, void* dk, void* dv,
+                       void* workspace, size_t workspace_bytes,
+                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                       int dkdv_tiles, int dq_tiles, void* stream) {
+  // What only the second launch checks is checked here, so that an argument
+  // error launches nothing.
+  if (!dq) return MM1_E_NULL;
+  if (!aligned16(dq)) return MM1_E_ALIGN;
+  if (pick_tiles(MM1_TILES_DQ, dq_tiles) < 0) return MM1_E_TILES;
+  int rc = bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes, B, S, H, Hkv, D,
+                    causal, sm_scale, dkdv_tiles, stream);
   if (rc) return rc;
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
-  const size_t need = mm1::bwd_workspace_bytes(B, S, H, Hkv);
-  if (need > 0 && (!workspace || workspace_bytes < need)) return MM1_E_WORKSPACE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) ||
-      !aligned16(dk) || !aligned16(dv) || (need > 0 && !aligned16(workspace)))
-    return MM1_E_ALIGN;
-  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, need > 0 ? workspace : nullptr,
-                                     dk, dv, B, S, H, Hkv, causal != 0, sm_scale, dq_variant(),
-                                     static_cast<hipStream_t>(stream)));
+  return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
+                D, causal, sm_scale, dq_tiles, stream);
 }
 
 int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
@@ -166,12 +252,8 @@ int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
                  void* workspace, size_t workspace_bytes,
                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                  void* stream) {
-  if (!dq) return MM1_E_NULL;
-  int rc = mm1_attn_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes,
-                             B, S, H, Hkv, D, causal, sm_scale, stream);
-  if (rc) return rc;
-  return mm1_attn_bwd_dq_reduce(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes,
-                                B, S, H, Hkv, D, causal, sm_scale, stream);
+  return mm1_attn_bwd_tiles(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes,
+                            B, S, H, Hkv, D, causal, sm_scale, -1, -1, stream);
 }
 
 static int check_qknorm(int B, int S, int H, int Hkv, int D, int rot_len, float eps, bool norm) {
@@ -222,6 +304,7 @@ const char* mm1_attn_strerror(int code) {
     case MM1_E_WORKSPACE: return "mm1_attn: workspace smaller than mm1_attn_bwd_workspace_size()";
     case MM1_E_SCALE: return "mm1_attn: sm_scale must be a positive finite number";
     case MM1_E_ALIGN: return "mm1_attn: tensor pointers must be 16-byte aligned";
+    case MM1_E_TILES: return "mm1_attn: tiling index out of range (see mm1_attn_tile_count)";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -50,7 +50,7 @@ def test_version_matches_header(lib):
 
 def test_error_codes_and_messages(lib):
     codes = dict(re.findall(r"#define (MM1_E_\w+) \((-\d+)\)", HEADER.read_text()))
-    assert len(codes) == 6
+    assert len(codes) == 7
     for name, code in codes.items():
         msg = lib.mm1_attn_strerror(int(code)).decode()
         assert msg.startswith("mm1_attn:") and "unknown" not in msg, name
@@ -139,3 +139,42 @@ def test_qknorm_rope_argument_errors_without_device(lib):
     assert bwd(*args, None, ws, 1, 64, 10, 2, 128, 64, 1e-5, None) == -4
     assert bwd(*args, FAKE, ws - 4, 1, 64, 10, 2, 128, 64, 1e-5, None) == -4
     assert bwd(*args[:9], None, FAKE, FAKE, ws, 1, 64, 10, 2, 128, 64, 1e-5, None) == -1
+
+
+def test_tilings_queries_and_errors_without_device(lib):
+    """The compiled tilings are enumerable; an index out of range is refused
+    before any launch, from both explicit-tiling entries."""
+    counts = [lib.mm1_attn_tile_count(kind) for kind in (0, 1, 2)]
+    assert counts[0] >= 3 and counts[1] >= 2 and counts[2] >= 2
+    assert lib.mm1_attn_tile_count(3) == 0 and lib.mm1_attn_tile_count(-1) == 0
+    for kind, n in enumerate(counts):
+        descs = [lib.mm1_attn_tile_desc(kind, i).decode() for i in range(n)]
+        assert len(set(descs)) == n
+        for d in descs:
+            keys = [item.split("=")[0] for item in d.split()]
+            assert keys == ["block_M", "block_N", "waves", "stages", "schedule"], d
+        assert lib.mm1_attn_tile_desc(kind, n) is None
+        assert lib.mm1_attn_tile_desc(kind, -1) is None
+
+    def fwd_t(tiles, **kw):
+        a = dict(q=FAKE, B=1, S=64, H=10, Hkv=2, D=128)
+        a.update(kw)
+        return lib.mm1_attn_fwd_tiles(a["q"], FAKE, FAKE, FAKE, FAKE, a["B"], a["S"], a["H"],
+                                      a["Hkv"], a["D"], 1, 0.088, tiles, None)
+
+    assert fwd_t(counts[0]) == -7
+    assert fwd_t(-2) == -7
+    assert fwd_t(counts[0], q=None) == -1          # argument checks come first
+    assert fwd_t(0, D=64) == -3
+    need = lib.mm1_attn_bwd_workspace_size(2, 100, 10, 2, 128)
+
+    def bwd_t(dkdv, dq, dq_ptr=FAKE, ws=FAKE):
+        return lib.mm1_attn_bwd_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, dq_ptr, FAKE, FAKE, ws,
+                                      need, 2, 100, 10, 2, 128, 1, 0.088, dkdv, dq, None)
+
+    assert bwd_t(counts[1], 0) == -7
+    assert bwd_t(0, counts[2]) == -7               # refused before the dK/dV launch
+    assert bwd_t(0, 0, dq_ptr=None) == -1
+    assert bwd_t(0, 0, dq_ptr=FAKE + 2) == -6
+    assert bwd_t(0, 0, ws=None) == -4
+    assert b"tiling" in lib.mm1_attn_strerror(-7)

@@ -71,18 +71,30 @@ def test_small_shapes_vs_cpu_oracle(hip_device, shape, causal):
     assert_bf16_close("dV", dv, wv, log)
 
 
-VARIANTS = [("MM1_FWD_VARIANT", 1), ("MM1_FWD_VARIANT", 2), ("MM1_DKDV_VARIANT", 1),
-            ("MM1_DQ_VARIANT", 1)]
+def _tilings():
+    from mimansm1_v1_amd import attention as A
+    return ([("fwd", i) for i in range(1, len(A.fwd_configs()))]
+            + [("bwd", i) for i in range(1, len(A.bwd_configs()))])
 
 
-@pytest.mark.parametrize("env,variant", VARIANTS, ids=[f"{e}={v}" for e, v in VARIANTS])
-def test_kernel_variants_vs_cpu_oracle(hip_device, monkeypatch, env, variant):
-    """The alternative tilings (selected per call by environment variable)
-    meet the same gates as the defaults, causal and full, ragged S."""
-    monkeypatch.setenv(env, str(variant))
+TILINGS = _tilings()
+
+
+@pytest.mark.parametrize("kind,index", TILINGS, ids=[f"{k}{i}" for k, i in TILINGS])
+def test_tilings_vs_cpu_oracle(hip_device, monkeypatch, kind, index):
+    """Every compiled tiling other than the defaults, launched through a kernel
+    handle that carries it (as a tuned record would), meets the same gates as
+    the defaults: causal and full, ragged S, GQA and MHA."""
+    from mimansm1_v1_amd import attention as A
+    config = (A.fwd_configs() if kind == "fwd" else A.bwd_configs())[index]
+    monkeypatch.setattr(A, "_kernels", {})
     for (B, S, H, Hkv), causal in [((2, 300, 10, 2), True), ((1, 200, 6, 3), False), ((1, 77, 4, 4), True)]:
         G = H // Hkv
-        log(f"[case] {env}={variant} B={B} S={S} H={H} Hkv={Hkv} causal={causal}")
+        log(f"[case] {kind} tiling {index} {config} B={B} S={S} H={H} Hkv={Hkv} causal={causal}")
+        shape = (B, H, S, 128, causal, G)
+        for k in ("fwd", "bwd"):
+            tiles = config if k == kind else (A.FWD_TILES if k == "fwd" else A.BWD_TILES)
+            A._kernels[(k, shape, A.AUTOTUNE)] = (A.FwdKernel if k == "fwd" else A.BwdKernel)(shape, tiles)
         q, k, v, do = R.make_inputs(B, S, H, Hkv, 128, seed=3 * S + H)
         o, lse, dq, dk, dv = hip_run(q, k, v, do, causal, G, hip_device)
         wq, wk, wv = R.grads(q, k, v, do, causal, G)
@@ -91,6 +103,84 @@ def test_kernel_variants_vs_cpu_oracle(hip_device, monkeypatch, env, variant):
         assert_bf16_close("dQ", dq, wq, log)
         assert_bf16_close("dK", dk, wk, log)
         assert_bf16_close("dV", dv, wv, log)
+
+
+ENV_TILINGS = [("MM1_FWD_VARIANT", 0, 2), ("MM1_DKDV_VARIANT", 1, 1), ("MM1_DQ_VARIANT", 2, 1)]
+
+
+@pytest.mark.parametrize("env,kind,index", ENV_TILINGS, ids=[e for e, *_ in ENV_TILINGS])
+def test_env_variable_selects_tiling(hip_device, monkeypatch, env, kind, index):
+    """The calls without a tiling argument launch the tiling the environment
+    variable names: bitwise the output of the explicit-tiling call."""
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    B, S, H, Hkv, causal = 1, 333, 10, 2, True
+    log(f"[case] {env}={index} B={B} S={S} H={H} Hkv={Hkv}")
+    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=5))
+    scale = 128 ** -0.5
+    sp = torch.cuda.current_stream(hip_device).cuda_stream
+    p = lambda t: t.data_ptr()
+    nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
+    ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=hip_device)
+
+    def run(explicit):
+        o, lse = torch.empty_like(q), torch.empty(B, H, S, dtype=torch.float32, device=hip_device)
+        delta = torch.empty_like(lse)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        t = [-1, -1, -1]
+        if explicit:
+            t[kind] = index
+        else:
+            monkeypatch.setenv(env, str(index))
+        args = (B, S, H, Hkv, 128, int(causal), scale)
+        if explicit:
+            assert lib.mm1_attn_fwd_tiles(p(q), p(k), p(v), p(o), p(lse), *args, t[0], sp) == 0
+        else:
+            assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), *args, sp) == 0
+        assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+        bwd_args = (p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk), p(dv), p(ws), nws, *args)
+        if explicit:
+            assert lib.mm1_attn_bwd_tiles(*bwd_args, t[1], t[2], sp) == 0
+        else:
+            assert lib.mm1_attn_bwd(*bwd_args, sp) == 0
+        monkeypatch.delenv(env, raising=False)
+        torch.cuda.synchronize()
+        return [x.cpu() for x in (o, lse, dq, dk, dv)]
+
+    for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), run(True), run(False)):
+        assert torch.equal(x, y), name
+
+
+def test_autotune_records_a_compiled_winner(hip_device, monkeypatch, tmp_path):
+    """get_kernel with AUTOTUNE and no record: every tiling is timed, the
+    fastest is recorded under (device, kernel, shape) and the handle uses it;
+    a second lookup is served from the record without a search."""
+    from mimansm1_v1_amd import attention as A
+    from mimansm1_v1_amd import tuned
+    monkeypatch.setattr(tuned, "STORE", tmp_path / "store.json")
+    monkeypatch.setattr(tuned, "TABLE", tmp_path / "none.json")
+    monkeypatch.setattr(A, "_kernels", {})
+    monkeypatch.setattr(A, "AUTOTUNE", True)
+    shape = (1, 10, 640, 128, True, 5)
+    log(f"[case] autotune {shape}")
+    best, ms, results = A.autotune("bwd", shape)
+    assert len(results) == len(A.bwd_configs()) and ms == min(r[0] for r in results) > 0
+    assert A.tile_index("bwd", best) is not None
+    for kind in ("fwd", "bwd"):
+        handle = A.get_kernel(kind, *shape)
+        assert handle.latency is not None and handle.latency > 0
+        assert tuned.lookup(f"attention_{kind}", shape) == handle.config
+    calls = []
+    monkeypatch.setattr(A, "autotune", lambda *a, **k: calls.append(a))
+    monkeypatch.setattr(A, "_kernels", {})
+    assert A.get_kernel("fwd", *shape).latency is None and not calls
+    q, k, v, do = R.make_inputs(1, 640, 10, 2, 128, seed=21)
+    o, lse, dq, dk, dv = hip_run(q, k, v, do, True, 5, hip_device)
+    wq, wk, wv = R.grads(q, k, v, do, True, 5)
+    assert_bf16_close("O", o, R.attention(q, k, v, True, 5, cast=False), log)
+    assert_bf16_close("dQ", dq, wq, log)
+    assert_bf16_close("dK", dk, wk, log)
+    assert_bf16_close("dV", dv, wv, log)
 
 
 def test_config1_forward_vs_cpu_oracle(hip_device):

@@ -96,12 +96,119 @@ def test_attention_flops():
     assert fwd == 2 * 2 * 10 * 8192 ** 2 * 128 and abs((fwd + bwd) - 1202.59e9) < 0.01e9
 
 
-def test_tuned_store_roundtrip(tmp_path, monkeypatch):
-    monkeypatch.setattr(tuned, "STORE", tmp_path / "tiles.json")
-    assert tuned.lookup("attention_fwd", (1, 10, 64, 128, True, 5)) is None
-    tuned.record("attention_fwd", (1, 10, 64, 128, True, 5), {"rows_per_wave": 32})
-    assert tuned.lookup("attention_fwd", (1, 10, 64, 128, True, 5)) == {"rows_per_wave": 32}
-    assert json.loads((tmp_path / "tiles.json").read_text())
+def test_tuned_store_roundtrip_and_precedence(tmp_path, monkeypatch):
+    """Nested device -> "kernel:shape" -> config records (tuned.py:45-74); the
+    machine's own store wins over the shipped table; other devices miss."""
+    monkeypatch.setattr(tuned, "STORE", tmp_path / "store.json")
+    monkeypatch.setattr(tuned, "TABLE", tmp_path / "table.json")
+    shape = (1, 10, 64, 128, True, 5)
+    assert tuned.lookup("attention_fwd", shape, device="gfx950-256cu") is None
+    tuned.record("attention_fwd", shape, dict(A.FWD_TILES), device="gfx950-256cu",
+                 store=tmp_path / "table.json")
+    assert tuned.lookup("attention_fwd", shape, device="gfx950-256cu") == A.FWD_TILES
+    other = dict(A.FWD_TILES, waves=8)
+    tuned.record("attention_fwd", shape, other, device="gfx950-256cu")
+    assert tuned.lookup("attention_fwd", shape, device="gfx950-256cu") == other
+    assert tuned.lookup("attention_fwd", shape, device="gfx942-304cu") is None
+    tuned.record("attention_fwd", (2,), {}, device="gfx950-256cu")      # empty: ignored
+    data = json.loads((tmp_path / "store.json").read_text())
+    assert list(data) == ["gfx950-256cu"]
+    assert list(data["gfx950-256cu"]) == ["attention_fwd:1,10,64,128,True,5"]
+    text = tuned.summary()
+    assert "gfx950-256cu  (1 kernels)" in text and "waves=8" in text
+    assert tuned.config_of(A.FwdKernel(shape, A.FWD_TILES)) == A.FWD_TILES
+    assert tuned.device_key() == "no-hip"
+
+
+def test_tile_space_matches_library_and_defaults():
+    """The configs are the library's own descriptions; index 0 is the default
+    and every config maps back to its index."""
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    fwd, bwd = A.fwd_configs(), A.bwd_configs()
+    assert A.FWD_TILES == fwd[0] and A.BWD_TILES == bwd[0]
+    assert len(fwd) == lib.mm1_attn_tile_count(0) >= 2
+    assert len(bwd) == lib.mm1_attn_tile_count(1) * lib.mm1_attn_tile_count(2)
+    assert [A.tile_index("fwd", c) for c in fwd] == list(range(len(fwd)))
+    pairs = [A.tile_index("bwd", c) for c in bwd]
+    assert sorted(pairs) == [(i, j) for i in range(lib.mm1_attn_tile_count(1))
+                             for j in range(lib.mm1_attn_tile_count(2))]
+    assert all(c["block_N"] == 64 and c["waves"] in (4, 8) for c in fwd)
+    # a config naming no compiled tiling: rejected by the handle, index None
+    assert A.tile_index("fwd", dict(A.FWD_TILES, block_M=96)) is None
+    assert A.tile_index("bwd", dict(A.BWD_TILES, extra=1)) is None
+    assert A.tile_index("bwd", {k: v for k, v in A.BWD_TILES.items() if k != "dq_waves"}) is None
+    with pytest.raises(ValueError, match="not a tiling"):
+        A.FwdKernel((1, 10, 64, 128, True, 5), dict(A.FWD_TILES, stages=9))
+    assert A.get_kernel("bwd", 1, 10, 64, 128, True, 5).tiles == (0, 0)
+
+
+def test_get_kernel_uses_record_and_ignores_stale_one(tmp_path, monkeypatch):
+    monkeypatch.setattr(tuned, "STORE", tmp_path / "store.json")
+    monkeypatch.setattr(tuned, "TABLE", tmp_path / "none.json")
+    monkeypatch.setattr(tuned, "device_key", lambda: "gfx950-256cu")
+    monkeypatch.setattr(A, "_kernels", {})
+    shape = (3, 10, 96, 128, True, 5)
+    tuned.record("attention_fwd", shape, A.fwd_configs()[2])
+    tuned.record("attention_bwd", shape, dict(A.BWD_TILES, dq_stages=11))   # not compiled
+    assert A.get_kernel("fwd", *shape).tiles == 2
+    assert A.get_kernel("bwd", *shape).config == A.BWD_TILES     # no GPU: defaults
+
+
+def test_shipped_tile_table_names_compiled_tilings():
+    """The measured gfx950 table covers both run shapes, fwd and bwd, and every
+    entry is a tiling this build has."""
+    from mimansm1_v1_amd import tune as T
+    data = json.loads(tuned.TABLE.read_text())
+    assert data, "empty shipped table"
+    cfg = A.AttnConfig()
+    for device, entries in data.items():
+        assert device.startswith("gfx950-"), device
+        for _, micro, seq in T.stage_shapes():
+            for name, kind, shape in T.jobs(micro, seq, cfg):
+                key = f"{name}:{','.join(str(x) for x in shape)}"
+                assert key in entries, (device, key)
+                assert A.tile_index(kind, entries[key]) is not None, (key, entries[key])
+
+
+def test_tune_cli_shapes_and_control_flow():
+    """stage_shapes follows the stage switch (tune.py:30-46): 8 x 2048 then
+    2 x 8192; tune_all skips known entries unless forced, records each
+    winner, and carries on past a failing job."""
+    from mimansm1_v1_amd import tune as T
+    assert T.stage_shapes() == [("foundation", 8, 2048), ("long_ctx", 2, 8192)]
+    assert T.stage_shapes(4, 4096) == [("foundation", 8, 2048), ("long_ctx", 2, 8192)]
+    cfg = A.AttnConfig()
+    known, recorded, lines = {}, [], []
+
+    def search(kind, shape):
+        if kind == "bwd" and shape[2] == 8192:
+            raise RuntimeError("boom")
+        return (A.FWD_TILES if kind == "fwd" else A.BWD_TILES), 1.5
+
+    def record(name, shape, config):
+        recorded.append((name, shape))
+        known[(name, shape)] = config
+
+    hooks = dict(lookup=lambda n, s: known.get((n, s)), search=search, record=record,
+                 out=lines.append)
+    done = T.tune_all(8, 2048, cfg, **hooks)
+    assert set(done) == {"attention_fwd", "attention_bwd"} and all(done.values())
+    assert recorded == [("attention_fwd", (8, 10, 2048, 128, True, 5)),
+                        ("attention_bwd", (8, 10, 2048, 128, True, 5))]
+    assert T.tune_all(8, 2048, cfg, **hooks) == {"attention_fwd": None, "attention_bwd": None}
+    assert sum("already known" in x for x in lines) == 2
+    T.tune_all(8, 2048, cfg, force=True, **hooks)
+    assert len(recorded) == 4
+    done = T.tune_all(2, 8192, cfg, **hooks)
+    assert done["attention_fwd"] and done["attention_bwd"] is None
+    assert any("FAILED" in x and "boom" in x for x in lines)
+
+
+def test_tune_cli_refuses_without_gpu():
+    r = subprocess.run([sys.executable, "-m", "mimansm1_v1_amd.tune"], cwd=ROOT,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "needs the gpu" in r.stderr
 
 
 def test_bench_refuses_multi_gpu():
