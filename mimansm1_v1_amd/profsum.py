@@ -23,6 +23,7 @@ from collections import defaultdict
 
 SHORT = {
     "attn_fwd_kernel": "fwd",
+    "attn_fwd_pp_kernel": "fwd",
     "attn_dkdv_pipe_kernel": "dkdv",
     "attn_dkdv_kernel": "dkdv",
     "attn_dq_kernel": "dq",
@@ -50,6 +51,15 @@ def counter_means(path: str):
     return {k: sum(v) / len(v) for k, v in vals.items()}
 
 
+def counter_table(path: str):
+    """{kernel: {counter: mean per dispatch}} of a --pmc CSV with any counters."""
+    vals = defaultdict(lambda: defaultdict(list))
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            vals[kernel_key(r["Kernel_Name"])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in vals.items()}
+
+
 def copy_kib(path: str) -> float:
     with open(path, newline="") as f:
         return max(float(r["Counter_Value"]) for r in csv.DictReader(f))
@@ -64,6 +74,8 @@ def main(argv=None):
     ap.add_argument("--copy-write")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--json", help="write {short kernel name: HBM bytes per launch} here")
+    ap.add_argument("--pmc", nargs="+", default=[],
+                    help="LABEL=CSV ...: per-kernel means of every counter in each --pmc CSV")
     args = ap.parse_args(argv)
 
     if args.trace:
@@ -94,6 +106,20 @@ def main(argv=None):
             with open(args.json, "w") as f:
                 json.dump(traffic, f, indent=1)
                 f.write("\n")
+
+
+    if args.pmc:
+        rows, names = [], []
+        for item in args.pmc:
+            label, path = item.split("=", 1)
+            for k, cs in sorted(counter_table(path).items()):
+                if k in SHORT:
+                    rows.append((label, k, cs))
+                    names += [c for c in cs if c not in names]
+        print("| run | kernel | " + " | ".join(names) + " |")
+        print("|---|---|" + "---:|" * len(names))
+        for label, k, cs in rows:
+            print(f"| {label} | `{k}` | " + " | ".join(f"{cs[c]:,.0f}" if c in cs else "" for c in names) + " |")
 
 
 if __name__ == "__main__":
