@@ -55,6 +55,10 @@ def parse(argv=None):
     ap.add_argument("--also", type=int, nargs="*", default=[2, 5],
                     help="extra configs reported beside the main one (5 = the attention sublayer)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-ffn", action="store_true",
+                    help="skip the SwiGLU feed-forward leg (reported beside the attention line)")
+    ap.add_argument("--ffn-tokens", type=int, default=16384,
+                    help="tokens of the SwiGLU leg (8 x 2048, the reference benchmark's default)")
     ap.add_argument("--no-autograd", action="store_true", help="skip the autograd cross-check")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run --steps device-to-device copies of MIB MiB (a plain copy "
@@ -313,6 +317,67 @@ def time_sublayer(batch, seq, device, steps, warmup):
     }
 
 
+def time_swiglu(tokens, device, steps, warmup):
+    """The SwiGLU feed-forward (d_model 1280, ffn 3328) on `tokens` tokens:
+    fused_swiglu forward + backward (autograd, bf16), and its two HIP kernels
+    alone through the C ABI on preallocated buffers: the gate/up GEMM with the
+    SwiGLU epilogue (training mode: gate, up, act out) and the gradient
+    kernel.  Inputs ~ N(0,1), weights ~ N(0, 0.02^2), synthetic."""
+    import torch
+    from mimansm1_v1_amd import _lib
+    from mimansm1_v1_amd import swiglu as SG
+    cfg = SG.FFNConfig()
+    T, d, Fh = tokens, cfg.d_model, cfg.ffn_hidden
+    gen = torch.Generator().manual_seed(0)
+    mk = lambda *shape, s=1.0: (torch.randn(*shape, generator=gen) * s).to(torch.bfloat16).to(device)
+    x, wg, wu, wd = mk(T, d), mk(d, Fh, s=0.02), mk(d, Fh, s=0.02), mk(Fh, d, s=0.02)
+    go = mk(T, d)
+    leaves = [t.clone().requires_grad_(True) for t in (x, wg, wu, wd)]
+
+    def full():
+        SG.fused_swiglu(*leaves).backward(go)
+        for t in leaves:
+            t.grad = None
+
+    lib = _lib.load()
+    sp = torch.cuda.current_stream(device).cuda_stream
+    gate, up, act = (torch.empty(T, Fh, dtype=torch.bfloat16, device=device) for _ in range(3))
+    dgu = torch.empty(T, 2 * Fh, dtype=torch.bfloat16, device=device)
+    dact = mk(T, Fh)
+
+    def gate_up():
+        _lib.check(lib.mm1_swiglu_gate_up(x.data_ptr(), wg.data_ptr(), wu.data_ptr(), gate.data_ptr(),
+                                          up.data_ptr(), act.data_ptr(), T, d, Fh, SG.MODE_TRAIN, sp),
+                   "mm1_swiglu_gate_up")
+
+    def grad():
+        _lib.check(lib.mm1_swiglu_grad(dact.data_ptr(), gate.data_ptr(), up.data_ptr(), dgu.data_ptr(),
+                                       dgu.data_ptr() + 2 * Fh, T, Fh, 2 * Fh, sp), "mm1_swiglu_grad")
+
+    ms_full = _timed(full, steps, warmup)
+    ms_gu = _timed(gate_up, steps, warmup)
+    ms_grad = _timed(grad, steps, warmup)
+    gu_flops = 4.0 * T * d * Fh
+    gu_bytes = 2.0 * (T * d + 2 * d * Fh + 3 * T * Fh)
+    grad_bytes = 2.0 * 5 * T * Fh
+    return {
+        "tokens": T, "d_model": d, "ffn": Fh,
+        "ms_per_step": round(ms_full, 4),
+        "tflops": round(SG.swiglu_flops(T, cfg) / (ms_full * 1e-3) / 1e12, 2),
+        "gate_up_ms": round(ms_gu, 4),
+        "gate_up_tflops": round(gu_flops / (ms_gu * 1e-3) / 1e12, 2),
+        "gate_up_frac_of_peak": round(gu_flops / (ms_gu * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "gate_up_hbm_gbps": round(gu_bytes / (ms_gu * 1e-3) / 1e9, 1),
+        "grad_ms": round(ms_grad, 4),
+        "grad_gbps": round(grad_bytes / (ms_grad * 1e-3) / 1e9, 1),
+        "grad_frac_of_hbm": round(grad_bytes / (ms_grad * 1e-3) / 1e12 / HBM_TBPS, 4),
+        "note": "fwd+bwd flops 18*T*d*F (3 GEMMs forward, 6 backward, as swiglu_tilelang.benchmark "
+                "counts); gate_up = the fused gate/up GEMM + SwiGLU epilogue kernel (4*T*d*F flops, "
+                "gate/up/act written); grad = the elementwise gradient kernel (3 reads + 2 writes of "
+                "T*F bf16)",
+    }
+
+
 def cpu_baseline(seq):
     """fp32 reference math (oracle restatement of AT:521-530, autograd backward)
     on one KV group (5 query heads, 1 KV head) of one batch element, full seq."""
@@ -413,6 +478,15 @@ def main(argv=None):
               f"stages {', '.join(f'{k} {v:.3f}' for k, v in stages.items())}",
               file=sys.stderr, flush=True)
 
+    ffn_res = None
+    if not args.no_ffn:
+        ffn_res = time_swiglu(args.ffn_tokens, device, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+        print(f"[bench] swiglu: {ffn_res['ms_per_step']:.3f} ms/step, {ffn_res['tflops']:.1f} TFLOP/s; "
+              f"gate_up {ffn_res['gate_up_ms']:.3f} ms ({ffn_res['gate_up_tflops']:.1f} TFLOP/s), "
+              f"grad {ffn_res['grad_ms']:.3f} ms ({ffn_res['grad_gbps']:.0f} GB/s)",
+              file=sys.stderr, flush=True)
+
     main_res = results[args.config]
     B, S = CONFIGS[args.config]["batch"], CONFIGS[args.config]["seq"]
     dom = max(("fwd", "dkdv", "dq"), key=lambda k: main_res["stage_ms"][k])
@@ -478,6 +552,8 @@ def main(argv=None):
             "fwd_tflops": round(res["fwd_tflops"], 2), "bwd_tflops": round(res["bwd_tflops"], 2),
             "stage_ms": {k: round(v, 4) for k, v in res["stage_ms"].items()},
         }
+    if ffn_res is not None:
+        out["swiglu"] = ffn_res
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(S)
     else:

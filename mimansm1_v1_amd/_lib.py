@@ -43,6 +43,8 @@ SIGNATURES = {
     "mm1_qknorm_rope_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _c_size, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                      _c_float, _vp]),
+    "mm1_swiglu_gate_up": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "mm1_swiglu_grad": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, ctypes.c_long, _vp]),
     "mm1_attn_strerror": (ctypes.c_char_p, [_c_int]),
 }
 

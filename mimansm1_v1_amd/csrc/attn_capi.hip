@@ -4,6 +4,7 @@
 #include <stdlib.h>
 
 #include "../../include/mm1_attn.h"
+#include "../../include/mm1_swiglu.h"
 #include "mm1_common.h"
 
 namespace mm1 {
@@ -28,6 +29,10 @@ size_t qknorm_bwd_workspace_bytes();
 hipError_t launch_qknorm_fwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
                              const float* sin_t, void* q, void* k, void* v, int B, int S, int H, int Hkv,
                              float eps, hipStream_t stream);
+hipError_t launch_swiglu_gate_up(const void* x, const void* wg, const void* wu, void* gate, void* up,
+                                 void* act, int T, int d, int F, int mode, hipStream_t stream);
+hipError_t launch_swiglu_grad(const void* dact, const void* gate, const void* up, void* dgate, void* dup,
+                              int T, int F, long ld_out, hipStream_t stream);
 hipError_t launch_qknorm_bwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
                              const float* sin_t, const void* dq, const void* dk, const void* dv,
                              void* dqkv, float* dwq, float* dwk, void* workspace, int B, int S, int H,
@@ -293,6 +298,43 @@ int mm1_qknorm_rope_bwd(const void* qkv, const float* wq, const float* wk, const
     return MM1_E_ALIGN;
   return from_hip(mm1::launch_qknorm_bwd(qkv, wq, wk, cos_t, sin_t, dq, dk, dv, dqkv, dwq, dwk,
                                          workspace, B, S, H, Hkv, eps, static_cast<hipStream_t>(stream)));
+}
+
+// Largest token count: keeps T * ffn / 8 and the row arithmetic well inside
+// the kernels' integer ranges.
+constexpr long kMaxTokens = 1L << 26;
+
+static int check_swiglu_shape(int T, int d, int F) {
+  if (T < 1 || (long)T > kMaxTokens || d < 128 || d % 128 != 0 || F < 128 || F % 128 != 0)
+    return MM1_E_SHAPE;
+  // 32-bit byte offsets inside x and the weights (the kernel's DMA addressing)
+  if ((long)T * d >= (1L << 30) || (long)d * F >= (1L << 30) || (long)T * F > (1L << 40)) return MM1_E_SHAPE;
+  return MM1_OK;
+}
+
+int mm1_swiglu_gate_up(const void* x, const void* w_gate, const void* w_up, void* gate, void* up,
+                       void* act, int T, int d_model, int ffn, int mode, void* stream) {
+  if (mode < MM1_SWIGLU_ACT || mode > MM1_SWIGLU_TRAIN) return MM1_E_SHAPE;
+  const bool split = mode != MM1_SWIGLU_ACT, with_act = mode != MM1_SWIGLU_SPLIT;
+  if (!x || !w_gate || !w_up || (split && (!gate || !up)) || (with_act && !act)) return MM1_E_NULL;
+  int rc = check_swiglu_shape(T, d_model, ffn);
+  if (rc) return rc;
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || (split && (!aligned16(gate) || !aligned16(up))) ||
+      (with_act && !aligned16(act)))
+    return MM1_E_ALIGN;
+  return from_hip(mm1::launch_swiglu_gate_up(x, w_gate, w_up, gate, up, act, T, d_model, ffn, mode,
+                                             static_cast<hipStream_t>(stream)));
+}
+
+int mm1_swiglu_grad(const void* d_act, const void* gate, const void* up, void* d_gate, void* d_up,
+                    int T, int ffn, long ld_out, void* stream) {
+  if (!d_act || !gate || !up || !d_gate || !d_up) return MM1_E_NULL;
+  if (T < 1 || (long)T > kMaxTokens || ffn < 8 || ffn % 8 != 0 || ld_out < ffn || ld_out % 8 != 0)
+    return MM1_E_SHAPE;
+  if (!aligned16(d_act) || !aligned16(gate) || !aligned16(up) || !aligned16(d_gate) || !aligned16(d_up))
+    return MM1_E_ALIGN;
+  return from_hip(mm1::launch_swiglu_grad(d_act, gate, up, d_gate, d_up, T, ffn, ld_out,
+                                          static_cast<hipStream_t>(stream)));
 }
 
 const char* mm1_attn_strerror(int code) {

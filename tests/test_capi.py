@@ -13,12 +13,16 @@ from mimansm1_v1_amd import _lib
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "mm1_attn.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 FAKE = 1 << 20  # aligned, non-null; never dereferenced (calls fail validation first)
 
 
 def declared_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(mm1_\w+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(mm1_\w+)\s*\(", text))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")
@@ -178,3 +182,32 @@ def test_tilings_queries_and_errors_without_device(lib):
     assert bwd_t(0, 0, dq_ptr=FAKE + 2) == -6
     assert bwd_t(0, 0, ws=None) == -4
     assert b"tiling" in lib.mm1_attn_strerror(-7)
+
+
+def test_swiglu_argument_errors_without_device(lib):
+    """The SwiGLU entries reject bad arguments before any launch."""
+    def gu(x=FAKE, gate=FAKE, up=FAKE, act=FAKE, T=256, d=1280, F=3328, mode=2):
+        return lib.mm1_swiglu_gate_up(x, FAKE, FAKE, gate, up, act, T, d, F, mode, None)
+
+    assert gu(x=None) == -1
+    assert gu(act=None) == -1                 # the training mode writes act
+    assert gu(gate=None, mode=1) == -1
+    assert gu(d=1000) == -2                   # d_model not a multiple of 128
+    assert gu(F=3300) == -2                   # ffn not a multiple of 128
+    assert gu(F=3264) == -2
+    assert gu(T=0) == -2
+    assert gu(mode=3) == -2
+    assert gu(up=FAKE + 2, mode=1) == -6
+    # unused outputs may be NULL and are not checked
+    assert gu(gate=None, up=None, act=FAKE + 2, mode=0) == -6
+
+    def grad(ld=3328, **kw):
+        a = dict(da=FAKE, dg=FAKE, T=256, F=3328)
+        a.update(kw)
+        return lib.mm1_swiglu_grad(a["da"], FAKE, FAKE, a["dg"], FAKE, a["T"], a["F"], ld, None)
+
+    assert grad(da=None) == -1
+    assert grad(ld=3320) == -2                # ld_out < ffn
+    assert grad(ld=6660) == -2                # not a multiple of 8
+    assert grad(F=3324) == -2
+    assert grad(dg=FAKE + 8) == -6

@@ -276,3 +276,81 @@ def test_qknorm_rope_column_split():
     w = torch.ones(128)
     qn, _, _ = R.qknorm_rope(qkv, w, w, cos, sin, 6, 3)
     assert torch.allclose(qn.pow(2).mean(-1), torch.ones(2, 9, 6), rtol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU oracle (oracle/swiglu.py)
+from oracle import swiglu as SW  # noqa: E402
+
+
+def _ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |x| (8 significant bits)."""
+    e = torch.floor(torch.log2(x.abs().clamp(min=2.0 ** -126)))
+    return torch.pow(2.0, e - 7)
+
+
+def test_swiglu_manual_grads_match_fp64_autograd():
+    """FusedSwiGLU.backward's formulas against autograd (the reference's own
+    check, swiglu_tilelang.py:426-462), in fp64."""
+    gen = torch.Generator().manual_seed(1)
+    m, d, h = 32, 64, 96
+    x = torch.randn(m, d, generator=gen, dtype=torch.float64)
+    wg = torch.randn(d, h, generator=gen, dtype=torch.float64) * 0.1
+    wu = torch.randn(d, h, generator=gen, dtype=torch.float64) * 0.1
+    wd = torch.randn(h, d, generator=gen, dtype=torch.float64) * 0.1
+    go = torch.randn(m, d, generator=gen, dtype=torch.float64)
+    auto = SW.grads(x, wg, wu, wd, go, dtype=torch.float64)
+    manual = SW.manual_grads(x, wg, wu, wd, go)
+    assert torch.allclose(auto[0], SW.reference(x, wg, wu, wd).double(), rtol=1e-6, atol=1e-6)
+    for a, b in zip(manual, auto[1:]):
+        assert ((a - b).abs().max() / b.abs().max()).item() < 1e-10
+
+
+def test_swiglu_grad_oracle_is_the_derivative():
+    """grad() equals autograd of silu(g) * u (fp64) rounded to bf16, to one
+    bf16 ulp; a dropped (1 + g(1 - s)) factor is caught."""
+    gen = torch.Generator().manual_seed(2)
+    a, g, u = (torch.randn(64, 96, generator=gen).mul(s).to(torch.bfloat16) for s in (1.0, 3.0, 2.0))
+    gd, ud = g.double().requires_grad_(True), u.double().requires_grad_(True)
+    (F.silu(gd) * ud).backward(a.double())
+    dg, du = SW.grad(a, g, u)
+    for got, want in ((dg, gd.grad), (du, ud.grad)):
+        err = (got.double() - want).abs()
+        assert (err <= _ulp_bf16(want) + 1e-30).all()
+    s = torch.sigmoid(g.float())
+    wrong = (a.float() * u.float() * s).to(torch.bfloat16)          # missing (1 + g (1 - s))
+    assert (wrong.double() - gd.grad).abs().max() > 0.1
+
+
+def test_swiglu_silu_derivative_closed_form():
+    """The reference's checks (swiglu_tilelang.py:413-424)."""
+    z = (torch.randn(2000, dtype=torch.float64) * 3).requires_grad_(True)
+    F.silu(z).sum().backward()
+    s = torch.sigmoid(z.detach())
+    assert (z.grad - s * (1 + z.detach() * (1 - s))).abs().max() < 1e-12
+    assert F.silu(torch.zeros(1)).item() == 0.0 and torch.sigmoid(torch.zeros(1)).item() == 0.5
+
+
+def test_swiglu_forward_oracles_round_once():
+    """split / act_fused are the fp64 products rounded once (to one bf16 ulp:
+    the oracle accumulates in fp32); act_train is F.silu(gate) * up on bf16."""
+    x, wg, wu, _, _ = SW.make_inputs(48, d_model=128, ffn=64, seed=3)
+    g64, u64 = x.double() @ wg.double(), x.double() @ wu.double()
+    gate, up = SW.split(x, wg, wu)
+    for got, want in ((gate, g64), (up, u64)):
+        assert ((got.double() - want).abs() <= _ulp_bf16(want) + 1e-30).all()
+    act = SW.act_fused(x, wg, wu)
+    want = g64 * torch.sigmoid(g64) * u64
+    assert ((act.double() - want).abs() <= _ulp_bf16(want) + 1e-12).all()
+    assert torch.equal(SW.act_train(gate, up), F.silu(gate) * up)
+    assert torch.equal(SW.act_train(gate, up), (F.silu(gate.float()).to(torch.bfloat16) * up))
+
+
+def test_swiglu_reference_matches_module_math_backend():
+    from mimansm1_v1_amd import swiglu as S
+    torch.manual_seed(0)
+    cfg = S.FFNConfig(d_model=256, ffn_hidden=384)
+    ffn = S.SwiGLU(cfg)
+    x = torch.randn(3, 5, 256)
+    want = SW.reference(x.reshape(-1, 256), ffn.w_gate, ffn.w_up, ffn.w_down).reshape(3, 5, 256)
+    assert (ffn(x, backend="math") - want).abs().max() < 1e-6
