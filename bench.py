@@ -57,6 +57,8 @@ def parse(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-ffn", action="store_true",
                     help="skip the SwiGLU feed-forward leg (reported beside the attention line)")
+    ap.add_argument("--no-head", action="store_true",
+                    help="skip the fused cross-entropy head leg (reported beside the attention line)")
     ap.add_argument("--ffn-tokens", type=int, default=16384,
                     help="tokens of the SwiGLU leg (8 x 2048, the reference benchmark's default)")
     ap.add_argument("--no-autograd", action="store_true", help="skip the autograd cross-check")
@@ -378,6 +380,65 @@ def time_swiglu(tokens, device, steps, warmup):
     }
 
 
+def time_lm_head(tokens, device, steps, warmup):
+    """The fused cross-entropy head (d_model 1280, vocabulary 49,152) on
+    `tokens` tokens: fused_cross_entropy forward + backward (whole-vocabulary
+    chunk), and its two GEMM-pass kernels alone through the C ABI: the
+    log-sum-exp pass (with target logits and per-token losses) and the
+    d_logits pass.  hidden ~ N(0, 0.1^2), weight ~ N(0, 0.02^2) (the
+    reference benchmark's scales), uniform targets; synthetic."""
+    import torch
+    from mimansm1_v1_amd import _lib
+    from mimansm1_v1_amd import lm_head as LH
+    cfg = LH.HeadConfig()
+    T, d, V = tokens, cfg.d_model, cfg.vocab
+    gen = torch.Generator().manual_seed(0)
+    hidden = (torch.randn(T, d, generator=gen) * 0.1).to(torch.bfloat16).to(device)
+    weight = (torch.randn(d, V, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    targets = torch.randint(0, V, (T,), generator=gen).to(device)
+    h_leaf, w_leaf = hidden.clone().requires_grad_(True), weight.clone().requires_grad_(True)
+
+    def full():
+        LH.fused_cross_entropy(h_leaf, w_leaf, targets).backward()
+        h_leaf.grad = w_leaf.grad = None
+
+    lib = _lib.load()
+    sp = torch.cuda.current_stream(device).cuda_stream
+    lse, tl, loss = (torch.empty(T, dtype=torch.float32, device=device) for _ in range(3))
+    ws_bytes = lib.mm1_lm_head_workspace_size(T, V)
+    ws = torch.empty(ws_bytes // 4 + 1, dtype=torch.float32, device=device)
+    scale = torch.tensor([1.0 / T], device=device)
+    dl = torch.empty(T, V, dtype=torch.bfloat16, device=device)
+
+    def lse_pass():
+        _lib.check(lib.mm1_lm_head_lse(hidden.data_ptr(), weight.data_ptr(), targets.data_ptr(), -100,
+                                       lse.data_ptr(), tl.data_ptr(), loss.data_ptr(), ws.data_ptr(), ws_bytes,
+                                       T, d, V, sp), "mm1_lm_head_lse")
+
+    def dlogits_pass():
+        _lib.check(lib.mm1_lm_head_dlogits(hidden.data_ptr(), weight.data_ptr(), targets.data_ptr(), -100,
+                                           lse.data_ptr(), scale.data_ptr(), dl.data_ptr(), V, T, d, V, 0, V,
+                                           sp), "mm1_lm_head_dlogits")
+
+    ms_full = _timed(full, steps, warmup)
+    ms_lse = _timed(lse_pass, steps, warmup)
+    ms_dl = _timed(dlogits_pass, steps, warmup)
+    unit = 2.0 * T * d * V
+    return {
+        "tokens": T, "d_model": d, "vocab": V,
+        "ms_per_step": round(ms_full, 4),
+        "tflops": round(4 * unit / (ms_full * 1e-3) / 1e12, 2),
+        "lse_ms": round(ms_lse, 4),
+        "lse_tflops": round(unit / (ms_lse * 1e-3) / 1e12, 2),
+        "lse_frac_of_peak": round(unit / (ms_lse * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "dlogits_ms": round(ms_dl, 4),
+        "dlogits_tflops": round(unit / (ms_dl * 1e-3) / 1e12, 2),
+        "note": "fwd+bwd flops 4 * 2*T*d*V (log-sum-exp pass; d_logits pass, d_hidden and d_weight "
+                "GEMMs); the [T, V] logits are never stored in the forward; lse = the log-sum-exp "
+                "kernel pass (2*T*d*V flops, partials + combine), dlogits = the d_logits GEMM pass",
+    }
+
+
 def cpu_baseline(seq):
     """fp32 reference math (oracle restatement of AT:521-530, autograd backward)
     on one KV group (5 query heads, 1 KV head) of one batch element, full seq."""
@@ -487,6 +548,15 @@ def main(argv=None):
               f"grad {ffn_res['grad_ms']:.3f} ms ({ffn_res['grad_gbps']:.0f} GB/s)",
               file=sys.stderr, flush=True)
 
+    head_res = None
+    if not args.no_head:
+        head_res = time_lm_head(args.ffn_tokens, device, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+        print(f"[bench] lm head: {head_res['ms_per_step']:.3f} ms/step, {head_res['tflops']:.1f} TFLOP/s; "
+              f"lse {head_res['lse_ms']:.3f} ms ({head_res['lse_tflops']:.1f} TFLOP/s), "
+              f"dlogits {head_res['dlogits_ms']:.3f} ms ({head_res['dlogits_tflops']:.1f} TFLOP/s)",
+              file=sys.stderr, flush=True)
+
     main_res = results[args.config]
     B, S = CONFIGS[args.config]["batch"], CONFIGS[args.config]["seq"]
     dom = max(("fwd", "dkdv", "dq"), key=lambda k: main_res["stage_ms"][k])
@@ -554,6 +624,8 @@ def main(argv=None):
         }
     if ffn_res is not None:
         out["swiglu"] = ffn_res
+    if head_res is not None:
+        out["lm_head"] = head_res
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(S)
     else:

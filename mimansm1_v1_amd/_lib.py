@@ -45,6 +45,11 @@ SIGNATURES = {
                                      _c_float, _vp]),
     "mm1_swiglu_gate_up": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "mm1_swiglu_grad": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, ctypes.c_long, _vp]),
+    "mm1_lm_head_workspace_size": (_c_size, [_c_int, _c_int]),
+    "mm1_lm_head_lse": (_c_int, [_vp, _vp, _vp, ctypes.c_longlong, _vp, _vp, _vp, _vp, _c_size,
+                                 _c_int, _c_int, _c_int, _vp]),
+    "mm1_lm_head_dlogits": (_c_int, [_vp, _vp, _vp, ctypes.c_longlong, _vp, _vp, _vp, ctypes.c_long,
+                                     _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "mm1_attn_strerror": (ctypes.c_char_p, [_c_int]),
 }
 

@@ -5,6 +5,7 @@
 
 #include "../../include/mm1_attn.h"
 #include "../../include/mm1_swiglu.h"
+#include "../../include/mm1_lm_head.h"
 #include "mm1_common.h"
 
 namespace mm1 {
@@ -33,6 +34,13 @@ hipError_t launch_swiglu_gate_up(const void* x, const void* wg, const void* wu, 
                                  void* act, int T, int d, int F, int mode, hipStream_t stream);
 hipError_t launch_swiglu_grad(const void* dact, const void* gate, const void* up, void* dgate, void* dup,
                               int T, int F, long ld_out, hipStream_t stream);
+size_t lm_head_workspace_bytes(int T, int V);
+hipError_t launch_lm_lse(const void* hidden, const void* weight, const long long* targets, long long ignore_index,
+                         float* lse, float* tlogit_out, float* loss, void* workspace, int T, int d, int V,
+                         hipStream_t stream);
+hipError_t launch_lm_dlogits(const void* hidden, const void* weight, const long long* targets,
+                             long long ignore_index, const float* lse, const float* scale, void* dlogits, long ld,
+                             int T, int d, int V, int v0, int vn, hipStream_t stream);
 hipError_t launch_qknorm_bwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
                              const float* sin_t, const void* dq, const void* dk, const void* dv,
                              void* dqkv, float* dwq, float* dwk, void* workspace, int B, int S, int H,
@@ -335,6 +343,44 @@ int mm1_swiglu_grad(const void* d_act, const void* gate, const void* up, void* d
     return MM1_E_ALIGN;
   return from_hip(mm1::launch_swiglu_grad(d_act, gate, up, d_gate, d_up, T, ffn, ld_out,
                                           static_cast<hipStream_t>(stream)));
+}
+
+static int check_lm_shape(int T, int d, int V) {
+  if (T < 1 || (long)T > kMaxTokens || d < 128 || d % 128 != 0 || V < 128 || V % 128 != 0) return MM1_E_SHAPE;
+  // 32-bit byte offsets inside hidden and a 64-row slab of the weight
+  if ((long)T * d >= (1L << 30) || 64L * V >= (1L << 30)) return MM1_E_SHAPE;
+  return MM1_OK;
+}
+
+size_t mm1_lm_head_workspace_size(int T, int vocab) {
+  if (check_lm_shape(T, 128, vocab) != MM1_OK) return 0;
+  return mm1::lm_head_workspace_bytes(T, vocab);
+}
+
+int mm1_lm_head_lse(const void* hidden, const void* weight, const long long* targets, long long ignore_index,
+                    float* lse, float* target_logit, float* loss, void* workspace, size_t workspace_bytes,
+                    int T, int d_model, int vocab, void* stream) {
+  if (!hidden || !weight || !lse) return MM1_E_NULL;
+  if (!targets && (target_logit || loss)) return MM1_E_NULL;
+  int rc = check_lm_shape(T, d_model, vocab);
+  if (rc) return rc;
+  if (!workspace || workspace_bytes < mm1::lm_head_workspace_bytes(T, vocab)) return MM1_E_WORKSPACE;
+  if (!aligned16(hidden) || !aligned16(weight) || !aligned16(workspace)) return MM1_E_ALIGN;
+  return from_hip(mm1::launch_lm_lse(hidden, weight, targets, ignore_index, lse, target_logit, loss, workspace,
+                                     T, d_model, vocab, static_cast<hipStream_t>(stream)));
+}
+
+int mm1_lm_head_dlogits(const void* hidden, const void* weight, const long long* targets, long long ignore_index,
+                        const float* lse, const float* scale, void* d_logits, long ld,
+                        int T, int d_model, int vocab, int v0, int vn, void* stream) {
+  if (!hidden || !weight || !targets || !lse || !scale || !d_logits) return MM1_E_NULL;
+  int rc = check_lm_shape(T, d_model, vocab);
+  if (rc) return rc;
+  if (v0 < 0 || vn < 128 || v0 % 128 != 0 || vn % 128 != 0 || (long)v0 + vn > vocab || ld < vn || ld % 8 != 0)
+    return MM1_E_SHAPE;
+  if (!aligned16(hidden) || !aligned16(weight) || !aligned16(d_logits)) return MM1_E_ALIGN;
+  return from_hip(mm1::launch_lm_dlogits(hidden, weight, targets, ignore_index, lse, scale, d_logits, ld, T,
+                                         d_model, vocab, v0, vn, static_cast<hipStream_t>(stream)));
 }
 
 const char* mm1_attn_strerror(int code) {

@@ -211,3 +211,33 @@ def test_swiglu_argument_errors_without_device(lib):
     assert grad(ld=6660) == -2                # not a multiple of 8
     assert grad(F=3324) == -2
     assert grad(dg=FAKE + 8) == -6
+
+
+def test_lm_head_argument_errors_without_device(lib):
+    """The cross-entropy head entries reject bad arguments before any launch."""
+    ws = lib.mm1_lm_head_workspace_size(256, 49152)
+    assert ws >= 256 * 384 * 8 + 256 * 4
+    assert lib.mm1_lm_head_workspace_size(256, 100) == 0       # vocab not a multiple of 128
+
+    def lse(h=FAKE, tg=FAKE, lse_=FAKE, tl=FAKE, ws_=FAKE, nb=None, T=256, d=1280, V=49152):
+        return lib.mm1_lm_head_lse(h, FAKE, tg, -100, lse_, tl, FAKE, ws_, ws if nb is None else nb,
+                                   T, d, V, None)
+
+    assert lse(h=None) == -1
+    assert lse(lse_=None) == -1
+    assert lse(tg=None) == -1                 # target_logit / loss need targets
+    assert lse(d=1000) == -2
+    assert lse(V=49000) == -2
+    assert lse(ws_=None) == -4
+    assert lse(nb=ws - 8) == -4
+    assert lse(h=FAKE + 2) == -6
+
+    def dl(v0=0, vn=4096, ld=4096, out=FAKE, V=49152):
+        return lib.mm1_lm_head_dlogits(FAKE, FAKE, FAKE, -100, FAKE, FAKE, out, ld, 256, 1280, V, v0, vn, None)
+
+    assert dl(out=None) == -1
+    assert dl(v0=64) == -2                    # chunk start not a multiple of 128
+    assert dl(vn=100) == -2
+    assert dl(v0=49152 - 128, vn=256) == -2   # past the vocabulary
+    assert dl(ld=4000) == -2                  # row stride shorter than the chunk
+    assert dl(out=FAKE + 8) == -6

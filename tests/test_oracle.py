@@ -354,3 +354,66 @@ def test_swiglu_reference_matches_module_math_backend():
     x = torch.randn(3, 5, 256)
     want = SW.reference(x.reshape(-1, 256), ffn.w_gate, ffn.w_up, ffn.w_down).reshape(3, 5, 256)
     assert (ffn(x, backend="math") - want).abs().max() < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# Cross-entropy head oracle (oracle/lm_head.py)
+from oracle import lm_head as LMO  # noqa: E402
+
+
+def test_lm_online_lse_and_lse_match_logsumexp():
+    """The kernel's online recurrence and the oracle's lse against
+    torch.logsumexp (the reference's check, lm_head_tilelang.py:393-406)."""
+    x = torch.randn(64, 5000, dtype=torch.float64) * 8
+    assert (LMO.online_lse(x, 128) - torch.logsumexp(x, dim=1)).abs().max() < 1e-12
+    h = torch.randn(16, 32, dtype=torch.float64)
+    w = torch.randn(32, 300, dtype=torch.float64)
+    assert torch.allclose(LMO.lse(h, w, torch.float64), torch.logsumexp(h @ w, dim=1), rtol=0, atol=1e-12)
+    big = torch.tensor([[1e4, 1e4 + 1.0]], dtype=torch.float64)
+    assert torch.isfinite(LMO.online_lse(big, 1)).all()
+
+
+def test_lm_loss_matches_cross_entropy_with_ignore_index():
+    gen = torch.Generator().manual_seed(4)
+    h = torch.randn(40, 24, generator=gen, dtype=torch.float64)
+    w = torch.randn(24, 256, generator=gen, dtype=torch.float64) * 0.3
+    t = torch.randint(0, 256, (40,), generator=gen)
+    t[:7] = LMO.IGNORE_INDEX
+    want = F.cross_entropy(h @ w, t, ignore_index=LMO.IGNORE_INDEX)
+    assert (LMO.loss(h, w, t, dtype=torch.float64) - want).abs() < 1e-12
+    assert LMO.loss(h, w, torch.full_like(t, LMO.IGNORE_INDEX), dtype=torch.float64).item() == 0.0
+    # planted mistake: averaging over every token instead of the valid ones
+    wrong = (torch.logsumexp(h @ w, 1) - LMO.target_logits(h, w, t, torch.float64))[7:].sum() / 40
+    assert (wrong - want).abs() > 1e-3
+
+
+def test_lm_dlogits_is_the_cross_entropy_gradient():
+    """dlogits = (softmax - onehot) * mask * scale equals autograd of the summed
+    cross entropy times scale (the reference's gradient identity, :420-428);
+    dropping the one-hot is caught."""
+    gen = torch.Generator().manual_seed(5)
+    h = torch.randn(32, 16, generator=gen, dtype=torch.float64)
+    w = torch.randn(16, 128, generator=gen, dtype=torch.float64) * 0.5
+    t = torch.randint(0, 128, (32,), generator=gen)
+    t[3] = LMO.IGNORE_INDEX
+    lg = (h @ w).requires_grad_(True)
+    scale = 0.37
+    (F.cross_entropy(lg, t, ignore_index=LMO.IGNORE_INDEX, reduction="sum") * scale).backward()
+    got = LMO.dlogits(h, w, t, LMO.lse(h, w, torch.float64), scale, dtype=torch.float64)
+    assert (got - lg.grad).abs().max() < 1e-12
+    no_onehot = torch.softmax(h @ w, 1) * (t != LMO.IGNORE_INDEX).unsqueeze(1) * scale
+    assert (no_onehot - lg.grad).abs().max() > 0.1
+
+
+def test_lm_grads_oracle_matches_manual_chain_rule():
+    gen = torch.Generator().manual_seed(6)
+    h = torch.randn(24, 16, generator=gen, dtype=torch.float64)
+    w = torch.randn(16, 256, generator=gen, dtype=torch.float64) * 0.2
+    t = torch.randint(0, 256, (24,), generator=gen)
+    t[:2] = LMO.IGNORE_INDEX
+    loss, dh, dw = LMO.grads(h, w, t, dtype=torch.float64)
+    count = (t != LMO.IGNORE_INDEX).sum()
+    dl = LMO.dlogits(h, w, t, LMO.lse(h, w, torch.float64), 1.0 / count.item(), dtype=torch.float64)
+    assert (dh - dl @ w.t()).abs().max() < 1e-12
+    assert (dw - h.t() @ dl).abs().max() < 1e-12
+    assert (loss - LMO.loss(h, w, t, dtype=torch.float64)).abs() < 1e-12
