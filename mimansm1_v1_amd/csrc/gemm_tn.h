@@ -1,26 +1,30 @@
 // Persistent bf16 GEMM core for gfx950 shared by the SwiGLU and LM-head
 // kernels: D = W^T X^T over token blocks of 256 and column blocks of 256,
-// fp32 accumulation in AGPRs, with the epilogue supplied by the caller.
+// fp32 accumulation, with the epilogue supplied by the caller.
 //
 //   X [T, d] bf16 rows (tokens), W [d, ldw] bf16 rows (k), D[col][token].
 //
-// A workgroup (4 waves, one per SIMD, 1 workgroup per CU) owns 256 tokens x
-// 256 columns and walks k in steps of 64 staged in a two-slot LDS ring (64 KiB
-// per slot) by the LDS DMA:
+// A workgroup (8 waves, two per SIMD, one workgroup per CU) owns 256 tokens
+// x 256 columns and walks k in steps of 64 staged in a two-slot LDS ring (64
+// KiB per slot) by the LDS DMA:
 //   * X: two 64 x 256 B tiles; row r of tile t holds tokens 128t + r (left
 //     half) and 128t + 64 + r (right half), 64 k values each;
 //   * W: two 64 x 256 B tiles, row k of tile t holding the columns
 //       PAIRED  : w0[k][64t .. 64t+63] then w1[k][64t .. 64t+63] (the SwiGLU
 //                 gate and up weights, workgroup column step 128 of each);
 //       !PAIRED : w0[k][128t .. 128t+127] (workgroup column step 256).
-// Wave (wm, wn) accumulates tokens 128wm .. +127 against the four 32-column
-// blocks b of W tile wn: acc[b][i] is the 32 x 32 product of block b and token
-// block i (lane: token 32i + (lane & 31); register 4q + e: column
-// 32b + 8q + 4(lane/32) + e of the tile).  W^T is read with the LDS transpose
-// read in natural k order, X with row reads; both conflict-free on the
-// swizzled tile layout.  Tiles are dealt to the 8 XCDs in contiguous runs of a
-// grouped order (8 token blocks, then the next column block) so an XCD's
-// concurrent tiles share X rows and W columns in its L2.
+// Wave (wm, wn), wm = w & 1, wn = w >> 1 (0..3), accumulates tokens
+// 128wm .. +127 against two 32-column blocks of W tile wn >> 1: PAIRED: w0
+// block wn & 1 (acc[0]) and the same w1 block (acc[1]); !PAIRED: blocks
+// 2(wn & 1) and 2(wn & 1) + 1.  acc[b][i] is the 32 x 32 product of block b
+// and token block i (lane: token 32i + (lane & 31); register 4q + e: column
+// 8q + 4(lane/32) + e of the block).  Two waves per SIMD let one wave's LDS
+// reads run under the other's MFMAs (128 accumulators each).  W^T is read
+// with the LDS transpose read in natural k order, X with row reads; both
+// conflict-free on the swizzled tile layout.  Tiles are dealt to the 8 XCDs
+// in contiguous runs of a grouped order (8 token blocks, then the next
+// column block) so an XCD's concurrent tiles share X rows and W columns in
+// its L2.
 #pragma once
 #include "mm1_common.h"
 
@@ -93,17 +97,15 @@ inline int persistent_grid(int cus, int total_tiles) {
   return grid < cap ? grid : cap;
 }
 
-// The persistent loop of one workgroup; calls epi(mb, nb, acc) after each tile
-// with acc[4][4] as described above.  All 256 threads must call it.
-template <bool PAIRED, class Epi>
-__device__ __forceinline__ void run(const Problem& p, char* smem, Epi&& epi) {
+// The persistent loop of one workgroup (512 threads, all of which must call
+// it); pro(mb, nb) runs at the start of each tile, epi(mb, nb, acc) at its
+// end with acc[2][4] as described above.
+template <bool PAIRED, class Pro, class Epi>
+__device__ __forceinline__ void run(const Problem& p, char* smem, Pro&& pro, Epi&& epi) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w & 1, wn = w >> 1;
   const int wu_ = __builtin_amdgcn_readfirstlane(w);
 
-  // This workgroup's tiles: XCD x = blockIdx % 8 owns tiles [t0, t1) of the
-  // sequence; its workgroups (index blockIdx / 8 among the XCD's n_wg) take
-  // every n_wg-th tile of it.
   const int total = p.n_mblk * p.n_nblk;
   const int xcd = blockIdx.x & 7, n_wg = gridDim.x >> 3;
   const int t0 = (int)(((long)xcd * total) >> 3), t1 = (int)(((long)(xcd + 1) * total) >> 3);
@@ -113,39 +115,30 @@ __device__ __forceinline__ void run(const Problem& p, char* smem, Epi&& epi) {
   const int n_steps = n_mine * n_kt;
   if (n_steps == 0) return;
 
-  // DMA addressing.  Lane L of wave w fills slot (row 16q + 4w + L/16, chunk
-  // L%16) of a tile (q = 0..3); the logical chunk c = (L%16) ^ swz(row) does
-  // not depend on q.  Every copy is a wave-uniform base (scalar registers:
-  // the tensor plus the k offset of the step) and a per-lane 32-bit byte
-  // offset computed once per tile; in the PAIRED layout the two halves of a
-  // weight row quad are two copies with complementary lane masks.
+  // DMA addressing: wave w fills row quads rq = 8q + w (q = 0, 1) of every
+  // tile, rows 32q + 4w + L/16; rq & 3 == w & 3, so the logical chunk
+  // c = (L%16) ^ swz(row) is the same for both quads.
   const int lrow = 4 * w + (lane >> 4);
   const int chunk = (lane & 15) ^ (((lane >> 4) << 2) | (w & 3));
   const int x_tok = lrow + 64 * (chunk >> 3);
   const int c8 = 8 * (chunk & 7);
   const bool first_half = chunk < 8;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-  uint32_t xoff[2][4], woff[2][4];
+  uint32_t xoff[2][2], woff[2][2];
   auto tile_offsets = [&](int tile) {
     int mb, nb;
     tile_coords(tile, p.n_mblk, p.n_nblk, mb, nb);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      int col;
-      if (PAIRED) {
-        col = nb * 128 + 64 * t + c8;
-      } else {
-        col = min(nb * 256 + 128 * t + 8 * chunk, p.ncols - 8);
-      }
+      const int col = PAIRED ? nb * 128 + 64 * t + c8 : min(nb * 256 + 128 * t + 8 * chunk, p.ncols - 8);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int tok = min(mb * BM + 128 * t + 16 * q + x_tok, p.T - 1);
+      for (int q = 0; q < 2; ++q) {
+        const int tok = min(mb * BM + 128 * t + 32 * q + x_tok, p.T - 1);
         xoff[t][q] = (uint32_t)(((long)tok * p.d + c8) * 2);
-        woff[t][q] = (uint32_t)(((long)(16 * q + lrow) * p.ldw + col) * 2);
+        woff[t][q] = (uint32_t)(((long)(32 * q + lrow) * p.ldw + col) * 2);
       }
     }
   };
-  // Stage k block kt of the tile whose offsets are loaded into `slot`.
   auto issue = [&](int kt, int slot) {
     const uint32_t sl = lds0 + slot * SLOT;
     const char* xb = reinterpret_cast<const char*>(p.x) + (long)kt * BK * 2;
@@ -154,75 +147,82 @@ __device__ __forceinline__ void run(const Problem& p, char* smem, Epi&& epi) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        dma16_sbase(xoff[t][q], xb, sl + t * TILE_BYTES + (4 * q + wu_) * 1024);
+      for (int q = 0; q < 2; ++q)
+        dma16_sbase(xoff[t][q], xb, sl + t * TILE_BYTES + (8 * q + wu_) * 1024);
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t dst = sl + (2 + t) * TILE_BYTES + (4 * q + wu_) * 1024;
-        if (!PAIRED || first_half) dma16_sbase(woff[t][q], b0, dst);
-        else dma16_sbase(woff[t][q], b1, dst);
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t dst = sl + (2 + t) * TILE_BYTES + (8 * q + wu_) * 1024;
+        if (PAIRED) {
+          if (first_half) dma16_sbase(woff[t][q], b0, dst);
+          else dma16_sbase(woff[t][q], b1, dst);
+        } else {
+          dma16_sbase(woff[t][q], b0, dst);
+        }
       }
     }
   };
 
   const LdsBases lb = make_lds_bases(lane);
-  const TrNat tn0 = make_tr_nat(lane, 0), tn1 = make_tr_nat(lane, 1), tn2 = make_tr_nat(lane, 2),
-              tn3 = make_tr_nat(lane, 3);
+  const int blk0 = PAIRED ? (wn & 1) : 2 * (wn & 1);
+  const TrNat ta = make_tr_nat(lane, blk0);
+  const TrNat tb = make_tr_nat(lane, PAIRED ? 2 + (wn & 1) : blk0 + 1);
 
-  // Operands of k step kk of a slot: X^T columns (4 token blocks) and W^T
-  // rows (column blocks 0..3 of W tile wn).
   struct Frags {
-    bf16x8 xb[4], w[4];
+    bf16x8 xb[4], w[2];
   };
   auto load_frags = [&](const char* xs, const char* ws, int kk, Frags& f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       f.xb[i] = *reinterpret_cast<const bf16x8*>(xs + (i & 1) * 8192 + (lb.row ^ (128 * (i >> 1) + 32 * kk)));
-    f.w[0] = tr_nat(ws, tn0, kk);
-    f.w[1] = tr_nat(ws, tn1, kk);
-    f.w[2] = tr_nat(ws, tn2, kk);
-    f.w[3] = tr_nat(ws, tn3, kk);
+    f.w[0] = tr_nat(ws, ta, kk);
+    f.w[1] = tr_nat(ws, tb, kk);
   };
 
-  tile_offsets(first);
-  issue(0, 0);
+  int iss_ti = 0, iss_kt = 0;
+  auto issue_next = [&](int slot) {
+    if (iss_kt == 0) tile_offsets(first + iss_ti * n_wg);
+    issue(iss_kt, slot);
+    if (++iss_kt == n_kt) {
+      iss_kt = 0;
+      ++iss_ti;
+    }
+  };
+  issue_next(0);
+
   int s = 0;
   for (int ti = 0; ti < n_mine; ++ti) {
-    f32x16 acc[4][4];
+    int mb, nb;
+    tile_coords(first + ti * n_wg, p.n_mblk, p.n_nblk, mb, nb);
+    f32x16 acc[2][4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < 2; ++b) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[b][i] = zero16();
     }
     for (int kt = 0; kt < n_kt; ++kt, ++s) {
       const int slot = s & 1;
-      wait_dma();          // this wave's copies of step s have landed (and its earlier stores)
+      wait_dma();          // this wave's copies of step s (the only ones in flight) have landed
       lds_barrier();       // ... and everyone's; everyone is also done with the other slot
+      if (kt == 0) pro(mb, nb);
+      if (s + 1 < n_steps) issue_next(slot ^ 1);
       const char* xs = smem + slot * SLOT + wm * TILE_BYTES;
-      const char* ws = smem + slot * SLOT + (2 + wn) * TILE_BYTES;
+      const char* ws = smem + slot * SLOT + (2 + (wn >> 1)) * TILE_BYTES;
       Frags cur, nxt;
       load_frags(xs, ws, 0, cur);
-      // prefetch the next step (the next tile's first k block after the last)
-      if (s + 1 < n_steps) {
-        if (kt + 1 == n_kt) tile_offsets(first + (ti + 1) * n_wg);
-        issue(kt + 1 == n_kt ? 0 : kt + 1, slot ^ 1);
-      }
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         if (kk + 1 < 4) load_frags(xs, ws, kk + 1, nxt);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-#pragma unroll
-          for (int b = 0; b < 4; ++b) acc[b][i] = mfma32(cur.w[b], cur.xb[i], acc[b][i]);
+          acc[0][i] = mfma32(cur.w[0], cur.xb[i], acc[0][i]);
+          acc[1][i] = mfma32(cur.w[1], cur.xb[i], acc[1][i]);
         }
         if (kk + 1 < 4) cur = nxt;
       }
     }
-    int mb, nb;
-    tile_coords(first + ti * n_wg, p.n_mblk, p.n_nblk, mb, nb);
     epi(mb, nb, acc);
   }
 }

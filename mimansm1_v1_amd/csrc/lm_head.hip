@@ -13,10 +13,10 @@
 //
 // Decomposition.  The logits are tiles of the persistent GEMM of gemm_tn.h in
 // its single-matrix layout (256 tokens x 256 vocabulary entries per
-// workgroup); the D tile gives a lane one token and 64 vocabulary entries of
-// its wave's 128, so per-token reductions are in-lane plus one exchange with
-// lane ^ 32.
-//   lm_lse_partial_kernel : per (token, 128-entry vocabulary block) the max m
+// workgroup, 64 entries per wave); the D tiles give a lane one token and 32
+// of its wave's 64 entries, so per-token reductions are in-lane plus one
+// exchange with lane ^ 32.
+//   lm_lse_partial_kernel : per (token, 64-entry vocabulary block) the max m
 //                           and sum_v exp(l_v - m), and the target's logit from
 //                           the block that holds it;
 //   lm_lse_combine_kernel : per token, the fixed-order combination of its
@@ -41,25 +41,25 @@ __device__ __forceinline__ float shfl_xor32(float v) { return __shfl_xor(v, 32);
 }  // namespace
 
 // Partials: part[t][blk] = (max, sum of exp(l - max)) over vocabulary block blk
-// (128 entries, blk = 2 * column block + wave column), (-inf, 0) for a block
+// (64 entries, blk = 4 * column block + wave column), (-inf, 0) for a block
 // beyond the vocabulary.  tlogit[t] = the target's logit (written by the one
 // lane that holds it; untouched for ignored or out-of-range targets).
-__global__ __launch_bounds__(256, 1) void lm_lse_partial_kernel(
+__global__ __launch_bounds__(512, 1) void lm_lse_partial_kernel(
     const __bf16* __restrict__ h, const __bf16* __restrict__ w, const long long* __restrict__ targets,
     float2* __restrict__ part, float* __restrict__ tlogit, int T, int d, int V, int n_mblk, int n_nblk) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int wm = wv & 1, wn = wv >> 1, hh = lane >> 5;
   const gemm::Problem p{h, w, w, T, d, V, V, n_mblk, n_nblk};
-  const int n_part = 2 * n_nblk;
-  gemm::run<false>(p, smem, [&](int mb, int nb, f32x16 (&acc)[4][4]) {
-    const int v0 = nb * 256 + 128 * wn;            // this wave's first vocabulary entry
+  const int n_part = 4 * n_nblk;
+  gemm::run<false>(p, smem, [](int, int) {}, [&](int mb, int nb, f32x16 (&acc)[2][4]) {
+    const int v0 = nb * 256 + 64 * wn;             // this wave's 64 vocabulary entries
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tok = mb * gemm::BM + 128 * wm + 32 * i + (lane & 31);
       float m = -INFINITY;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
+      for (int b = 0; b < 2; ++b) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int v = v0 + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256, 1) void lm_lse_partial_kernel(
       if (m > -INFINITY) {
         const float ms = m * kLog2e;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int b = 0; b < 2; ++b) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int v = v0 + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
@@ -81,17 +81,17 @@ __global__ __launch_bounds__(256, 1) void lm_lse_partial_kernel(
       }
       s += shfl_xor32(s);
       if (tok < T) {
-        if (hh == 0) part[(long)tok * n_part + 2 * nb + wn] = make_float2(m, s);
+        if (hh == 0) part[(long)tok * n_part + 4 * nb + wn] = make_float2(m, s);
         if (targets != nullptr) {
           const long long tv = targets[tok];
-          if (tv >= v0 && tv < v0 + 128 && tv < V) {
+          if (tv >= v0 && tv < v0 + 64 && tv < V) {
             const int rel = (int)(tv - v0);
             const int b = rel >> 5, rr = rel & 31;       // block, row inside the D tile
             if (((rr >> 2) & 1) == hh) {
               const int reg = 4 * (rr >> 3) + (rr & 3);
               float val = 0.f;
 #pragma unroll
-              for (int bb = 0; bb < 4; ++bb) {
+              for (int bb = 0; bb < 2; ++bb) {
 #pragma unroll
                 for (int q = 0; q < 16; ++q)
                   if (bb == b && q == reg) val = acc[bb][i][q];
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void lm_lse_combine_kernel(
 // columns of weight + v0; out[t][v] (row stride ld) = bf16((exp(l - lse[t]) -
 // [v0 + v == target[t]]) * scale) for valid targets, 0 for ignored ones.
 // `scale` is a device scalar (the loss gradient over the valid count).
-__global__ __launch_bounds__(256, 1) void lm_dlogits_kernel(
+__global__ __launch_bounds__(512, 1) void lm_dlogits_kernel(
     const __bf16* __restrict__ h, const __bf16* __restrict__ w, const long long* __restrict__ targets,
     const float* __restrict__ lse, const float* __restrict__ scale, __bf16* __restrict__ out, long ld,
     int T, int d, int V, int v0, int vn, long long ignore_index, int n_mblk, int n_nblk) {
@@ -150,8 +150,8 @@ __global__ __launch_bounds__(256, 1) void lm_dlogits_kernel(
   const int wm = wv & 1, wn = wv >> 1, hh = lane >> 5;
   const gemm::Problem p{h, w + v0, w + v0, T, d, V, vn, n_mblk, n_nblk};
   const float sc = *scale;
-  gemm::run<false>(p, smem, [&](int mb, int nb, f32x16 (&acc)[4][4]) {
-    const int c0 = nb * 256 + 128 * wn;            // this wave's first column of the chunk
+  gemm::run<false>(p, smem, [](int, int) {}, [&](int mb, int nb, f32x16 (&acc)[2][4]) {
+    const int c0 = nb * 256 + 64 * wn;             // this wave's first column of the chunk
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tok = mb * gemm::BM + 128 * wm + 32 * i + (lane & 31);
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256, 1) void lm_dlogits_kernel(
       const float l2 = lse[tok] * kLog2e;
       const long long tcol = tv - v0;               // the target's column in this chunk
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
+      for (int b = 0; b < 2; ++b) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int c = c0 + 32 * b + 8 * q + 4 * hh;
@@ -193,7 +193,7 @@ static hipError_t gemm_geometry(int T, int cols, int& n_mblk, int& n_nblk, int& 
 }
 
 size_t lm_head_workspace_bytes(int T, int V) {
-  const long n_part = 2L * ((V + 255) / 256);
+  const long n_part = 4L * ((V + 255) / 256);
   return (size_t)T * n_part * sizeof(float2) + (size_t)T * sizeof(float) + 256;
 }
 
@@ -206,12 +206,12 @@ hipError_t launch_lm_lse(const void* hidden, const void* weight, const long long
   e = hipFuncSetAttribute(reinterpret_cast<const void*>(lm_lse_partial_kernel),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm::LDS_BYTES);
   if (e != hipSuccess) return e;
-  const int n_part = 2 * n_nblk;
+  const int n_part = 4 * n_nblk;
   auto part = static_cast<float2*>(workspace);
   float* tl = tlogit_out != nullptr
                   ? tlogit_out
                   : reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)T * n_part * sizeof(float2));
-  hipLaunchKernelGGL(lm_lse_partial_kernel, dim3(grid), dim3(256), gemm::LDS_BYTES, stream,
+  hipLaunchKernelGGL(lm_lse_partial_kernel, dim3(grid), dim3(512), gemm::LDS_BYTES, stream,
                      static_cast<const __bf16*>(hidden), static_cast<const __bf16*>(weight), targets, part, tl,
                      T, d, V, n_mblk, n_nblk);
   hipLaunchKernelGGL(lm_lse_combine_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, part, tl, targets, lse,
@@ -228,7 +228,7 @@ hipError_t launch_lm_dlogits(const void* hidden, const void* weight, const long 
   e = hipFuncSetAttribute(reinterpret_cast<const void*>(lm_dlogits_kernel),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm::LDS_BYTES);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(lm_dlogits_kernel, dim3(grid), dim3(256), gemm::LDS_BYTES, stream,
+  hipLaunchKernelGGL(lm_dlogits_kernel, dim3(grid), dim3(512), gemm::LDS_BYTES, stream,
                      static_cast<const __bf16*>(hidden), static_cast<const __bf16*>(weight), targets, lse, scale,
                      static_cast<__bf16*>(dlogits), ld, T, d, V, v0, vn, ignore_index, n_mblk, n_nblk);
   return hipGetLastError();

@@ -65,7 +65,7 @@ __device__ __forceinline__ void store_quad(const f32x16& g, const f32x16& u, int
 }
 
 template <bool SPLIT, int ACT>
-__global__ __launch_bounds__(256, 1) void swiglu_gate_up_kernel(
+__global__ __launch_bounds__(512, 1) void swiglu_gate_up_kernel(
     const __bf16* __restrict__ x, const __bf16* __restrict__ wg, const __bf16* __restrict__ wu,
     __bf16* __restrict__ gate, __bf16* __restrict__ up, __bf16* __restrict__ act,
     int T, int d, int F, int n_mblk, int n_nblk) {
@@ -73,21 +73,17 @@ __global__ __launch_bounds__(256, 1) void swiglu_gate_up_kernel(
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w & 1, wn = w >> 1;
   const gemm::Problem p{x, wg, wu, T, d, F, F, n_mblk, n_nblk};
-  // Epilogue of a tile: block (j, i) / (2 + j, i) give lane the token
+  // Epilogue of a tile: acc[0][i] / acc[1][i] give lane the token
   // m0 + 128wm + 32i + (lane & 31) and, in registers 4q .. 4q+3, the columns
-  // n0 + 64wn + 32j + 8q + 4(lane/32) + 0..3 of Gate / Up.
-  gemm::run<true>(p, smem, [&](int mb, int nb, f32x16 (&acc)[4][4]) {
+  // n0 + 32wn + 8q + 4(lane/32) + 0..3 of Gate / Up (n0 = 128 nb, wn = 0..3).
+  gemm::run<true>(p, smem, [](int, int) {}, [&](int mb, int nb, f32x16 (&acc)[2][4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tok = mb * gemm::BM + 128 * wm + 32 * i + (lane & 31);
       if (tok < T) {
+        const long o0 = (long)tok * F + nb * 128 + 32 * wn + 4 * (lane >> 5);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const long o0 = (long)tok * F + nb * 128 + 64 * wn + 32 * j + 4 * (lane >> 5);
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            store_quad<SPLIT, ACT>(acc[j][i], acc[2 + j][i], q, o0 + 8 * q, gate, up, act);
-        }
+        for (int q = 0; q < 4; ++q) store_quad<SPLIT, ACT>(acc[0][i], acc[1][i], q, o0 + 8 * q, gate, up, act);
       }
     }
   });
@@ -131,7 +127,7 @@ static hipError_t launch_gate_up_t(const __bf16* x, const __bf16* wg, const __bf
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   const int n_mblk = (T + gemm::BM - 1) / gemm::BM, n_nblk = F / 128;
-  hipLaunchKernelGGL(kern, dim3(gemm::persistent_grid(cus, n_mblk * n_nblk)), dim3(256), gemm::LDS_BYTES,
+  hipLaunchKernelGGL(kern, dim3(gemm::persistent_grid(cus, n_mblk * n_nblk)), dim3(512), gemm::LDS_BYTES,
                      stream, x, wg, wu, gate, up, act, T, d, F, n_mblk, n_nblk);
   return hipGetLastError();
 }

@@ -216,7 +216,7 @@ def test_swiglu_argument_errors_without_device(lib):
 def test_lm_head_argument_errors_without_device(lib):
     """The cross-entropy head entries reject bad arguments before any launch."""
     ws = lib.mm1_lm_head_workspace_size(256, 49152)
-    assert ws >= 256 * 384 * 8 + 256 * 4
+    assert ws >= 256 * 768 * 8 + 256 * 4
     assert lib.mm1_lm_head_workspace_size(256, 100) == 0       # vocab not a multiple of 128
 
     def lse(h=FAKE, tg=FAKE, lse_=FAKE, tl=FAKE, ws_=FAKE, nb=None, T=256, d=1280, V=49152):
