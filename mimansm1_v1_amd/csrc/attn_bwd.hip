@@ -27,6 +27,7 @@
 //     dQ is written once in bf16 -- no fp32 scratch and no un-swizzle pass.
 #include <type_traits>
 
+#include "dispatch_order.h"
 #include "mm1_common.h"
 
 namespace mm1 {
@@ -617,6 +618,16 @@ struct TailReduce {
   int n_red;   // 0: no reduction in this launch
 };
 
+// The slice of launch slot blockIdx.x (slices go to the last n_red slots).
+__device__ __forceinline__ void tail_reduce(const TailReduce& red, int tid, int nthreads) {
+  const int slice = (int)blockIdx.x - ((int)gridDim.x - red.n_red);
+  if (slice < 0) return;
+  const long per = ((red.n + red.n_red - 1) / red.n_red + 3) & ~3L;
+  const long end = min(red.n, per * (slice + 1));
+  for (long i = per * slice + 4L * tid; i < end; i += 4L * nthreads)
+    reduce4(red.ws_dk, red.ws_dv, red.dk, red.dv, red.n, red.G, i);
+}
+
 // ---------------------------------------------------------------------------
 // dQ: one workgroup per NW*32 packed query rows (32 per wave); K and V tiles
 // of 64 keys arrive by LDS DMA (row-major) in an NSTAGE-deep ring; K^T for
@@ -626,7 +637,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     __bf16* __restrict__ dq,
-    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles, TailReduce red) {
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles, TailReduce red,
+    const DispatchOrder ord) {
   constexpr int BM = NW * 32;
   constexpr int BN = TILE_ROWS;
   constexpr int BUF = 2 * TILE_BYTES;   // K, V
@@ -636,9 +648,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int nbg = B * Hkv;
-  int tile = blockIdx.x / nbg;
+  const int item = dispatch_item(ord);    // default order: blockIdx.x
+  if (item < 0) {                         // a launch slot without rows still sums its slice
+    tail_reduce(red, tid, NW * 64);
+    return;
+  }
+  int tile = item / nbg;
   if (CAUSAL) tile = n_tiles - 1 - tile;
-  const int bg = blockIdx.x % nbg;
+  const int bg = item % nbg;
   const int b = bg / Hkv, g = bg % Hkv;
   const int R = G * S;
   const int r0 = tile * BM;
@@ -769,13 +786,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
   }
 
   // dK/dV group sum slice (the partials were completed by an earlier launch)
-  const int slice = (int)blockIdx.x - ((int)gridDim.x - red.n_red);
-  if (slice >= 0) {
-    const long per = ((red.n + red.n_red - 1) / red.n_red + 3) & ~3L;
-    const long end = min(red.n, per * (slice + 1));
-    for (long i = per * slice + 4L * tid; i < end; i += 4L * NW * 64)
-      reduce4(red.ws_dk, red.ws_dv, red.dk, red.dv, red.n, red.G, i);
-  }
+  tail_reduce(red, tid, NW * 64);
 }
 
 // ---------------------------------------------------------------------------
@@ -844,19 +855,19 @@ template <int NW, int NSTAGE>
 static void launch_dq_t(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* dO,
                         const float* lse2, const float* delta, __bf16* dq, int B, int S, int H,
                         int Hkv, bool causal, float scale2, float sm_scale, TailReduce red,
-                        hipStream_t stream) {
+                        const DispatchOrder& ord, hipStream_t stream) {
   const int G = H / Hkv;
   const int BM = NW * 32;
   const int n_qtiles = (G * S + BM - 1) / BM;
-  const int n_blocks = n_qtiles * B * Hkv;
+  const int n_blocks = ord.n ? ord.n : n_qtiles * B * Hkv;
   if (red.n_red > 0) red.n_red = min(red.n_red, n_blocks);
   dim3 grid(n_blocks), block(NW * 64);
   if (causal)
     hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, true>), grid, block, 0, stream, q, k, v, dO, lse2, delta, dq,
-                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red);
+                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
   else
     hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, false>), grid, block, 0, stream, q, k, v, dO, lse2, delta, dq,
-                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red);
+                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
 }
 
 // variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
@@ -884,10 +895,11 @@ hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void
     red.dv = static_cast<__bf16*>(dv);
     red.n_red = 1 << 30;   // every workgroup of the grid takes a slice
   }
+  const DispatchOrder& ord = dispatch_order(row_block_grid(variant, B, S, H, Hkv), causal);
   if (variant == 1)
-    launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, stream);
+    launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
   else
-    launch_dq_t<4, 2>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, stream);
+    launch_dq_t<4, 2>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
   return hipGetLastError();
 }
 

@@ -6,6 +6,7 @@
 #include "../../include/mm1_attn.h"
 #include "../../include/mm1_swiglu.h"
 #include "../../include/mm1_lm_head.h"
+#include "dispatch_order.h"
 #include "mm1_common.h"
 
 namespace mm1 {
@@ -257,6 +258,21 @@ int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* 
   if (rc) return rc;
   return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
                 D, causal, sm_scale, dq_tiles, stream);
+}
+
+int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, int causal, int cus,
+                            unsigned short* out, int cap) {
+  if (kind < MM1_TILES_FWD || kind > MM1_TILES_DQ) return MM1_E_TILES;
+  const int variant = pick_tiles(kind, tiles);
+  if (variant < 0) return MM1_E_TILES;
+  if (const int rc = check_shape(B, S, H, Hkv, mm1::HD)) return rc;
+  if (cus < 1 || cap < 0) return MM1_E_SHAPE;
+  if (cap > 0 && !out) return MM1_E_NULL;
+  if (kind == MM1_TILES_DKDV) return 0;   // the dK/dV grid always runs in the default order
+  const mm1::DispatchOrder& ord =
+      mm1::dispatch_order_for(mm1::row_block_grid(variant, B, S, H, Hkv), causal != 0, cus);
+  for (int i = 0; i < ord.n && i < cap; ++i) out[i] = ord.item[i];
+  return ord.n;
 }
 
 int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,

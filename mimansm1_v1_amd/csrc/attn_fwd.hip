@@ -23,6 +23,7 @@
 //     frame, so the result is unchanged.
 #include <type_traits>
 
+#include "dispatch_order.h"
 #include "mm1_common.h"
 
 namespace mm1 {
@@ -34,7 +35,7 @@ template <int NW, int NSTAGE, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     __bf16* __restrict__ o, float* __restrict__ lse2,
-    int B, int S, int H, int Hkv, int G, float scale2, int n_tiles) {
+    int B, int S, int H, int Hkv, int G, float scale2, int n_tiles, const DispatchOrder ord) {
   constexpr int BM = NW * 32;     // packed rows per workgroup
   constexpr int BN = TILE_ROWS;   // keys per iteration
   constexpr int BUF = 2 * TILE_BYTES;
@@ -44,9 +45,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int nbg = B * Hkv;
-  int tile = blockIdx.x / nbg;
+  const int item = dispatch_item(ord);     // default order: blockIdx.x
+  if (item < 0) return;
+  int tile = item / nbg;
   if (CAUSAL) tile = n_tiles - 1 - tile;   // longest rows first
-  const int bg = blockIdx.x % nbg;
+  const int bg = item % nbg;
   const int b = bg / Hkv, g = bg % Hkv;
   const int R = G * S;
   const int r0 = tile * BM;
@@ -219,7 +222,7 @@ template <bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     __bf16* __restrict__ o, float* __restrict__ lse2,
-    int B, int S, int H, int Hkv, int G, float scale2, int n_tiles) {
+    int B, int S, int H, int Hkv, int G, float scale2, int n_tiles, const DispatchOrder ord) {
   constexpr int BM = 256;         // packed rows per workgroup
   constexpr int BN = TILE_ROWS;   // keys per tile
   __shared__ __attribute__((aligned(1024))) char smem[4 * TILE_BYTES];   // K slots 0, 1; V slots 0, 1
@@ -228,9 +231,11 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int grp = w >> 2;                                    // 0 = A, 1 = B
   const int nbg = B * Hkv;
-  int tile = blockIdx.x / nbg;
+  const int item = dispatch_item(ord);     // default order: blockIdx.x
+  if (item < 0) return;
+  int tile = item / nbg;
   if (CAUSAL) tile = n_tiles - 1 - tile;   // longest rows first
-  const int bg = blockIdx.x % nbg;
+  const int bg = item % nbg;
   const int b = bg / Hkv, g = bg % Hkv;
   const int R = G * S;
   const int r0 = tile * BM;
@@ -414,15 +419,16 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
 
 template <int NW, int NSTAGE>
 static void launch_fwd_t(const __bf16* q, const __bf16* k, const __bf16* v, __bf16* o, float* lse2,
-                         int B, int S, int H, int Hkv, bool causal, float scale2, hipStream_t stream) {
+                         int B, int S, int H, int Hkv, bool causal, float scale2, const DispatchOrder& ord,
+                         hipStream_t stream) {
   const int G = H / Hkv;
   const int BM = NW * 32;
   const int n_tiles = (G * S + BM - 1) / BM;
-  dim3 grid(n_tiles * B * Hkv), block(NW * 64);
+  dim3 grid(ord.n ? ord.n : n_tiles * B * Hkv), block(NW * 64);
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, true>), grid, block, 0, stream, q, k, v, o, lse2, B, S, H, Hkv, G, scale2, n_tiles);
+    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, true>), grid, block, 0, stream, q, k, v, o, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, false>), grid, block, 0, stream, q, k, v, o, lse2, B, S, H, Hkv, G, scale2, n_tiles);
+    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, false>), grid, block, 0, stream, q, k, v, o, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
 }
 
 // variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
@@ -436,18 +442,19 @@ hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, floa
   auto kp = static_cast<const __bf16*>(k);
   auto vp = static_cast<const __bf16*>(v);
   auto op = static_cast<__bf16*>(o);
+  const DispatchOrder& ord = dispatch_order(row_block_grid(variant, B, S, H, Hkv), causal);
   if (variant == 2) {
     const int G = H / Hkv;
     const int n_tiles = (G * S + 255) / 256;
-    dim3 grid(n_tiles * B * Hkv), block(512);
+    dim3 grid(ord.n ? ord.n : n_tiles * B * Hkv), block(512);
     if (causal)
-      hipLaunchKernelGGL(attn_fwd_pp_kernel<true>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles);
+      hipLaunchKernelGGL(attn_fwd_pp_kernel<true>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
     else
-      hipLaunchKernelGGL(attn_fwd_pp_kernel<false>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles);
+      hipLaunchKernelGGL(attn_fwd_pp_kernel<false>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
   } else if (variant == 1)
-    launch_fwd_t<8, 3>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, stream);
+    launch_fwd_t<8, 3>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
   else
-    launch_fwd_t<4, 2>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, stream);
+    launch_fwd_t<4, 2>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
   return hipGetLastError();
 }
 

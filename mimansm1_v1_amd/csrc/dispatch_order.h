@@ -1,0 +1,71 @@
+// Workgroup dispatch order for the causal forward and dQ grids.
+//
+// The row blocks of a causal grid carry very different amounts of work: row
+// block i walks about i key tiles.  How gfx950 deals workgroups out
+// (measured with a per-workgroup probe of XCC / SE / CU ids and timestamps):
+// launch slot b goes to XCD b % 8; each XCD hands its k-th workgroup to
+// shader engine k % 4 (4 SEs of 8 CUs) and waits, in order, until that SE
+// has a free CU.  With one workgroup per CU and 2-3 per CU in total (the
+// training shapes) the longest-first order then ends in a ragged last round.
+//
+// Instead, the host deals each XCD's items to its 4 SE lanes (longest first,
+// in a snake, so every lane gets the same mix), packs each lane into its
+// SE's CUs (bins of near-equal modelled work), lists each lane's items in
+// the order in which those CUs would ask for them, and interleaves the lanes
+// position by position so the SEs progress together.  Launch slot b runs
+// item order.item[b]; b % 8 is the XCD the default order gives that item, so
+// each XCD works on the same (batch, KV head) set as before.  The order only
+// permutes which workgroup does which row block: the results are bitwise the
+// same.
+//
+// The table travels in the kernel arguments (no device memory, no copy).  It
+// is built once per shape and cached.  The default order (order.n == 0) is
+// kept for non-causal grids (equal items), tilings with two workgroups per
+// CU (the two share the CU's throughput, which this model does not capture;
+// the packed order measured slower for them), shapes with more items than
+// the table holds, and shapes where the model finds no gain.  The dK/dV grid
+// is not reordered: its items are closer in size, and the model's gain there
+// (about 1%) did not show in measurement.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mm1 {
+
+constexpr int kOrderCap = 1536;            // items a table holds
+constexpr uint16_t kNoItem = 0xFFFF;       // a launch slot without an item
+
+struct DispatchOrder {
+  int n;                                   // launch slots; 0: default order
+  uint16_t item[kOrderCap];                // item of launch slot b, in the default numbering
+};
+
+// Item of this workgroup in the default numbering (blockIdx.x when the order
+// is the default one), or -1 when its launch slot carries no item.
+__device__ __forceinline__ int dispatch_item(const DispatchOrder& ord) {
+  if (ord.n == 0) return (int)blockIdx.x;
+  const int it = ord.item[blockIdx.x];
+  return it == kNoItem ? -1 : it;
+}
+
+// A row-block grid: item j = (tile n_tiles-1-j/nbg, bg j%nbg) of `rows`
+// packed query rows, walking 64-key tiles; `wg_per_cu` resident workgroups.
+struct GridShape {
+  int B, S, H, Hkv;
+  int rows;
+  int wg_per_cu;
+};
+
+// The grid of the forward / dQ launchers for a tiling index (0 = 128 rows,
+// 2 workgroups per CU; 1, 2 = 256 rows, 1 per CU).
+GridShape row_block_grid(int variant, int B, int S, int H, int Hkv);
+
+// Cached order for the current device (its CU count); a table with n == 0
+// when the default order applies (see above, or the MM1_DISPATCH_ORDER=0
+// switch).
+const DispatchOrder& dispatch_order(const GridShape& g, bool causal);
+
+// Same for a given CU count (the host-side model; no device needed).
+const DispatchOrder& dispatch_order_for(const GridShape& g, bool causal, int cus);
+
+}  // namespace mm1

@@ -241,3 +241,108 @@ def test_lm_head_argument_errors_without_device(lib):
     assert dl(v0=49152 - 128, vn=256) == -2   # past the vocabulary
     assert dl(ld=4000) == -2                  # row stride shorter than the chunk
     assert dl(out=FAKE + 8) == -6
+
+
+# ---------------------------------------------------------------------------
+# Workgroup dispatch order of the causal grids (host-side model, no device).
+
+def _order(lib, kind, tiles, B, S, H=10, Hkv=2, causal=1, cus=256):
+    import ctypes
+    n = lib.mm1_attn_dispatch_order(kind, tiles, B, S, H, Hkv, causal, cus, None, 0)
+    if n <= 0:
+        return n, []
+    buf = (ctypes.c_ushort * n)()
+    assert lib.mm1_attn_dispatch_order(kind, tiles, B, S, H, Hkv, causal, cus, buf, n) == n
+    return n, list(buf)
+
+
+def _items_and_costs(kind, tiles, B, S, H=10, Hkv=2):
+    """Default numbering and relative work of a grid's items: forward / dQ row
+    blocks walk their causal key tiles (64 keys), dK/dV key tiles their query
+    tiles (32 or 64 queries); the kernels' own index arithmetic."""
+    G = H // Hkv
+    if kind == 1:
+        bq = 64 if tiles == 1 else 32
+        nbh, nkt = B * H, (S + 127) // 128
+        return [((S - (j // nbh) * 128 + bq - 1) // bq) * (bq // 32) for j in range(nkt * nbh)]
+    bm = 128 if tiles == 0 else 256
+    nbg, R = B * Hkv, G * S
+    nt = (R + bm - 1) // bm
+    out = []
+    for j in range(nt * nbg):
+        tile = nt - 1 - j // nbg
+        last = min(tile * bm + bm, R) - 1
+        out.append(min(S - 1, last // G) // 64 + 1)
+    return out
+
+
+def _makespan(order, costs, slots_per_se):
+    """Dispatch as measured on gfx950: launch slot b goes to XCD b % 8; an
+    XCD hands its k-th workgroup to shader engine k % 4 and waits, in order,
+    for a free slot there (item cost + 1 fixed unit per workgroup)."""
+    import heapq
+    worst = 0
+    for x in range(8):
+        free = [[0] * slots_per_se for _ in range(4)]
+        last = 0
+        for k, b in enumerate(range(x, len(order), 8)):
+            t = max(heapq.heappop(free[k % 4]), last)
+            last = t
+            heapq.heappush(free[k % 4], t + (costs[order[b]] + 1 if order[b] != 0xFFFF else 0))
+        worst = max(worst, max(max(f) for f in free))
+    return worst
+
+
+GRIDS = [(0, 0), (0, 1), (0, 2), (1, 0), (1, 1), (2, 0), (2, 1)]
+SHAPES = [(2, 8192), (8, 2048), (4, 4096), (1, 1000), (3, 777)]
+
+
+@pytest.mark.parametrize("kind,tiles", GRIDS)
+@pytest.mark.parametrize("B,S", SHAPES)
+def test_dispatch_order_is_a_balanced_permutation(lib, kind, tiles, B, S):
+    costs = _items_and_costs(kind, tiles, B, S)
+    n, order = _order(lib, kind, tiles, B, S)
+    table = n > 0
+    if not table:                    # launched in the default order
+        n, order = len(costs), list(range(len(costs)))
+    assert len(costs) <= n <= len(costs) + 8 * 4 and (n % 8 == 0 or n == len(costs))
+    items = [i for i in order if i != 0xFFFF]
+    assert sorted(items) == list(range(len(costs)))          # every item exactly once
+    assert all(i % 8 == b % 8 for b, i in enumerate(order) if i != 0xFFFF)   # XCD kept
+    slots = 8 * (2 if (kind != 1 and tiles == 0) else 1)
+    default = list(range(len(costs)))
+    new_span, old_span = _makespan(order, costs, slots), _makespan(default, costs, slots)
+    bound = max(max(costs), -(-sum(c + 1 for c in costs) // (8 * 4 * slots)))
+    assert new_span <= old_span * 1.01 + 2, (new_span, old_span, bound)
+    if table:
+        assert new_span <= 1.10 * bound + 4, (new_span, old_span, bound)
+
+
+def test_dispatch_order_defaults_and_errors(lib, monkeypatch):
+    import ctypes
+    # non-causal grids (equal items) and grids beyond the table run in the default order
+    assert lib.mm1_attn_dispatch_order(0, 2, 2, 8192, 10, 2, 0, 256, None, 0) == 0
+    assert lib.mm1_attn_dispatch_order(0, 2, 16, 8192, 10, 2, 1, 256, None, 0) == 0   # 5120 blocks
+    assert lib.mm1_attn_dispatch_order(1, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0    # dK/dV
+    monkeypatch.setenv("MM1_DISPATCH_ORDER", "0")
+    assert lib.mm1_attn_dispatch_order(0, 2, 2, 8192, 10, 2, 1, 256, None, 0) == 0
+    monkeypatch.delenv("MM1_DISPATCH_ORDER")
+    n = lib.mm1_attn_dispatch_order(0, 2, 2, 8192, 10, 2, 1, 256, None, 0)
+    assert n >= 640
+    buf = (ctypes.c_ushort * 8)()
+    assert lib.mm1_attn_dispatch_order(0, 2, 2, 8192, 10, 2, 1, 256, buf, 8) == n
+    _, full = _order(lib, 0, 2, 2, 8192)
+    assert list(buf) == full[:8]
+    # a device with fewer CUs gets its own table; two workgroups per CU: default order
+    _, small = _order(lib, 0, 2, 2, 8192, cus=128)
+    assert small != full and sorted(small) == sorted(full)
+    assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0
+    assert lib.mm1_attn_dispatch_order(2, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0
+    E_TILES, E_SHAPE, E_NULL, E_HEAD = -7, -2, -1, -3
+    assert lib.mm1_attn_dispatch_order(3, 0, 2, 8192, 10, 2, 1, 256, None, 0) == E_TILES
+    assert lib.mm1_attn_dispatch_order(0, 9, 2, 8192, 10, 2, 1, 256, None, 0) == E_TILES
+    assert lib.mm1_attn_dispatch_order(0, 0, 0, 8192, 10, 2, 1, 256, None, 0) == E_SHAPE
+    assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 3, 1, 256, None, 0) == E_SHAPE
+    assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 0, None, 0) == E_SHAPE
+    assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 256, None, 4) == E_NULL
+    assert E_HEAD != E_SHAPE

@@ -151,6 +151,44 @@ def test_env_variable_selects_tiling(hip_device, monkeypatch, env, kind, index):
         assert torch.equal(x, y), name
 
 
+@pytest.mark.parametrize("B,S", [(8, 2048), (4, 4096)])
+@pytest.mark.parametrize("tiles", [(1, 0, 1), (2, 1, 1), (2, 0, 0)], ids=["t101", "t211", "t200"])
+def test_dispatch_order_is_bitwise_neutral(hip_device, monkeypatch, B, S, tiles):
+    """The dispatch order only changes which workgroup runs which item: every
+    output is bitwise the one of the default (longest-first) order, which the
+    full-size parity tests check against the oracle."""
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    H, Hkv = 10, 2
+    tables = [lib.mm1_attn_dispatch_order(kind, tiles[kind], B, S, H, Hkv, 1, 256, None, 0) for kind in range(3)]
+    log(f"[case] dispatch order B={B} S={S} tiles={tiles} table sizes {tables}")
+    assert any(n > 0 for n in tables)
+    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=B + S))
+    scale = 128 ** -0.5
+    sp = torch.cuda.current_stream(hip_device).cuda_stream
+    p = lambda t: t.data_ptr()
+    nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
+    ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=hip_device)
+
+    def run(order):
+        monkeypatch.setenv("MM1_DISPATCH_ORDER", "1" if order else "0")
+        o, lse = torch.empty_like(q), torch.empty(B, H, S, dtype=torch.float32, device=hip_device)
+        delta = torch.empty_like(lse)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        args = (B, S, H, Hkv, 128, 1, scale)
+        assert lib.mm1_attn_fwd_tiles(p(q), p(k), p(v), p(o), p(lse), *args, tiles[0], sp) == 0
+        assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+        assert lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk), p(dv),
+                                      p(ws), nws, *args, tiles[1], tiles[2], sp) == 0
+        torch.cuda.synchronize()
+        monkeypatch.delenv("MM1_DISPATCH_ORDER")
+        return [x.cpu() for x in (o, lse, dq, dk, dv)]
+
+    base, packed = run(False), run(True)
+    for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), base, packed):
+        assert torch.equal(x, y), name
+
+
 def test_autotune_records_a_compiled_winner(hip_device, monkeypatch, tmp_path):
     """get_kernel with AUTOTUNE and no record: every tiling is timed, the
     fastest is recorded under (device, kernel, shape) and the handle uses it;
