@@ -25,15 +25,17 @@
 extern "C" {
 #endif
 
-/* Bytes of scratch mm1_lm_head_lse needs (per-token partial maxima and sums
- * of the 128-entry vocabulary blocks). */
+/* Bytes of scratch mm1_lm_head_lse needs (per-token partial maxima and sums,
+ * one per 64-entry column group of each 256-entry vocabulary block). */
 size_t mm1_lm_head_workspace_size(int T, int vocab);
 
 /* lse[t] = log sum_v exp(hidden[t] . weight[:, v]) with fp32 accumulation of
  * the bf16 products, the [T, vocab] logits never stored.  With targets:
- * target_logit[t] = hidden[t] . weight[:, targets[t]] (the same accumulation)
- * and loss[t] = lse[t] - target_logit[t], 0 for ignored tokens (either may be
- * NULL).  Replaces get_kernel((T, d_model, vocab))(hidden, weight) -> Lse
+ * target_logit[t] = hidden[t] . weight[:, c] (the same accumulation) with
+ * c = targets[t], or c = 0 when targets[t] is negative (ignore_index) or
+ * >= vocab, as the reference's gather over targets.clamp(min=0); and
+ * loss[t] = lse[t] - target_logit[t], 0 for ignored or out-of-range targets
+ * (either output may be NULL).  Replaces get_kernel((T, d_model, vocab))(hidden, weight) -> Lse
  * (logsumexp_kernel, lm_head_tilelang.py:92-156) and, in
  * FusedCrossEntropy.forward, gather_target_logits and the per-token loss
  * (:186-190, :201-209).  Deterministic. */

@@ -42,8 +42,10 @@ __device__ __forceinline__ float shfl_xor32(float v) { return __shfl_xor(v, 32);
 
 // Partials: part[t][blk] = (max, sum of exp(l - max)) over vocabulary block blk
 // (64 entries, blk = 4 * column block + wave column), (-inf, 0) for a block
-// beyond the vocabulary.  tlogit[t] = the target's logit (written by the one
-// lane that holds it; untouched for ignored or out-of-range targets).
+// beyond the vocabulary.  tlogit[t] = the logit of column targets[t], or of
+// column 0 when the target is negative (ignore_index) or >= V, as the
+// reference's gather over targets.clamp(min=0); written by the one lane that
+// holds that column.
 __global__ __launch_bounds__(512, 1) void lm_lse_partial_kernel(
     const __bf16* __restrict__ h, const __bf16* __restrict__ w, const long long* __restrict__ targets,
     float2* __restrict__ part, float* __restrict__ tlogit, int T, int d, int V, int n_mblk, int n_nblk) {
@@ -83,8 +85,9 @@ __global__ __launch_bounds__(512, 1) void lm_lse_partial_kernel(
       if (tok < T) {
         if (hh == 0) part[(long)tok * n_part + 4 * nb + wn] = make_float2(m, s);
         if (targets != nullptr) {
-          const long long tv = targets[tok];
-          if (tv >= v0 && tv < v0 + 64 && tv < V) {
+          long long tv = targets[tok];
+          if (tv < 0 || tv >= V) tv = 0;     // the reference gathers column clamp(t, min=0)
+          if (tv >= v0 && tv < v0 + 64) {
             const int rel = (int)(tv - v0);
             const int b = rel >> 5, rr = rel & 31;       // block, row inside the D tile
             if (((rr >> 2) & 1) == hh) {
