@@ -261,6 +261,35 @@ def test_full_config_vs_gpu_oracle(hip_device, config):
     assert_bf16_close("dV", dv, wv, log, emulated=ev)
 
 
+RAGGED = [(3, 4097, 10, 2), (5, 2999, 10, 2), (2, 7777, 10, 2)]
+
+
+@pytest.mark.parametrize("B,S,H,Hkv", RAGGED, ids=[f"B{b}S{s}" for b, s, _, _ in RAGGED])
+def test_large_ragged_vs_gpu_oracle(hip_device, B, S, H, Hkv):
+    """Sequence lengths that are no multiple of any tile (32, 64, 128, 256)
+    at sizes where the launches use the packed dispatch tables with item
+    counts that are no multiple of 8 (empty launch slots): the same gates as
+    the full configs, against the chunked closed form on the GPU."""
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    tables = [lib.mm1_attn_dispatch_order(0, 2, B, S, H, Hkv, 1, 256, None, 0),
+              lib.mm1_attn_dispatch_order(2, 1, B, S, H, Hkv, 1, 256, None, 0)]
+    log(f"[case] ragged B={B} S={S} H={H} Hkv={Hkv} dispatch tables {tables}")
+    assert min(tables) > 0
+    q, k, v, do = R.make_inputs(B, S, H, Hkv, 128, seed=S)
+    o, lse, dq, dk, dv = hip_run(q, k, v, do, True, H // Hkv, hip_device)
+    dev = [t.to(hip_device) for t in (q, k, v, do)]
+    want_o, want_lse = R.forward_chunked(*dev[:3], True, H // Hkv)
+    assert_bf16_close("O", o, want_o, log)
+    assert_lse_close(lse, want_lse, log)
+    del want_o, want_lse
+    wq, wk, wv = R.grads_analytic(*dev, True, H // Hkv)
+    eq, ek, ev = R.grads_analytic(*dev, True, H // Hkv, bf16_products=True, o=o.to(hip_device))
+    assert_bf16_close("dQ", dq, wq, log, emulated=eq)
+    assert_bf16_close("dK", dk, wk, log, emulated=ek)
+    assert_bf16_close("dV", dv, wv, log, emulated=ev)
+
+
 def test_backward_deterministic(hip_device):
     log("[case] determinism B2 S1024")
     q, k, v, do = R.make_inputs(2, 1024, 10, 2, 128, seed=5)
