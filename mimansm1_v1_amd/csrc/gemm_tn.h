@@ -24,7 +24,7 @@
 // conflict-free on the swizzled tile layout.  Tiles are dealt to the 8 XCDs
 // in contiguous runs of a grouped order (8 token blocks, then the next
 // column block) so an XCD's concurrent tiles share X rows and W columns in
-// its L2.
+// its L2.  A ragged last round is split into half tiles (see run()).
 #pragma once
 #include "mm1_common.h"
 
@@ -107,10 +107,26 @@ __device__ __forceinline__ void run(const Problem& p, char* smem, Pro&& pro, Epi
   const int wu_ = __builtin_amdgcn_readfirstlane(w);
 
   const int total = p.n_mblk * p.n_nblk;
-  const int xcd = blockIdx.x & 7, n_wg = gridDim.x >> 3;
+  const int xcd = blockIdx.x & 7, n_wg = gridDim.x >> 3, j = (int)(blockIdx.x >> 3);
   const int t0 = (int)(((long)xcd * total) >> 3), t1 = (int)(((long)(xcd + 1) * total) >> 3);
-  const int first = t0 + (int)(blockIdx.x >> 3);
-  const int n_mine = first < t1 ? (t1 - first + n_wg - 1) / n_wg : 0;
+  const int first = t0 + j;
+  // Ragged last round: when at most half of this XCD's workgroups would get
+  // one more tile, its rem leftover tiles are split by W tile into 2 rem half
+  // tiles, one for each of the first 2 rem workgroups (the waves of the other
+  // W tile skip the products and the epilogue), so no workgroup runs a whole
+  // extra tile alone.
+  const int n_full = (t1 - t0) / n_wg, rem = (t1 - t0) % n_wg;
+  const bool split = rem > 0 && 2 * rem <= n_wg;
+  const int n_mine = split ? n_full + (j < 2 * rem ? 1 : 0)
+                           : (first < t1 ? (t1 - first + n_wg - 1) / n_wg : 0);
+  auto tile_at = [&](int ti, int& half) {   // half: -1 whole tile, else the W tile kept
+    if (split && ti == n_full) {
+      half = j & 1;
+      return t0 + n_full * n_wg + (j >> 1);
+    }
+    half = -1;
+    return first + ti * n_wg;
+  };
   const int n_kt = p.d / BK;
   const int n_steps = n_mine * n_kt;
   if (n_steps == 0) return;
@@ -183,7 +199,8 @@ __device__ __forceinline__ void run(const Problem& p, char* smem, Pro&& pro, Epi
 
   int iss_ti = 0, iss_kt = 0;
   auto issue_next = [&](int slot) {
-    if (iss_kt == 0) tile_offsets(first + iss_ti * n_wg);
+    int h;
+    if (iss_kt == 0) tile_offsets(tile_at(iss_ti, h));
     issue(iss_kt, slot);
     if (++iss_kt == n_kt) {
       iss_kt = 0;
@@ -194,8 +211,9 @@ __device__ __forceinline__ void run(const Problem& p, char* smem, Pro&& pro, Epi
 
   int s = 0;
   for (int ti = 0; ti < n_mine; ++ti) {
-    int mb, nb;
-    tile_coords(first + ti * n_wg, p.n_mblk, p.n_nblk, mb, nb);
+    int mb, nb, half;
+    tile_coords(tile_at(ti, half), p.n_mblk, p.n_nblk, mb, nb);
+    const bool active = half < 0 || (wn >> 1) == half;   // wave-uniform
     f32x16 acc[2][4];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -208,22 +226,24 @@ __device__ __forceinline__ void run(const Problem& p, char* smem, Pro&& pro, Epi
       lds_barrier();       // ... and everyone's; everyone is also done with the other slot
       if (kt == 0) pro(mb, nb);
       if (s + 1 < n_steps) issue_next(slot ^ 1);
-      const char* xs = smem + slot * SLOT + wm * TILE_BYTES;
-      const char* ws = smem + slot * SLOT + (2 + (wn >> 1)) * TILE_BYTES;
-      Frags cur, nxt;
-      load_frags(xs, ws, 0, cur);
+      if (active) {
+        const char* xs = smem + slot * SLOT + wm * TILE_BYTES;
+        const char* ws = smem + slot * SLOT + (2 + (wn >> 1)) * TILE_BYTES;
+        Frags cur, nxt;
+        load_frags(xs, ws, 0, cur);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        if (kk + 1 < 4) load_frags(xs, ws, kk + 1, nxt);
+        for (int kk = 0; kk < 4; ++kk) {
+          if (kk + 1 < 4) load_frags(xs, ws, kk + 1, nxt);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[0][i] = mfma32(cur.w[0], cur.xb[i], acc[0][i]);
-          acc[1][i] = mfma32(cur.w[1], cur.xb[i], acc[1][i]);
+          for (int i = 0; i < 4; ++i) {
+            acc[0][i] = mfma32(cur.w[0], cur.xb[i], acc[0][i]);
+            acc[1][i] = mfma32(cur.w[1], cur.xb[i], acc[1][i]);
+          }
+          if (kk + 1 < 4) cur = nxt;
         }
-        if (kk + 1 < 4) cur = nxt;
       }
     }
-    epi(mb, nb, acc);
+    if (active) epi(mb, nb, acc);
   }
 }
 
