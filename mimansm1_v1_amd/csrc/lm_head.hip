@@ -109,8 +109,17 @@ __global__ __launch_bounds__(512, 1) void lm_lse_partial_kernel(
 }
 
 // One wave per token: lse = m* + ln(sum_j s_j exp(m_j - m*)) over the token's
-// partials in a fixed order (lane-strided, then a fixed shuffle tree), and the
-// token loss lse - target_logit (0 for ignored or out-of-range targets).
+// partials, in one pass: each lane folds partials lane, lane + 64, ... into a
+// running (max, sum) in index order, then the lanes' pairs merge by a fixed
+// shuffle tree (deterministic); the token loss is lse - target_logit (0 for
+// ignored or out-of-range targets).
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;                    // both empty
+  s = s * exp2_fast((m - mn) * kLog2e) + s2 * exp2_fast((m2 - mn) * kLog2e);
+  m = mn;
+}
+
 __global__ __launch_bounds__(256) void lm_lse_combine_kernel(
     const float2* __restrict__ part, const float* __restrict__ tlogit, const long long* __restrict__ targets,
     float* __restrict__ lse, float* __restrict__ loss, int T, int V, int n_part, long long ignore_index) {
@@ -118,18 +127,24 @@ __global__ __launch_bounds__(256) void lm_lse_combine_kernel(
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= T) return;
   const float2* row = part + (long)tok * n_part;
-  float m = -INFINITY;
-  for (int j = lane; j < n_part; j += 64) m = fmaxf(m, row[j].x);
+  float m = -INFINITY, s = 0.f;
+  int j = lane;
+  for (; j + 192 < n_part; j += 256) {            // four loads in flight per lane
+    float2 v[4];
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  float s = 0.f;
-  const float ms = m * kLog2e;
-  for (int j = lane; j < n_part; j += 64) {
-    const float2 pj = row[j];
-    if (pj.x > -INFINITY) s += pj.y * exp2_fast(pj.x * kLog2e - ms);
+    for (int u = 0; u < 4; ++u) v[u] = row[j + 64 * u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) lse_merge(m, s, v[u].x, v[u].y);
+  }
+  for (; j < n_part; j += 64) {
+    const float2 v = row[j];
+    lse_merge(m, s, v.x, v.y);
   }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+    lse_merge(m, s, m2, s2);
+  }
   if (lane == 0) {
     const float l = m + log2f(s) * kLn2;
     lse[tok] = l;
