@@ -39,7 +39,7 @@ IGNORE_INDEX = -100
 AUTOTUNE = True
 # The gfx950 tiling of both vocabulary GEMMs (LM:61-85 describes the
 # reference's TileLang search space instead).
-LSE_TILES = dict(block_M=256, block_N=256, block_K=64, waves=4, stages=2)
+LSE_TILES = dict(block_M=256, block_N=256, block_K=64, waves=8, stages=2)
 VOCAB_CHUNK = 49152
 
 

@@ -36,7 +36,7 @@ MODE_ACT, MODE_SPLIT, MODE_TRAIN = 0, 1, 2     # MM1_SWIGLU_ACT / _SPLIT / _TRAI
 
 # The gfx950 tilings (one per kernel; SW:59-100 describes the reference's
 # TileLang search space instead).
-GATE_UP_TILES = dict(block_M=256, block_N=128, block_K=64, waves=4, stages=2)
+GATE_UP_TILES = dict(block_M=256, block_N=128, block_K=64, waves=8, stages=2)
 GRAD_TILES = dict(cols_per_thread=8, threads=256)
 AUTOTUNE = True
 
