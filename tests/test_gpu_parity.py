@@ -261,7 +261,7 @@ def test_full_config_vs_gpu_oracle(hip_device, config):
     assert_bf16_close("dV", dv, wv, log, emulated=ev)
 
 
-RAGGED = [(3, 4097, 10, 2), (5, 2999, 10, 2), (2, 7777, 10, 2)]
+RAGGED = [(3, 4097, 10, 2), (5, 2999, 10, 2), (2, 7777, 10, 2), (1, 16384, 10, 2)]
 
 
 @pytest.mark.parametrize("B,S,H,Hkv", RAGGED, ids=[f"B{b}S{s}" for b, s, _, _ in RAGGED])
