@@ -73,13 +73,41 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 // Query tiles (Q, dO row-major; lse2, Delta) arrive by LDS DMA in a two-stage
 // ring; the transposed operands of dV^T and dK^T are read with the LDS
 // transpose read.
+// Work item of a dK/dV workgroup: key tile kt = item / (B*H) of query head
+// bh = item % (B*H), or -1 for a launch slot without one.  Slot b runs on XCD
+// b % 8.  The slots are dealt so that each XCD owns whole query heads, and
+// the workgroups it runs at one time share the Q/dO tiles they stream.  Each
+// head's key tiles are split by kt mod q into q parts, q = 8 / gcd(B*H, 8),
+// so that the 8 XCDs get m = B*H*q/8 parts each.  XCD x runs its parts
+// x*m .. x*m+m-1 interleaved, key tiles ascending (longest first).  When 8
+// divides B*H (q = 1) every XCD holds whole heads.  (The plain b -> (b /
+// (B*H), b % (B*H)) order spreads each head over several XCDs unless 8
+// divides B*H; at B*H = 20 that fetched 2.3x the bytes from beyond L2.)
+struct KeyTileOrder {
+  int q, m;   // parts per head, parts per XCD
+};
+
+inline KeyTileOrder key_tile_order(int nbh) {
+  int g = 8;
+  while (nbh % g) g >>= 1;   // gcd(nbh, 8)
+  const int q = 8 / g;
+  return {q, nbh * q / 8};
+}
+
+__device__ __forceinline__ int key_tile_item(int slot, int nbh, int n_kt, KeyTileOrder o) {
+  const int x = slot & 7, r = slot >> 3;
+  const int part = x * o.m + r % o.m;
+  const int kt = o.q * (r / o.m) + part % o.q;
+  return kt < n_kt ? kt * nbh + part / o.q : -1;
+}
+
 template <bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     float* __restrict__ ws_dk, float* __restrict__ ws_dv,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale) {
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order) {
   constexpr int BQ = TILE_ROWS;                      // query positions per tile
   constexpr int BUF = 2 * TILE_BYTES + 2 * BQ * 4;   // Q, dO, lse2, delta
   constexpr int MBOX = 32 * 32 * 4;                  // one 32 x 32 fp32 P block
@@ -96,8 +124,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
   const int pair = w & 3;
   const bool pwave = w < 4;
   const int nbh = B * H;
-  const int kt = blockIdx.x / nbh;        // heaviest key tiles first
-  const int bh = blockIdx.x % nbh;
+  const int item = key_tile_item(blockIdx.x, nbh, (S + 127) / 128, order);
+  if (item < 0) return;
+  const int kt = item / nbh;              // heaviest key tiles first
+  const int bh = item % nbh;
   const int b = bh / H, hq = bh % H;
   const int g = hq / G, hh = hq % G;
   const int kw0 = kt * 128 + 32 * pair;   // this pair's first key
@@ -321,7 +351,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     float* __restrict__ ws_dk, float* __restrict__ ws_dv,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale) {
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order) {
   static_assert(NSTAGE >= 6, "ring depth: at least 6");
   constexpr int BQ = 32;                  // query positions per tile
   constexpr int QT = BQ * HD * 2;         // one 32 x 128 bf16 operand tile
@@ -334,8 +364,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   const int pair = w & 3;
   const bool pwave = w < 4;
   const int nbh = B * H;
-  const int kt = blockIdx.x / nbh;        // heaviest key tiles first
-  const int bh = blockIdx.x % nbh;
+  const int item = key_tile_item(blockIdx.x, nbh, (S + 127) / 128, order);
+  if (item < 0) return;
+  const int kt = item / nbh;              // heaviest key tiles first
+  const int bh = item % nbh;
   const int b = bh / H, hq = bh % H;
   const int g = hq / G, hh = hq % G;
   const int kw0 = kt * 128 + 32 * pair;   // this pair's first key
@@ -823,10 +855,11 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
   auto dkp = static_cast<__bf16*>(dk);
   auto dvp = static_cast<__bf16*>(dv);
   const int n_ktiles = (S + 127) / 128;
-  dim3 grid(n_ktiles * B * H);
+  const KeyTileOrder order = key_tile_order(B * H);
+  dim3 grid(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
 #define MM1_DKDV_LAUNCH(KERNEL)                                                               \
   hipLaunchKernelGGL(KERNEL, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta, ws_dk, \
-                     ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale)
+                     ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, order)
   if (variant == 1) {
     if (causal) MM1_DKDV_LAUNCH(attn_dkdv_kernel<true>);
     else MM1_DKDV_LAUNCH(attn_dkdv_kernel<false>);
