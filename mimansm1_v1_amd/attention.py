@@ -568,7 +568,11 @@ class Attention(nn.Module):
         if backend in _HIP_BACKENDS:
             out = flash_attention(q.to(DTYPE).contiguous(), k.to(DTYPE).contiguous(),
                                   v.to(DTYPE).contiguous(), True, cfg.groups)
-            out = out.to(x.dtype)
+            # Under bf16 autocast wo casts its input back to bf16, so the
+            # reference's cast to x.dtype (AT:494) is a bf16 -> fp32 -> bf16
+            # round trip, exact both ways (its gradient too): skipped there.
+            if not (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == DTYPE):
+                out = out.to(x.dtype)
         else:
             qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))
             if backend == "sdpa":

@@ -450,6 +450,39 @@ def test_qknorm_rope_kernel_vs_oracle(hip_device, B, S, H, Hkv, norm):
             assert err < 2e-3, name
 
 
+def test_sublayer_skipped_cast_is_bitwise_neutral(hip_device, monkeypatch):
+    """Under bf16 autocast the "hip" sublayer keeps the attention output in
+    bf16 instead of the reference's cast to x.dtype that wo casts straight
+    back: output and every gradient equal the path with the cast, bitwise."""
+    from mimansm1_v1_amd import attention as A
+    log("[case] sublayer B2 S256: skipped fp32 round trip vs the reference's cast")
+    torch.manual_seed(0)
+    cfg = A.AttnConfig(max_seq_len=256)
+    mod = A.Attention(cfg, A.Rotary(cfg.head_dim, cfg.max_seq_len, cfg.rope_theta)).to(hip_device)
+    with torch.no_grad():
+        for lin in (mod.wq, mod.wk, mod.wv, mod.wo):
+            lin.weight.normal_(0.0, 0.02)
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(2, 256, cfg.d_model, generator=gen).to(hip_device)
+    dy = torch.randn(2, 256, cfg.d_model, generator=gen).to(hip_device)
+
+    def run():
+        mod.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = mod(xi, backend="hip")
+        y.backward(dy.to(y.dtype))
+        torch.cuda.synchronize()
+        return [y.detach().cpu(), xi.grad.cpu()] + [p.grad.cpu() for p in mod.parameters() if p.grad is not None]
+
+    skipped = run()
+    monkeypatch.setattr(A.torch, "is_autocast_enabled", lambda *a: False)   # take the reference's cast
+    cast = run()
+    assert len(skipped) == len(cast)
+    for i, (a, b) in enumerate(zip(skipped, cast)):
+        assert a.dtype == b.dtype and torch.equal(a, b), i
+
+
 def test_sublayer_hip_matches_reference_backend(hip_device):
     """The config-5 sublayer (fused QKV GEMM, QK-norm + RoPE kernel, flash
     attention, wo) under bf16 autocast against the same module run with the
