@@ -59,8 +59,8 @@ int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
 int mm1_attn_delta(const void* o, const void* dO, float* delta,
                    int B, int S, int H, int D, void* stream);
 
-/* Bytes of fp32 scratch mm1_attn_bwd needs for the per-head dK/dV partial sums
- * (0 when H == Hkv).  No counterpart in the reference, whose backward takes
+/* Bytes of fp32 scratch mm1_attn_bwd needs for the dK/dV partial sums
+ * (0 when H == Hkv): G = H / Hkv slots of [B, S, Hkv, D] for dK and for dV.  No counterpart in the reference, whose backward takes
  * caller-zeroed fp32 dQ/dK/dV accumulators instead (attention_tilelang.py:381-383). */
 size_t mm1_attn_bwd_workspace_size(int B, int S, int H, int Hkv, int D);
 
@@ -79,11 +79,17 @@ int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
  * separately (same arguments and checks as mm1_attn_bwd).  mm1_attn_bwd runs
  * mm1_attn_bwd_dkdv then mm1_attn_bwd_dq_reduce; mm1_attn_bwd_dkdv_reduce
  * followed by mm1_attn_bwd_dq is the same result in two launches.
- *  - mm1_attn_bwd_dkdv: dK/dV.  With H == Hkv it writes bf16 dk, dv directly;
- *    otherwise it writes the per-query-head fp32 partial sums into `workspace`
- *    ([2][G][B][S][Hkv][D], G = H / Hkv) and leaves dk/dv untouched.
- *  - mm1_attn_bwd_dkdv_reduce: sums the G partials of each KV head and writes
- *    bf16 dk, dv (no-op when H == Hkv).
+ *  - mm1_attn_bwd_dkdv: dK/dV.  With H == Hkv it writes bf16 dk, dv directly.
+ *    Otherwise, with the per-head tilings (0, 1) it writes the per-query-head
+ *    fp32 partial sums into `workspace` ([2][G][B][S][Hkv][D], G = H / Hkv)
+ *    and leaves dk/dv untouched; with the grouped tiling (2) it writes bf16
+ *    dk, dv directly for the key tiles one workgroup covers and fp32 partials
+ *    (one slot per chunk, see mm1_attn_dkdv_plan) for the others.
+ *  - mm1_attn_bwd_dkdv_reduce: sums the partials of each KV head and writes
+ *    bf16 dk, dv (no-op when H == Hkv).  It follows the layout of the default
+ *    dK/dV tiling (MM1_DKDV_VARIANT, read per call), so it must see the same
+ *    environment and `causal` as the mm1_attn_bwd_dkdv call before it; the
+ *    same holds for mm1_attn_bwd_dq_reduce.
  *  - mm1_attn_bwd_dq: bf16 dq.
  *  - mm1_attn_bwd_dq_reduce: bf16 dq, and the group sum of
  *    mm1_attn_bwd_dkdv_reduce done by the tail of the same launch (must run
@@ -96,7 +102,7 @@ int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* d
                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                       void* stream);
 int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
-                             int B, int S, int H, int Hkv, int D, void* stream);
+                             int B, int S, int H, int Hkv, int D, int causal, void* stream);
 int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                     const float* lse2, const float* delta, void* dq,
                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
@@ -146,16 +152,33 @@ int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* 
  * blocks to the 4 SE lanes, packs each lane into its CUs in bins of equal
  * modelled work and lists the blocks in the order the CUs ask for them.
  * This call returns the table a launch of grid `kind` (MM1_TILES_FWD,
- * MM1_TILES_DQ) with tiling `tiles` builds for a device with `cus` compute
- * units: entry b is the row block of launch slot b in the default numbering
- * (0xFFFF for a slot without one).  Writes min(n, cap) entries and returns
- * n, the launch's grid size; 0 when the launch uses the default order
- * (MM1_TILES_DKDV, causal == 0, a tiling with two workgroups per CU, more
- * blocks than the table holds, no modelled gain, or MM1_DISPATCH_ORDER=0 in
- * the environment, read per call); a negative MM1_E_* code for bad
+ * MM1_TILES_DQ, or MM1_TILES_DKDV with the grouped tiling 2) with tiling
+ * `tiles` builds for a device with `cus` compute units: entry b is the work
+ * item of launch slot b in the default numbering (0xFFFF for a slot without
+ * one).  Writes min(n, cap) entries and returns n, the launch's grid size; 0
+ * when the launch uses the default order (the per-head dK/dV tilings,
+ * causal == 0 for the forward / dQ, a tiling with two workgroups per CU,
+ * more items than the table holds, no modelled gain, or MM1_DISPATCH_ORDER=0
+ * in the environment, read per call); a negative MM1_E_* code for bad
  * arguments.  Runs on the host only. */
 int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, int causal, int cus,
                             unsigned short* out, int cap);
+
+/* Work plan of the grouped dK/dV tiling (MM1_TILES_DKDV tiling 2; diagnostic,
+ * no counterpart in the reference).  A workgroup of that launch owns one
+ * 128-key tile of one (batch, KV head) and walks the 32-query tiles of all
+ * G = H / Hkv query heads of the group, so K and V are read once per group
+ * and the sum over the group's heads stays in registers.  Key tile kt meets
+ * len = G * ceil((S - q0) / 32) query tiles (q0 = 128 * kt when causal, else
+ * 0), split into nc = min(C, max(1, ceil(len / L))) chunks; chunk c walks
+ * tiles c, c + nc, c + 2 * nc, ... < len of the position-major walk
+ * (position tiles from the sequence end down, the G heads of each in turn).  L is the candidate chunk length whose workgroup order
+ * the library's dispatch model rates fastest for `cus` compute units.
+ * Writes out[0..4] = L, C, split_keys (keys [0, split_keys) of each batch lie
+ * in key tiles with more than one chunk), the number of items in the default
+ * numbering (n_kt * C * B * Hkv, item j = (kt * C + c) * B * Hkv + b * Hkv + g)
+ * and the launch's table size (0: default order).  Runs on the host only. */
+int mm1_attn_dkdv_plan(int B, int S, int H, int Hkv, int causal, int cus, int* out);
 
 /* QK-RMSNorm + RoPE between the fused QKV projection and the attention
  * kernel.  Replaces, in Attention.forward (attention_tilelang.py:483-487), the

@@ -34,7 +34,8 @@ SIGNATURES = {
     "mm1_attn_bwd_dkdv": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_attn_bwd_dkdv_reduce": (_c_int, [_vp, _c_size, _vp, _vp,
-                                          _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
+                                          _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "mm1_attn_dkdv_plan": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "mm1_attn_bwd_dq": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_attn_bwd_dq_reduce": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,

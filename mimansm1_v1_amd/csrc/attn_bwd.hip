@@ -345,13 +345,14 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // segments of lead).  Tiles whose queries all precede a pair's keys (causal)
 // are computed with the mask (P = 0): the pair would otherwise only wait at
 // the barrier.
-template <int NSTAGE, bool CAUSAL>
+template <int NSTAGE, bool CAUSAL, bool GROUP, bool RAGGED>
 __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     float* __restrict__ ws_dk, float* __restrict__ ws_dv,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order) {
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order,
+    int chunk_tiles, int max_chunks, const DispatchOrder ord) {
   static_assert(NSTAGE >= 6, "ring depth: at least 6");
   constexpr int BQ = 32;                  // query positions per tile
   constexpr int QT = BQ * HD * 2;         // one 32 x 128 bf16 operand tile
@@ -363,13 +364,54 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
   const int pair = w & 3;
   const bool pwave = w < 4;
-  const int nbh = B * H;
-  const int item = key_tile_item(blockIdx.x, nbh, (S + 127) / 128, order);
-  if (item < 0) return;
-  const int kt = item / nbh;              // heaviest key tiles first
-  const int bh = item % nbh;
-  const int b = bh / H, hq = bh % H;
-  const int g = hq / G, hh = hq % G;
+  const int n_kt = (S + 127) / 128;
+  // The work of this workgroup: key tile kt of (b, g) and the n_u query
+  // tiles u0, u0 + ustep, u0 + 2*ustep, ... of the position-major walk over
+  // HW heads (tile u: position tile u / HW counted from the sequence end,
+  // head hbase + u % HW of the group).  The chunks of a split key tile
+  // interleave, so every workgroup starts at the sequence end and those that
+  // run together stream the same rows.  The sums go to partial slot `part`
+  // of `nparts`, or straight to dk/dv when nparts == 1.
+  int b, g, kt, n_qt, u0, n_u, ustep, part, nparts, hbase, HW;
+  if constexpr (GROUP) {
+    const int j = dispatch_item(ord);
+    if (j < 0) return;
+    const int nbg = B * Hkv;
+    const int bg = j % nbg, r = j / nbg;
+    kt = r / max_chunks;                  // heaviest key tiles first
+    const int c = r - kt * max_chunks;
+    if (kt >= n_kt) return;
+    b = bg / Hkv;
+    g = bg - b * Hkv;
+    n_qt = dkdv_n_qt(S, kt, CAUSAL);
+    const int len = G * n_qt;
+    nparts = dkdv_chunks(len, chunk_tiles, max_chunks);
+    if (c >= nparts) return;              // an empty item of the default numbering
+    u0 = c;
+    ustep = nparts;   // <= max_chunks <= G: one wrap of the head index at most
+    n_u = (len - c + nparts - 1) / nparts;
+    part = c;
+    hbase = 0;
+    HW = G;
+  } else {
+    const int nbh = B * H;
+    const int item = key_tile_item(blockIdx.x, nbh, n_kt, order);
+    if (item < 0) return;
+    kt = item / nbh;                      // heaviest key tiles first
+    const int bh = item % nbh;
+    b = bh / H;
+    const int hq = bh % H;
+    g = hq / G;
+    const int hh = hq % G;
+    n_qt = dkdv_n_qt(S, kt, CAUSAL);
+    u0 = 0;
+    ustep = 1;
+    n_u = n_qt;
+    part = hh;
+    nparts = G;
+    hbase = hh;
+    HW = 1;
+  }
   const int kw0 = kt * 128 + 32 * pair;   // this pair's first key
   const int key = kw0 + l32;
   // mailbox of this pair, two slots; [register group a4][lane] x 4 floats so
@@ -377,39 +419,52 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   float* const mbox = reinterpret_cast<float*>(smem + NSTAGE * BUF + pair * 2 * MBOX) + lane * 4;
 
   const int q_begin = CAUSAL ? kt * 128 : 0;
-  const int n_qt = (S - q_begin + BQ - 1) / BQ;
   const long qstride = (long)H * HD;
-  const __bf16* qbase = q + ((long)b * S * H + hq) * HD;
-  const __bf16* dobase = dO + ((long)b * S * H + hq) * HD;
-  const float* lse_row = lse2 + ((long)b * H + hq) * S;
-  const float* dl_row = delta + ((long)b * H + hq) * S;
+  // walk head hh: Q / dO rows at grp_rows + hh*HD, lse2 / Delta at
+  // vec_src + hh*S (lanes 0-31 lse2, lanes 32-63 Delta)
+  const long grp_rows = ((long)b * S * H + g * G + hbase) * HD;
+  const float* vec_src = (h ? delta : lse2) + ((long)b * H + g * G + hbase) * S + l32;
 
-  // Query tiles are walked from the sequence end down to q_begin, so the
-  // workgroups of one head that start together read the same tiles together.
-  // Only the first tile walked (it = 0) can be partial (S % 32 != 0).
-  auto tile_p0 = [&](int it) { return q_begin + (n_qt - 1 - it) * BQ; };
+  // Position tiles are walked from the sequence end down to q_begin, so the
+  // workgroups that start together read the same rows together; the first
+  // position tile can be partial (S % 32 != 0).  Tile cursors (walk head,
+  // position tile) advance one tile at a time.
+  auto tile_p0 = [&](int t) { return q_begin + (n_qt - 1 - t) * BQ; };
+  auto advance = [&](int& hh, int& t) {
+    hh += ustep;
+    if (hh >= HW) {
+      hh -= HW;
+      ++t;
+    }
+  };
   // LDS DMA, per wave and tile: row quad w of Q and of dO; wave 0 adds the
-  // lse2 | Delta vector (lanes 0-31 lse2, lanes 32-63 Delta).
+  // lse2 | Delta vector.
   const uint32_t dma_off = tile_lane_off(qstride, tid);
   const uint32_t lds_smem = __builtin_amdgcn_readfirstlane(lds_addr(smem));
   const uint32_t lds_quad = lds_smem + w * 1024;       // this wave's row quad in slot 0
   const long quad_rows = (long)(4 * w) * qstride;      // its first row, in elements
-  const float* vec_src = (h ? dl_row : lse_row) + l32;
-  auto issue_full = [&](int slot, int p0) {
-    const uint32_t l = lds_quad + slot * BUF;
-    dma16_sbase(dma_off, qbase + (long)p0 * qstride + quad_rows, l);
-    dma16_sbase(dma_off, dobase + (long)p0 * qstride + quad_rows, l + QT);
-    if (w == 0) dma4(vec_src + p0, lds_smem + slot * BUF + 2 * QT);
-  };
-  for (int it = 0; it < NSTAGE - 3 && it < n_qt; ++it) {
-    const int p0 = tile_p0(it);
-    if (p0 + BQ <= S) {
-      issue_full(it, p0);
-    } else {
-      tile32_dma(smem + it * BUF, qbase + (long)p0 * qstride, qstride, S - p0, dma_off, tid);
-      tile32_dma(smem + it * BUF + QT, dobase + (long)p0 * qstride, qstride, S - p0, dma_off, tid);
-      if (w == 0) dma4((h ? dl_row : lse_row) + min(p0 + l32, S - 1), lds_smem + it * BUF + 2 * QT);
+  // Only position tile 0 can be partial, and only when S % 32 != 0
+  // (RAGGED); the walks without partial tiles carry no code for them.
+  auto issue = [&](int slot, int hh, int t, auto may_be_partial) {
+    const int p0 = tile_p0(t);
+    const long rows = grp_rows + (long)hh * HD + (long)p0 * qstride;
+    const float* vs = vec_src + (long)hh * S;
+    if (!decltype(may_be_partial)::value || p0 + BQ <= S) {
+      const uint32_t l = lds_quad + slot * BUF;
+      dma16_sbase(dma_off, q + rows + quad_rows, l);
+      dma16_sbase(dma_off, dO + rows + quad_rows, l + QT);
+      if (w == 0) dma4(vs + p0, lds_smem + slot * BUF + 2 * QT);
+    } else {   // same DMA count per wave as a full tile
+      tile32_dma(smem + slot * BUF, q + rows, qstride, S - p0, dma_off, tid);
+      tile32_dma(smem + slot * BUF + QT, dO + rows, qstride, S - p0, dma_off, tid);
+      if (w == 0) dma4(vs + min(p0, S - 1 - l32), lds_smem + slot * BUF + 2 * QT);
     }
+  };
+  int itl = u0 / HW, ih = u0 - itl * HW;      // issue cursor
+  int ch = ih, ctl = itl;                     // compute cursor (tile s of the walk)
+  for (int it = 0; it < NSTAGE - 3 && it < n_u; ++it) {
+    issue(it, ih, itl, std::bool_constant<RAGGED>{});
+    advance(ih, itl);
   }
 
   // This lane's key row of K (P wave) or V (dS wave) as the B operand.
@@ -444,7 +499,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   if (pwave) snext = product(smem);
 
   // Segment s.  tn, tc, tp, tp2: ring slots of tiles s+1, s, s-1, s-2.
-  // CUR: s < n_qt; PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a
+  // CUR: s < n_u; PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a
   // later segment reads what this one publishes (mailbox, ring).  In the last
   // segment with CUR, S(s+1) reads a slot holding another tile (or nothing
   // yet) and is discarded: every read stays inside the ring.
@@ -453,7 +508,11 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     constexpr bool PW = decltype(role)::value;
     constexpr bool CUR = decltype(cur)::value, PREV = decltype(prev)::value;
     constexpr bool PREV2 = decltype(prev2)::value, SYNC = decltype(sync)::value;
-    if (CUR && s + NSTAGE - 3 < n_qt) issue_full(refill, tile_p0(s + NSTAGE - 3));
+    if (CUR && s + NSTAGE - 3 < n_u) {
+      // a per-head walk meets position tile 0 only in the prologue
+      issue(refill, ih, itl, std::bool_constant<RAGGED && GROUP>{});
+      advance(ih, itl);
+    }
     if constexpr (PW) {
       f32x16 sv;
       if constexpr (CUR) {
@@ -479,7 +538,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
       }
       if constexpr (CUR) {
         // causal / past-the-end mask, only in the tiles that need it
-        const int p0 = tile_p0(s);
+        const int p0 = tile_p0(ctl);
         if ((CAUSAL && p0 < kw0 + 31) || p0 + BQ > S) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
@@ -531,9 +590,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
       }
       if constexpr (CUR) dpp = dpn;
     }
+    if constexpr (CUR) advance(ch, ctl);
     if constexpr (SYNC) {
       // tile s+2 must have landed; the newer prefetches stay in flight
-      if (s + NSTAGE - 3 < n_qt) {
+      if (s + NSTAGE - 3 < n_u) {
         if (w == 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (NSTAGE - 5)) : "memory");
         else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (NSTAGE - 5)) : "memory");
       } else {
@@ -544,7 +604,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   };
 
   // Each role runs its own specialised copy of the loop (same barriers).
-  // Segments 2 .. n_qt-1 are unrolled NSTAGE at a time so that every ring
+  // Segments 2 .. n_u-1 are unrolled NSTAGE at a time so that every ring
   // slot, and so every LDS offset, is a compile-time constant.
   using T = std::true_type;
   using F = std::false_type;
@@ -552,7 +612,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   auto run = [&](auto role) {
     const char* s0p = slot(0);
     const char* s1p = slot(1);
-    if (n_qt == 1) {
+    if (n_u == 1) {
       segment(s1p, s0p, s0p, s0p, NSTAGE - 3, 0, role, T{}, F{}, F{}, T{});
       segment(s0p, s0p, s0p, s0p, 0, 1, role, F{}, T{}, F{}, F{});
       segment(s0p, s0p, s0p, s0p, 0, 2, role, F{}, F{}, T{}, F{});
@@ -560,20 +620,20 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     }
     segment(s1p, s0p, s0p, s0p, NSTAGE - 3, 0, role, T{}, F{}, F{}, T{});
     segment(slot(2), s1p, s0p, s0p, NSTAGE - 2, 1, role, T{}, T{}, F{}, T{});
-    for (int b0 = 2; b0 < n_qt; b0 += NSTAGE) {
+    for (int b0 = 2; b0 < n_u; b0 += NSTAGE) {
       unroll_while<0, NSTAGE>([&](auto j) {
         constexpr int C = (2 + decltype(j)::value) % NSTAGE;
         const int s = b0 + decltype(j)::value;
-        if (s >= n_qt) return false;
+        if (s >= n_u) return false;
         segment(slot((C + 1) % NSTAGE), slot(C), slot((C + NSTAGE - 1) % NSTAGE),
                 slot((C + NSTAGE - 2) % NSTAGE), (C + NSTAGE - 3) % NSTAGE, s, role, T{}, T{}, T{}, T{});
         return true;
       });
     }
-    const char* tl = slot((n_qt - 1) % NSTAGE);
-    const char* tl2 = slot((n_qt - 2) % NSTAGE);
-    segment(tl, tl, tl, tl2, 0, n_qt, role, F{}, T{}, T{}, F{});
-    segment(tl, tl, tl, tl, 0, n_qt + 1, role, F{}, F{}, T{}, F{});
+    const char* tl = slot((n_u - 1) % NSTAGE);
+    const char* tl2 = slot((n_u - 2) % NSTAGE);
+    segment(tl, tl, tl, tl2, 0, n_u, role, F{}, T{}, T{}, F{});
+    segment(tl, tl, tl, tl, 0, n_u + 1, role, F{}, F{}, T{}, F{});
   };
   if (pwave) run(std::true_type{});
   else run(std::false_type{});
@@ -582,7 +642,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // D layout of dK^T / dV^T: register r of block db holds column
   // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
   const float scale_out = pwave ? 1.f : sm_scale;
-  if (G == 1) {
+  if (nparts == 1) {
     __bf16* row = (pwave ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -595,7 +655,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
       }
     }
   } else {
-    const long slot = (long)hh * B * S * Hkv * HD;
+    const long slot = (long)part * B * S * Hkv * HD;
     float* row = (pwave ? ws_dv : ws_dk) + slot + ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -610,54 +670,79 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   }
 }
 
-// Sum the G per-head partials of dK and dV (workspace [G][n]) at element i
-// .. i+3 and round to bf16 once; the sum runs in head order, so the result
-// does not depend on which thread or kernel does it.
-__device__ __forceinline__ void reduce4(const float* __restrict__ ws_dk, const float* __restrict__ ws_dv,
-                                        __bf16* __restrict__ dk, __bf16* __restrict__ dv, long n, int G, long i) {
-  f32x4 sk = *reinterpret_cast<const f32x4*>(ws_dk + i);
-  f32x4 sv = *reinterpret_cast<const f32x4*>(ws_dv + i);
-  for (int j = 1; j < G; ++j) {
-    sk += *reinterpret_cast<const f32x4*>(ws_dk + (long)j * n + i);
-    sv += *reinterpret_cast<const f32x4*>(ws_dv + (long)j * n + i);
-  }
-  bf16x4 ok, ov;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) { ok[c] = (__bf16)sk[c]; ov[c] = (__bf16)sv[c]; }
-  *reinterpret_cast<bf16x4*>(dk + i) = ok;
-  *reinterpret_cast<bf16x4*>(dv + i) = ov;
-}
-
-__global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(
-    const float* __restrict__ ws_dk, const float* __restrict__ ws_dv,
-    __bf16* __restrict__ dk, __bf16* __restrict__ dv, long n, int G) {
-  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i >= n) return;
-  reduce4(ws_dk, ws_dv, dk, dv, n, G, i);
-}
-
-// Where the dQ kernel folds the dK/dV group sum in: the last n_red workgroups
-// of its grid each reduce one contiguous slice of the n elements after their
-// own work (with n_red = the grid size, a small slice per workgroup, spread
-// over the whole launch).
+// The dK/dV partial sums to reduce, and where the reduction runs.  Two
+// layouts, both [slot][B][S][Hkv][D] fp32 for dK and for dV:
+//   per-head dK/dV (chunk_tiles == 0): slot = query head of the group; every
+//     element sums its G slots;
+//   grouped dK/dV (chunk_tiles > 0): slot = chunk of the key tile; only keys
+//     [0, split_keys) of each batch are split, and a key of tile kt sums its
+//     dkdv_chunks(G * dkdv_n_qt(S, kt), chunk_tiles, max_chunks) slots (the
+//     other keys were written as bf16 by the dK/dV kernel itself).
+// The dQ kernel folds the reduction in: the last n_red workgroups of its grid
+// each reduce one contiguous slice after their own work (with n_red = the
+// grid size, a small slice per workgroup, spread over the whole launch).
 struct TailReduce {
   const float* ws_dk;
   const float* ws_dv;
   __bf16* dk;
   __bf16* dv;
-  long n;
+  long n;           // elements of one slot: B*S*Hkv*D
   int G;
-  int n_red;   // 0: no reduction in this launch
+  int n_red;        // 0: no reduction in this launch
+  int chunk_tiles;  // grouped dK/dV: the plan's chunk length; 0: per-head
+  int max_chunks;
+  int split_keys;
+  int S, Hkv;
+  int causal;
 };
+
+// Elements of the reduction (a multiple of 4).
+__host__ __device__ inline long reduce_len(const TailReduce& red) {
+  return red.chunk_tiles > 0 ? red.n / red.S * red.split_keys : red.n;
+}
+
+// Sum the slots of reduction elements i .. i+3 in slot order and round to
+// bf16 once, so the result does not depend on which thread or kernel does it.
+__device__ __forceinline__ void reduce_at(const TailReduce& red, long i) {
+  long e = i;
+  int slots = red.G;
+  if (red.chunk_tiles > 0) {
+    const long row = (long)red.Hkv * HD;
+    const long per_b = red.split_keys * row;
+    const long bb = i / per_b;
+    const long r = i - bb * per_b;
+    e = bb * red.S * row + r;
+    const int kt = (int)(r / row) >> 7;
+    slots = dkdv_chunks(red.G * dkdv_n_qt(red.S, kt, red.causal != 0), red.chunk_tiles, red.max_chunks);
+    if (slots <= 1) return;
+  }
+  f32x4 sk = *reinterpret_cast<const f32x4*>(red.ws_dk + e);
+  f32x4 sv = *reinterpret_cast<const f32x4*>(red.ws_dv + e);
+  for (int j = 1; j < slots; ++j) {
+    sk += *reinterpret_cast<const f32x4*>(red.ws_dk + (long)j * red.n + e);
+    sv += *reinterpret_cast<const f32x4*>(red.ws_dv + (long)j * red.n + e);
+  }
+  bf16x4 ok, ov;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) { ok[c] = (__bf16)sk[c]; ov[c] = (__bf16)sv[c]; }
+  *reinterpret_cast<bf16x4*>(red.dk + e) = ok;
+  *reinterpret_cast<bf16x4*>(red.dv + e) = ov;
+}
+
+__global__ __launch_bounds__(256) void attn_dkdv_reduce_kernel(const TailReduce red) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= reduce_len(red)) return;
+  reduce_at(red, i);
+}
 
 // The slice of launch slot blockIdx.x (slices go to the last n_red slots).
 __device__ __forceinline__ void tail_reduce(const TailReduce& red, int tid, int nthreads) {
   const int slice = (int)blockIdx.x - ((int)gridDim.x - red.n_red);
   if (slice < 0) return;
-  const long per = ((red.n + red.n_red - 1) / red.n_red + 3) & ~3L;
-  const long end = min(red.n, per * (slice + 1));
-  for (long i = per * slice + 4L * tid; i < end; i += 4L * nthreads)
-    reduce4(red.ws_dk, red.ws_dv, red.dk, red.dv, red.n, red.G, i);
+  const long len = reduce_len(red);
+  const long per = ((len + red.n_red - 1) / red.n_red + 3) & ~3L;
+  const long end = min(len, per * (slice + 1));
+  for (long i = per * slice + 4L * tid; i < end; i += 4L * nthreads) reduce_at(red, i);
 }
 
 // ---------------------------------------------------------------------------
@@ -837,8 +922,37 @@ size_t bwd_workspace_bytes(int B, int S, int H, int Hkv) {
   return (size_t)2 * G * B * S * Hkv * HD * sizeof(float);
 }
 
-// variant: 0 = attn_dkdv_pipe_kernel (7-slot ring of 32-query tiles),
-//          1 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries).
+// The reduction that follows dK/dV tiling `dkdv_variant` (n_red = 0 when
+// there is nothing to sum).
+TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
+                       bool causal, int dkdv_variant) {
+  const int G = H / Hkv;
+  TailReduce red{};
+  red.G = G;
+  red.S = S;
+  red.Hkv = Hkv;
+  red.causal = causal ? 1 : 0;
+  if (!workspace || G <= 1) return red;
+  red.n = (long)B * S * Hkv * HD;
+  red.ws_dk = static_cast<const float*>(workspace);
+  red.ws_dv = red.ws_dk + (long)G * red.n;
+  red.dk = static_cast<__bf16*>(dk);
+  red.dv = static_cast<__bf16*>(dv);
+  if (dkdv_variant == 2) {
+    const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
+    red.chunk_tiles = plan.L;
+    red.max_chunks = plan.C;
+    red.split_keys = plan.split_keys;
+  }
+  red.n_red = reduce_len(red) > 0 ? 1 << 30 : 0;
+  return red;
+}
+
+// variant: 0 = attn_dkdv_pipe_kernel (7-slot ring of 32-query tiles, one
+//              workgroup per (key tile, query head)),
+//          1 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries),
+//          2 = attn_dkdv_pipe_kernel over the whole GQA group per key tile
+//              (chunked by dkdv_plan).
 hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
                            const float* lse2, const float* delta, void* dk, void* dv,
                            void* workspace, int B, int S, int H, int Hkv, bool causal,
@@ -856,31 +970,56 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
   auto dvp = static_cast<__bf16*>(dv);
   const int n_ktiles = (S + 127) / 128;
   const KeyTileOrder order = key_tile_order(B * H);
-  dim3 grid(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
-#define MM1_DKDV_LAUNCH(KERNEL)                                                               \
+  const bool ragged = S % 32 != 0;
+  if (variant == 2) {
+    const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
+    const dim3 grid(plan.order.n ? plan.order.n : plan.n_items);
+#define MM1_DKDV_GROUP(CS, RG)                                                                  \
+  hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, true, RG>), grid, dim3(512), 0, stream, qp, kp, vp, \
+                     dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale,   \
+                     order, plan.L, plan.C, plan.order)
+    if (causal) {
+      if (ragged) MM1_DKDV_GROUP(true, true);
+      else MM1_DKDV_GROUP(true, false);
+    } else {
+      if (ragged) MM1_DKDV_GROUP(false, true);
+      else MM1_DKDV_GROUP(false, false);
+    }
+#undef MM1_DKDV_GROUP
+    return hipGetLastError();
+  }
+  const dim3 grid(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
+  if (variant == 1) {
+#define MM1_DKDV_PAIRED(KERNEL)                                                               \
   hipLaunchKernelGGL(KERNEL, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta, ws_dk, \
                      ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, order)
-  if (variant == 1) {
-    if (causal) MM1_DKDV_LAUNCH(attn_dkdv_kernel<true>);
-    else MM1_DKDV_LAUNCH(attn_dkdv_kernel<false>);
+    if (causal) MM1_DKDV_PAIRED(attn_dkdv_kernel<true>);
+    else MM1_DKDV_PAIRED(attn_dkdv_kernel<false>);
+#undef MM1_DKDV_PAIRED
   } else {
-    if (causal) MM1_DKDV_LAUNCH((attn_dkdv_pipe_kernel<7, true>));
-    else MM1_DKDV_LAUNCH((attn_dkdv_pipe_kernel<7, false>));
+    const DispatchOrder& none = dispatch_order(row_block_grid(0, B, S, H, Hkv), false);
+#define MM1_DKDV_HEAD(CS, RG)                                                                   \
+  hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, false, RG>), grid, dim3(512), 0, stream, qp, kp, vp, \
+                     dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale,    \
+                     order, 0, G, none)
+    if (causal) {
+      if (ragged) MM1_DKDV_HEAD(true, true);
+      else MM1_DKDV_HEAD(true, false);
+    } else {
+      if (ragged) MM1_DKDV_HEAD(false, true);
+      else MM1_DKDV_HEAD(false, false);
+    }
+#undef MM1_DKDV_HEAD
   }
-#undef MM1_DKDV_LAUNCH
   return hipGetLastError();
 }
 
 hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
-                             hipStream_t stream) {
-  const int G = H / Hkv;
-  if (G <= 1) return hipSuccess;
-  const long n_kv = (long)B * S * Hkv * HD;
-  const float* ws_dk = static_cast<const float*>(workspace);
-  const float* ws_dv = ws_dk + (long)G * n_kv;
-  const long blocks = (n_kv / 4 + 255) / 256;
-  hipLaunchKernelGGL(attn_dkdv_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
-                     ws_dk, ws_dv, static_cast<__bf16*>(dk), static_cast<__bf16*>(dv), n_kv, G);
+                             bool causal, int dkdv_variant, hipStream_t stream) {
+  const TailReduce red = make_reduce(workspace, dk, dv, B, S, H, Hkv, causal, dkdv_variant);
+  if (red.n_red == 0) return hipSuccess;
+  const long blocks = (reduce_len(red) / 4 + 255) / 256;
+  hipLaunchKernelGGL(attn_dkdv_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, red);
   return hipGetLastError();
 }
 
@@ -905,29 +1044,21 @@ static void launch_dq_t(const __bf16* q, const __bf16* k, const __bf16* v, const
 
 // variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
 //          1 = 8 waves x 3-stage ring (one workgroup per CU).
-// workspace != nullptr: also sum the G dK/dV partials it holds into dk, dv
-// (what launch_bwd_reduce does), in the dQ grid's tail.
+// workspace != nullptr: also sum the dK/dV partials that tiling dkdv_variant
+// left in it into dk, dv (what launch_bwd_reduce does), in the dQ grid's tail.
 hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                          const float* lse2, const float* delta, void* dq,
                          const void* workspace, void* dk, void* dv,
                          int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
-                         hipStream_t stream) {
+                         int dkdv_variant, hipStream_t stream) {
   const float scale2 = sm_scale * 1.4426950408889634f;
   auto qp = static_cast<const __bf16*>(q);
   auto kp = static_cast<const __bf16*>(k);
   auto vp = static_cast<const __bf16*>(v);
   auto dop = static_cast<const __bf16*>(dO);
   auto dqp = static_cast<__bf16*>(dq);
-  const int G = H / Hkv;
-  TailReduce red{nullptr, nullptr, nullptr, nullptr, 0, G, 0};
-  if (workspace && G > 1) {
-    red.n = (long)B * S * Hkv * HD;
-    red.ws_dk = static_cast<const float*>(workspace);
-    red.ws_dv = red.ws_dk + (long)G * red.n;
-    red.dk = static_cast<__bf16*>(dk);
-    red.dv = static_cast<__bf16*>(dv);
-    red.n_red = 1 << 30;   // every workgroup of the grid takes a slice
-  }
+  // with n_red = 1 << 30 every workgroup of the grid takes a slice
+  const TailReduce red = make_reduce(workspace, dk, dv, B, S, H, Hkv, causal, dkdv_variant);
   const DispatchOrder& ord = dispatch_order(row_block_grid(variant, B, S, H, Hkv), causal);
   if (variant == 1)
     launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);

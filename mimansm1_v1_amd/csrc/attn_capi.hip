@@ -21,12 +21,12 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
                            void* workspace, int B, int S, int H, int Hkv, bool causal,
                            float sm_scale, int variant, hipStream_t stream);
 hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
-                             hipStream_t stream);
+                             bool causal, int dkdv_variant, hipStream_t stream);
 hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                          const float* lse2, const float* delta, void* dq,
                          const void* workspace, void* dk, void* dv,
                          int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
-                         hipStream_t stream);
+                         int dkdv_variant, hipStream_t stream);
 size_t qknorm_bwd_workspace_bytes();
 hipError_t launch_qknorm_fwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
                              const float* sin_t, void* q, void* k, void* v, int B, int S, int H, int Hkv,
@@ -74,6 +74,7 @@ const char* const kFwdTiles[] = {
 const char* const kDkdvTiles[] = {
     "block_M=128 block_N=32 waves=8 stages=7 schedule=pipelined",
     "block_M=128 block_N=64 waves=8 stages=3 schedule=paired",
+    "block_M=128 block_N=32 waves=8 stages=7 schedule=group",
 };
 const char* const kDqTiles[] = {
     "block_M=128 block_N=64 waves=4 stages=2 schedule=ring",
@@ -184,7 +185,7 @@ static int bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                   const float* lse2, const float* delta, void* dq, void* dk, void* dv,
                   const void* workspace, size_t workspace_bytes, bool reduce,
                   int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                  int tiles, void* stream) {
+                  int tiles, int dkdv_tiles, void* stream) {
   if (!q || !k || !v || !dO || !lse2 || !delta || !dq) return MM1_E_NULL;
   if (reduce && (!dk || !dv)) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
@@ -196,10 +197,11 @@ static int bwd_dq(const void* q, const void* k, const void* v, const void* dO,
       (reduce && (!aligned16(dk) || !aligned16(dv))) || (need > 0 && !aligned16(workspace)))
     return MM1_E_ALIGN;
   const int variant = pick_tiles(MM1_TILES_DQ, tiles);
-  if (variant < 0) return MM1_E_TILES;
+  const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, dkdv_tiles);
+  if (variant < 0 || dkdv_variant < 0) return MM1_E_TILES;
   return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, need > 0 ? workspace : nullptr,
                                      reduce ? dk : nullptr, reduce ? dv : nullptr,
-                                     B, S, H, Hkv, causal != 0, sm_scale, variant,
+                                     B, S, H, Hkv, causal != 0, sm_scale, variant, dkdv_variant,
                                      static_cast<hipStream_t>(stream)));
 }
 
@@ -213,7 +215,7 @@ int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* d
 }
 
 int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
-                             int B, int S, int H, int Hkv, int D, void* stream) {
+                             int B, int S, int H, int Hkv, int D, int causal, void* stream) {
   if (!dk || !dv) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
   if (rc) return rc;
@@ -221,7 +223,9 @@ int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void
   if (need == 0) return MM1_OK;
   if (!workspace || workspace_bytes < need) return MM1_E_WORKSPACE;
   if (!aligned16(workspace) || !aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
-  return from_hip(mm1::launch_bwd_reduce(workspace, dk, dv, B, S, H, Hkv,
+  const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, -1);
+  if (dkdv_variant < 0) return MM1_E_TILES;
+  return from_hip(mm1::launch_bwd_reduce(workspace, dk, dv, B, S, H, Hkv, causal != 0, dkdv_variant,
                                          static_cast<hipStream_t>(stream)));
 }
 
@@ -230,7 +234,7 @@ int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                     void* stream) {
   return bwd_dq(q, k, v, dO, lse2, delta, dq, nullptr, nullptr, nullptr, 0, false, B, S, H, Hkv, D,
-                causal, sm_scale, -1, stream);
+                causal, sm_scale, -1, -1, stream);
 }
 
 int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const void* dO,
@@ -239,7 +243,7 @@ int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const vo
                            int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                            void* stream) {
   return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
-                D, causal, sm_scale, -1, stream);
+                D, causal, sm_scale, -1, -1, stream);
 }
 
 int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* dO,
@@ -252,12 +256,12 @@ int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* 
   // error launches nothing.
   if (!dq) return MM1_E_NULL;
   if (!aligned16(dq)) return MM1_E_ALIGN;
-  if (pick_tiles(MM1_TILES_DQ, dq_tiles) < 0) return MM1_E_TILES;
+  if (pick_tiles(MM1_TILES_DQ, dq_tiles) < 0 || pick_tiles(MM1_TILES_DKDV, dkdv_tiles) < 0) return MM1_E_TILES;
   int rc = bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes, B, S, H, Hkv, D,
                     causal, sm_scale, dkdv_tiles, stream);
   if (rc) return rc;
   return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
-                D, causal, sm_scale, dq_tiles, stream);
+                D, causal, sm_scale, dq_tiles, dkdv_tiles, stream);
 }
 
 int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, int causal, int cus,
@@ -268,11 +272,26 @@ int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, i
   if (const int rc = check_shape(B, S, H, Hkv, mm1::HD)) return rc;
   if (cus < 1 || cap < 0) return MM1_E_SHAPE;
   if (cap > 0 && !out) return MM1_E_NULL;
-  if (kind == MM1_TILES_DKDV) return 0;   // the dK/dV grid always runs in the default order
+  if (kind == MM1_TILES_DKDV && variant != 2) return 0;   // per-head grids: default order
   const mm1::DispatchOrder& ord =
-      mm1::dispatch_order_for(mm1::row_block_grid(variant, B, S, H, Hkv), causal != 0, cus);
+      kind == MM1_TILES_DKDV
+          ? mm1::dkdv_plan_for(B, S, H, Hkv, causal != 0, cus).order
+          : mm1::dispatch_order_for(mm1::row_block_grid(variant, B, S, H, Hkv), causal != 0, cus);
   for (int i = 0; i < ord.n && i < cap; ++i) out[i] = ord.item[i];
   return ord.n;
+}
+
+int mm1_attn_dkdv_plan(int B, int S, int H, int Hkv, int causal, int cus, int* out) {
+  if (!out) return MM1_E_NULL;
+  if (const int rc = check_shape(B, S, H, Hkv, mm1::HD)) return rc;
+  if (cus < 1) return MM1_E_SHAPE;
+  const mm1::DkdvPlan& plan = mm1::dkdv_plan_for(B, S, H, Hkv, causal != 0, cus);
+  out[0] = plan.L;
+  out[1] = plan.C;
+  out[2] = plan.split_keys;
+  out[3] = plan.n_items;
+  out[4] = plan.order.n;
+  return MM1_OK;
 }
 
 int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,

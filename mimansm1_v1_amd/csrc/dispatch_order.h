@@ -68,4 +68,46 @@ const DispatchOrder& dispatch_order(const GridShape& g, bool causal);
 // Same for a given CU count (the host-side model; no device needed).
 const DispatchOrder& dispatch_order_for(const GridShape& g, bool causal, int cus);
 
+// ---------------------------------------------------------------------------
+// Grouped dK/dV grid.  A workgroup owns one 128-key tile of one (batch, KV
+// head) and walks the 32-query tiles of all G query heads of the group
+// (position-major: position tiles from the sequence end down, the G heads of
+// each in turn), so K and V are loaded once per group and the group sum
+// happens in registers.  Key tile kt has
+// len(kt) = G * n_qt(kt) query tiles; the plan splits it into
+// nc(kt) = min(C, ceil(len / L)) interleaved chunks (chunk c walks tiles c,
+// c + nc, c + 2*nc, ... of the position-major walk, so all chunks start at
+// the sequence end and stream the same rows together), so that the long key
+// tiles of a causal grid do not set the finish time.  A key tile with one chunk writes bf16
+// dK/dV directly; the chunks of a split key tile write fp32 partials to
+// workspace slot c, summed (in slot order) by the reduction.
+//
+// Default item numbering: j = (kt * C + c) * (B * Hkv) + (b * Hkv + g), key
+// tiles ascending (longest first when causal); items with c >= nc(kt) are
+// empty.
+
+// Query tiles of 32 rows that key tile kt meets in one head.
+__host__ __device__ inline int dkdv_n_qt(int S, int kt, bool causal) {
+  const int q_begin = causal ? 128 * kt : 0;
+  return (S - q_begin + 31) / 32;
+}
+
+// Chunks of a key tile with `len` query tiles.
+__host__ __device__ inline int dkdv_chunks(int len, int L, int C) {
+  const int n = (len + L - 1) / L;
+  return n < 1 ? 1 : (n > C ? C : n);
+}
+
+struct DkdvPlan {
+  int L;            // target query tiles per chunk
+  int C;            // chunks per key tile at most (<= G: the workspace holds G slots)
+  int split_keys;   // keys [0, split_keys) of each batch lie in split key tiles
+  int n_items;      // items in the default numbering (n_kt * C * B * Hkv)
+  DispatchOrder order;   // n == 0: default order, n_items launch slots
+};
+
+// Cached plan for the current device's CU count / for a given CU count.
+const DkdvPlan& dkdv_plan(int B, int S, int H, int Hkv, bool causal);
+const DkdvPlan& dkdv_plan_for(int B, int S, int H, int Hkv, bool causal, int cus);
+
 }  // namespace mm1

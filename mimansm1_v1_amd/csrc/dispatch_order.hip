@@ -147,25 +147,37 @@ std::vector<int> snake_stream(const std::vector<int>& cost, int slots_per_se, bo
   return stream;
 }
 
-void build(const GridShape& g, int cus, DispatchOrder& out) {
+// Builds the table for items with the given modelled costs (-1: an empty
+// item, which runs in no slot of a table), `slots_per_se` workgroup slots per
+// shader engine.  Per XCD it keeps the best-rated of the default order and
+// the two snake streams.  Returns the modelled span of the order kept
+// (out.n == 0: the default order, whose slots include the empty items).
+long build_from_costs(const std::vector<int>& cost_in, int slots_per_se, DispatchOrder& out) {
   out.n = 0;
-  const std::vector<int> cost = item_costs(g);
-  const int n = (int)cost.size();
-  if (n == 0) return;
-  const int slots_per_se = std::max(1, cus / (8 * kSe)) * std::max(1, g.wg_per_cu);
+  const int n = (int)cost_in.size();
+  if (n == 0) return 0;
   std::vector<std::vector<int>> streams(8);
   size_t rounds = 0;
   bool any_change = false;
+  long span_default = 0, span_best = 0;
   for (int x = 0; x < 8; ++x) {
-    std::vector<int> mine, c;   // this XCD's items (default numbering) and their costs
+    // this XCD's items (default numbering) and their costs; the default
+    // stream also keeps its empty slots
+    std::vector<int> mine, c, dflt;
     for (int j = x; j < n; j += 8) {
-      mine.push_back(j);
-      c.push_back(cost[j]);
+      if (cost_in[j] >= 0) {
+        dflt.push_back((int)mine.size());
+        mine.push_back(j);
+        c.push_back(cost_in[j]);
+      } else {
+        dflt.push_back(-1);
+      }
     }
-    std::vector<int> best(mine.size());
-    for (size_t i = 0; i < mine.size(); ++i) best[i] = (int)i;   // the default order
+    std::vector<int> best = dflt;
     long best_span = stream_span(best, c, slots_per_se);
+    span_default = std::max(span_default, best_span);
     for (bool pack : {false, true}) {
+      if (c.empty()) break;
       std::vector<int> cand = snake_stream(c, slots_per_se, pack);
       const long span = stream_span(cand, c, slots_per_se);
       if (span < best_span) {
@@ -174,15 +186,80 @@ void build(const GridShape& g, int cus, DispatchOrder& out) {
         any_change = true;
       }
     }
+    span_best = std::max(span_best, best_span);
     for (int i : best) streams[x].push_back(i < 0 ? -1 : mine[i]);
     rounds = std::max(rounds, streams[x].size());
   }
-  if (!any_change || 8 * rounds > (size_t)kOrderCap) return;
+  if (!any_change || 8 * rounds > (size_t)kOrderCap || n > (int)kNoItem) return span_default;
   for (int i = 0; i < kOrderCap; ++i) out.item[i] = kNoItem;
   for (int x = 0; x < 8; ++x)
     for (size_t r = 0; r < streams[x].size(); ++r)
       if (streams[x][r] >= 0) out.item[8 * r + x] = (uint16_t)streams[x][r];
   out.n = (int)(8 * rounds);
+  return span_best;
+}
+
+void build(const GridShape& g, int cus, DispatchOrder& out) {
+  const int slots_per_se = std::max(1, cus / (8 * kSe)) * std::max(1, g.wg_per_cu);
+  build_from_costs(item_costs(g), slots_per_se, out);
+}
+
+// Grouped dK/dV: modelled cost of a chunk, in 32-query tiles: its tiles, the
+// fixed cost of a workgroup (K/V loads, ring fill, pipeline drain, stores)
+// and, for a chunk of a split key tile, its fp32 partial stores and their
+// share of the reduction.
+constexpr int kDkdvFixed = 6;
+constexpr int kDkdvSplit = 2;
+
+std::vector<int> dkdv_costs(int B, int S, int G, int Hkv, bool causal, int L, int C) {
+  const int n_kt = (S + 127) / 128, nbg = B * Hkv;
+  std::vector<int> cost((size_t)n_kt * C * nbg, -1);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int len = G * dkdv_n_qt(S, kt, causal);
+    const int nc = dkdv_chunks(len, L, C);
+    for (int c = 0; c < nc; ++c) {
+      const int size = (len - c + nc - 1) / nc;
+      const int cc = size + kDkdvFixed + (nc > 1 ? kDkdvSplit : 0);
+      for (int bg = 0; bg < nbg; ++bg) cost[((size_t)kt * C + c) * nbg + bg] = cc;
+    }
+  }
+  return cost;
+}
+
+// Chunk length: the candidate (fractions of the per-CU share of the work,
+// and no split at all) whose order the dispatch model rates fastest; on a
+// tie the one with fewer split key tiles.
+void build_dkdv(int B, int S, int H, int Hkv, bool causal, int cus, int forced_L, DkdvPlan& plan) {
+  const int G = H / Hkv, n_kt = (S + 127) / 128, nbg = B * Hkv;
+  const int C = G;
+  long total = 0;
+  int longest = 0;
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int len = G * dkdv_n_qt(S, kt, causal);
+    total += (long)len * nbg;
+    longest = std::max(longest, len);
+  }
+  const long share = std::max<long>(1, (total + cus - 1) / std::max(1, cus));
+  const int slots_per_se = std::max(1, cus / (8 * kSe));
+  std::vector<long> cands = {share / 3, share / 2, (2 * share) / 3, share, (4 * share) / 3, longest};
+  if (forced_L > 0) cands = {forced_L};
+  long best_span = -1;
+  plan.C = C;
+  for (long cand : cands) {
+    const int L = (int)std::min<long>(std::max<long>(1, cand), longest);
+    auto ord = std::make_unique<DispatchOrder>();
+    const long span = build_from_costs(dkdv_costs(B, S, G, Hkv, causal, L, C), slots_per_se, *ord);
+    if (best_span < 0 || span < best_span || (span == best_span && L > plan.L)) {
+      best_span = span;
+      plan.L = L;
+      plan.order = *ord;
+    }
+  }
+  plan.n_items = n_kt * C * nbg;
+  plan.split_keys = 0;
+  for (int kt = 0; kt < n_kt; ++kt)
+    if (dkdv_chunks(G * dkdv_n_qt(S, kt, causal), plan.L, C) > 1)
+      plan.split_keys = std::min(S, 128 * (kt + 1));
 }
 
 bool order_enabled() {
@@ -239,6 +316,31 @@ const DispatchOrder& dispatch_order_for(const GridShape& g, bool causal, int cus
 const DispatchOrder& dispatch_order(const GridShape& g, bool causal) {
   if (!causal || !order_enabled()) return default_order();
   return dispatch_order_for(g, causal, device_cus());
+}
+
+const DkdvPlan& dkdv_plan_for(int B, int S, int H, int Hkv, bool causal, int cus) {
+  const bool ordered = order_enabled();
+  // MM1_DKDV_CHUNK=<tiles>: a fixed chunk length instead of the modelled
+  // choice (tuning experiments; read per call)
+  const char* e = getenv("MM1_DKDV_CHUNK");
+  const int forced_L = e ? std::max(0, atoi(e)) : 0;
+  using Key = std::tuple<int, int, int, int, bool, int, bool, int>;
+  const Key key{B, S, H, Hkv, causal, cus, ordered, forced_L};
+  static std::mutex mu;
+  static std::map<Key, std::unique_ptr<DkdvPlan>> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it == cache.end()) {
+    auto plan = std::make_unique<DkdvPlan>();
+    build_dkdv(B, S, H, Hkv, causal, std::max(1, cus), forced_L, *plan);
+    if (!ordered) plan->order.n = 0;
+    it = cache.emplace(key, std::move(plan)).first;
+  }
+  return *it->second;
+}
+
+const DkdvPlan& dkdv_plan(int B, int S, int H, int Hkv, bool causal) {
+  return dkdv_plan_for(B, S, H, Hkv, causal, device_cus());
 }
 
 }  // namespace mm1

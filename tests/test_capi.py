@@ -107,9 +107,9 @@ def test_bwd_argument_errors(lib):
                                       None, 0, 2, 100, 10, 2, 128, 1, 0.1, None) == -4
     assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
                                       FAKE + 4, need, 2, 100, 10, 2, 128, 1, 0.1, None) == -6
-    assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 10, 2, 128, None) == -4
+    assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 10, 2, 128, 1, None) == -4
     # nothing to reduce without groups: success without a device call
-    assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 4, 4, 128, None) == 0
+    assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 4, 4, 128, 1, None) == 0
     assert lib.mm1_attn_delta(FAKE, None, FAKE, 1, 64, 10, 128, None) == -1
     assert lib.mm1_attn_delta(FAKE, FAKE, FAKE, 1, 64, 10, 64, None) == -3
 
@@ -346,3 +346,79 @@ def test_dispatch_order_defaults_and_errors(lib, monkeypatch):
     assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 0, None, 0) == E_SHAPE
     assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 256, None, 4) == E_NULL
     assert E_HEAD != E_SHAPE
+
+
+# ---------------------------------------------------------------------------
+# Grouped dK/dV tiling: work plan and dispatch table (host-side, no device).
+
+GROUPED = [(2, 8192, 10, 2, 1), (8, 2048, 10, 2, 1), (4, 4096, 10, 2, 1), (2, 7777, 10, 2, 1),
+           (3, 1000, 10, 2, 1), (2, 2048, 10, 2, 0), (1, 4096, 8, 1, 1), (1, 333, 6, 3, 0),
+           (1, 16384, 10, 2, 1), (1, 64, 10, 2, 1)]
+
+
+def _grouped_items(B, S, H, Hkv, causal, L, C):
+    """Default numbering of the grouped dK/dV grid, j = (kt*C + c)*B*Hkv + bg,
+    with each item's query tiles in the position-major walk of its key tile
+    (None for an empty item), as the header states the plan."""
+    G, nkt, nbg = H // Hkv, (S + 127) // 128, B * Hkv
+    out = []
+    for kt in range(nkt):
+        ln = G * ((S - (128 * kt if causal else 0) + 31) // 32)
+        nc = min(C, max(1, -(-ln // L)))
+        for c in range(C):
+            for bg in range(nbg):
+                out.append((kt, bg, ln, nc, list(range(c, ln, nc)) if c < nc else None))
+    return out
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,causal", GROUPED,
+                         ids=[f"B{b}S{s}G{h // kv}{'c' if c else 'f'}" for b, s, h, kv, c in GROUPED])
+def test_grouped_dkdv_plan(lib, B, S, H, Hkv, causal):
+    """The plan's chunks cover every (position tile, head) of every key tile
+    exactly once, split only the key tiles below split_keys, fit the G
+    workspace slots; its table runs every non-empty item once on the XCD of
+    its default slot, with a modelled span no worse than the default order."""
+    import ctypes
+    plan = (ctypes.c_int * 5)()
+    assert lib.mm1_attn_dkdv_plan(B, S, H, Hkv, causal, 256, plan) == 0
+    L, C, split_keys, n_items, n_table = list(plan)
+    G, nkt = H // Hkv, (S + 127) // 128
+    assert C == G and L >= 1 and n_items == nkt * C * B * Hkv
+    items = _grouped_items(B, S, H, Hkv, causal, L, C)
+    by_tile = {}
+    for kt, bg, ln, nc, tiles in items:
+        assert nc <= C
+        assert (nc > 1) == (128 * kt < split_keys), (kt, nc, split_keys)
+        if tiles is not None:
+            by_tile.setdefault((kt, bg), []).extend(tiles)
+    for (kt, bg), tiles in by_tile.items():
+        ln = items[(kt * C) * B * Hkv + bg][2]
+        assert sorted(tiles) == list(range(ln))
+    assert split_keys % 128 == 0 or split_keys == S
+    n, order = _order(lib, 1, 2, B, S, H=H, Hkv=Hkv, causal=causal)
+    assert n == n_table
+    live = [j for j, it in enumerate(items) if it[4] is not None]
+    if n == 0:
+        return
+    assert sorted(i for i in order if i != 0xFFFF) == live
+    assert all(i % 8 == b % 8 for b, i in enumerate(order) if i != 0xFFFF)
+    costs = [len(it[4]) if it[4] is not None else 0 for it in items]
+    default = [j if items[j][4] is not None else 0xFFFF for j in range(len(items))]
+    assert _makespan(order, costs, 8) <= _makespan(default, costs, 8) * 1.01 + 8
+
+
+def test_grouped_dkdv_plan_errors_and_override(lib, monkeypatch):
+    import ctypes
+    plan = (ctypes.c_int * 5)()
+    assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, None) == -1
+    assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 3, 1, 256, plan) == -2
+    assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 0, plan) == -2
+    # the dK/dV tiling index is checked by the dispatch-order query
+    assert lib.mm1_attn_dispatch_order(1, 3, 2, 8192, 10, 2, 1, 256, None, 0) == -7
+    assert lib.mm1_attn_dispatch_order(1, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0
+    monkeypatch.setenv("MM1_DKDV_CHUNK", "300")
+    assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, plan) == 0
+    assert plan[0] == 300
+    monkeypatch.setenv("MM1_DISPATCH_ORDER", "0")
+    assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, plan) == 0
+    assert plan[4] == 0

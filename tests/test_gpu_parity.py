@@ -290,6 +290,79 @@ def test_large_ragged_vs_gpu_oracle(hip_device, B, S, H, Hkv):
     assert_bf16_close("dV", dv, wv, log, emulated=ev)
 
 
+def _capi_run(lib, q, k, v, do, H, Hkv, causal, dkdv_tiles, dq_tiles, device):
+    """Forward + backward through the C ABI with explicit tilings (GPU tensors)."""
+    B, S = q.shape[0], q.shape[1]
+    scale = 128 ** -0.5
+    sp = torch.cuda.current_stream(device).cuda_stream
+    p = lambda t: t.data_ptr()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, dtype=torch.float32, device=device)
+    delta = torch.empty_like(lse)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
+    ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=device)
+    args = (B, S, H, Hkv, 128, int(causal), scale)
+    assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), *args, sp) == 0
+    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+    assert lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk), p(dv),
+                                  p(ws), nws, *args, dkdv_tiles, dq_tiles, sp) == 0
+    torch.cuda.synchronize()
+    return o, lse, dq, dk, dv
+
+
+GROUPED = [(8, 2048, 10, 2, True), (2, 8192, 10, 2, True), (2, 7777, 10, 2, True),
+           (3, 1000, 10, 2, True), (2, 2048, 10, 2, False), (1, 4096, 8, 1, True)]
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,causal", GROUPED,
+                         ids=[f"B{b}S{s}G{h // kv}{'c' if c else 'f'}" for b, s, h, kv, c in GROUPED])
+def test_grouped_dkdv_vs_gpu_oracle(hip_device, B, S, H, Hkv, causal):
+    """The grouped dK/dV tiling (one workgroup walks all G heads of a KV head
+    for its key tile; long key tiles split into chunks whose fp32 partials the
+    dQ launch sums) at sizes where its plan splits key tiles and launches a
+    dispatch table: dK/dV against the chunked closed form on the GPU, and the
+    staged calls bitwise equal to the combined one."""
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    plan = (ctypes.c_int * 5)()
+    assert lib.mm1_attn_dkdv_plan(B, S, H, Hkv, int(causal), 256, plan) == 0
+    log(f"[case] grouped dkdv B={B} S={S} H={H} Hkv={Hkv} causal={causal} plan {list(plan)}")
+    G = H // Hkv
+    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S + B))
+    o, lse, dq, dk, dv = _capi_run(lib, q, k, v, do, H, Hkv, causal, 2, 1, hip_device)
+    wq, wk, wv = R.grads_analytic(q, k, v, do, causal, G)
+    eq, ek, ev = R.grads_analytic(q, k, v, do, causal, G, bf16_products=True, o=o)
+    assert_bf16_close("dQ", dq.cpu(), wq.cpu(), log, emulated=eq.cpu())
+    assert_bf16_close("dK", dk.cpu(), wk.cpu(), log, emulated=ek.cpu())
+    assert_bf16_close("dV", dv.cpu(), wv.cpu(), log, emulated=ev.cpu())
+    del wq, wk, wv, eq, ek, ev
+    # staged: dK/dV, then the separate reduction, then dQ
+    sp = torch.cuda.current_stream(hip_device).cuda_stream
+    p = lambda t: t.data_ptr()
+    nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
+    ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=hip_device)
+    delta = torch.empty_like(lse)
+    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+    sk, sv = torch.empty_like(k), torch.empty_like(v)
+    args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5, sp)
+    os_env = __import__("os").environ
+    old = os_env.get("MM1_DKDV_VARIANT")
+    os_env["MM1_DKDV_VARIANT"] = "2"
+    try:
+        assert lib.mm1_attn_bwd_dkdv(p(q), p(k), p(v), p(do), p(lse), p(delta), p(sk), p(sv),
+                                     p(ws), nws, *args) == 0
+        assert lib.mm1_attn_bwd_dkdv_reduce(p(ws), nws, p(sk), p(sv), B, S, H, Hkv, 128,
+                                            int(causal), sp) == 0
+    finally:
+        if old is None:
+            del os_env["MM1_DKDV_VARIANT"]
+        else:
+            os_env["MM1_DKDV_VARIANT"] = old
+    torch.cuda.synchronize()
+    assert torch.equal(sk, dk) and torch.equal(sv, dv)
+
+
 def test_backward_deterministic(hip_device):
     log("[case] determinism B2 S1024")
     q, k, v, do = R.make_inputs(2, 1024, 10, 2, 128, seed=5)
@@ -330,7 +403,7 @@ def test_backward_stages_match_combined(hip_device, shape):
         else:
             assert lib.mm1_attn_bwd_dkdv(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dk), p(dv),
                                          p(ws), nws, *args) == 0
-            assert lib.mm1_attn_bwd_dkdv_reduce(p(ws), nws, p(dk), p(dv), B, S, H, Hkv, 128, sp) == 0
+            assert lib.mm1_attn_bwd_dkdv_reduce(p(ws), nws, p(dk), p(dv), B, S, H, Hkv, 128, int(causal), sp) == 0
             assert lib.mm1_attn_bwd_dq(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), *args) == 0
         torch.cuda.synchronize()
         outs.append((dq.cpu(), dk.cpu(), dv.cpu()))
