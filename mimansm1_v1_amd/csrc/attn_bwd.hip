@@ -844,10 +844,22 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
         f32x16 sv = zero16(), dp = zero16();
+        // K / V fragments read one k-step ahead of their products
+        bf16x8 ka[2], va[2];
+        ka[0] = rows_a(kl, lb, jb, 0);
+        va[0] = rows_a(vl, lb, jb, 0);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-          sv = mfma32(rows_a(kl, lb, jb, ks), qreg[ks], sv);
-          dp = mfma32(rows_a(vl, lb, jb, ks), doreg[ks], dp);
+          if (ks + 1 < 8) {
+            ka[(ks + 1) & 1] = rows_a(kl, lb, jb, ks + 1);
+            va[(ks + 1) & 1] = rows_a(vl, lb, jb, ks + 1);
+          }
+          // keep the reads ahead: the scheduler would otherwise sink them
+          // to their products and expose the LDS latency on every pair
+          __builtin_amdgcn_sched_barrier(0);
+          sv = mfma32(ka[ks & 1], qreg[ks], sv);
+          dp = mfma32(va[ks & 1], doreg[ks], dp);
+          __builtin_amdgcn_sched_barrier(0);
         }
         // dS^T = P^T (dP^T - Delta), masked only in the tiles that need it,
         // as separate straight-line code

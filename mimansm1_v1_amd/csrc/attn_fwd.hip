@@ -114,11 +114,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
       f32x16 sacc[2];
       sacc[0] = zero16();
       sacc[1] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) sacc[jb] = mfma32(rows_a(kl, lb, jb, ks), qreg[ks], sacc[jb]);
-      }
+      rows_chain2(kl, lb, qreg, sacc);
       const bool need_mask = CAUSAL ? (k0 + BN - 1 > pw_lo) : (k0 + BN > S);
       if (need_mask) {
 #pragma unroll
@@ -305,11 +301,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
     f32x16 sacc[2];
     sacc[0] = zero16();
     sacc[1] = zero16();
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) sacc[jb] = mfma32(rows_a(kl, lb, jb, ks), qreg[ks], sacc[jb]);
-    }
+    rows_chain2(kl, lb, qreg, sacc);
     if (CAUSAL ? (k0 + BN - 1 > pw_lo) : (k0 + BN > S)) {
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {

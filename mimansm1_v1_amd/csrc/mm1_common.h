@@ -251,6 +251,29 @@ __device__ __forceinline__ bf16x8 rows_a(const char* tile, const LdsBases& lb, i
   return *reinterpret_cast<const bf16x8*>(tile + blk * 8192 + (lb.row ^ (32 * ks)));
 }
 
+// acc[jb] += A B over the 8 k-steps for the two 32-row blocks jb = 0, 1 of a
+// row-major LDS tile (A = rows_a, B in registers), the A fragments read one
+// k-step ahead of their products.  The scheduling barriers keep them there:
+// the compiler would otherwise sink each read to its product, so every
+// product pair would wait for the full LDS latency.
+__device__ __forceinline__ void rows_chain2(const char* tile, const LdsBases& lb, const bf16x8 (&b)[8],
+                                            f32x16 (&acc)[2]) {
+  bf16x8 fa[2][2];
+  fa[0][0] = rows_a(tile, lb, 0, 0);
+  fa[0][1] = rows_a(tile, lb, 1, 0);
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    if (ks + 1 < 8) {
+      fa[(ks + 1) & 1][0] = rows_a(tile, lb, 0, ks + 1);
+      fa[(ks + 1) & 1][1] = rows_a(tile, lb, 1, ks + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    acc[0] = mfma32(fa[ks & 1][0], b[ks], acc[0]);
+    acc[1] = mfma32(fa[ks & 1][1], b[ks], acc[1]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 __device__ __forceinline__ bf16x8 tr_a(const char* tile, const LdsBases& lb, int blk, int ks) {
   bf16x8 out;
 #pragma unroll
