@@ -23,9 +23,10 @@
 // kept for non-causal grids (equal items), tilings with two workgroups per
 // CU (the two share the CU's throughput, which this model does not capture;
 // the packed order measured slower for them), shapes with more items than
-// the table holds, and shapes where the model finds no gain.  The dK/dV grid
-// is not reordered: its items are closer in size, and the model's gain there
-// (about 1%) did not show in measurement.
+// the table holds, and shapes where the model finds no gain.  The per-head
+// dK/dV grid is not reordered: its items are closer in size, and the model's
+// gain there (about 1%) did not show in measurement.  The grouped dK/dV grid
+// (below) is: its chunks run about two per CU.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
