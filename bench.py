@@ -72,8 +72,8 @@ def parse(argv=None):
 
 
 # Kernel launched by each tiling index of a stage (mm1_attn_tile_desc order).
-KERNEL_NAMES = {"fwd": ("attn_fwd_kernel", "attn_fwd_kernel", "attn_fwd_pp_kernel"),
-                "dkdv": ("attn_dkdv_pipe_kernel", "attn_dkdv_kernel", "attn_dkdv_pipe_kernel"),
+KERNEL_NAMES = {"fwd": ("attn_fwd_pp_kernel", "attn_fwd_kernel", "attn_fwd_kernel"),
+                "dkdv": ("attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel", "attn_dkdv_kernel"),
                 "dq": ("attn_dq_kernel", "attn_dq_kernel")}
 TILE_ENV = {"fwd": "MM1_FWD_VARIANT", "dkdv": "MM1_DKDV_VARIANT", "dq": "MM1_DQ_VARIANT"}
 USER_TILE_ENV = {k: os.environ[v] for k, v in TILE_ENV.items() if v in os.environ}

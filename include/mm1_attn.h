@@ -80,9 +80,9 @@ int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
  * mm1_attn_bwd_dkdv then mm1_attn_bwd_dq_reduce; mm1_attn_bwd_dkdv_reduce
  * followed by mm1_attn_bwd_dq is the same result in two launches.
  *  - mm1_attn_bwd_dkdv: dK/dV.  With H == Hkv it writes bf16 dk, dv directly.
- *    Otherwise, with the per-head tilings (0, 1) it writes the per-query-head
+ *    Otherwise, with the per-head tilings (1, 2) it writes the per-query-head
  *    fp32 partial sums into `workspace` ([2][G][B][S][Hkv][D], G = H / Hkv)
- *    and leaves dk/dv untouched; with the grouped tiling (2) it writes bf16
+ *    and leaves dk/dv untouched; with the grouped tiling (0) it writes bf16
  *    dk, dv directly for the key tiles one workgroup covers and fp32 partials
  *    (one slot per chunk, see mm1_attn_dkdv_plan) for the others.
  *  - mm1_attn_bwd_dkdv_reduce: sums the partials of each KV head and writes
@@ -152,7 +152,7 @@ int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* 
  * blocks to the 4 SE lanes, packs each lane into its CUs in bins of equal
  * modelled work and lists the blocks in the order the CUs ask for them.
  * This call returns the table a launch of grid `kind` (MM1_TILES_FWD,
- * MM1_TILES_DQ, or MM1_TILES_DKDV with the grouped tiling 2) with tiling
+ * MM1_TILES_DQ, or MM1_TILES_DKDV with the grouped tiling 0) with tiling
  * `tiles` builds for a device with `cus` compute units: entry b is the work
  * item of launch slot b in the default numbering (0xFFFF for a slot without
  * one).  Writes min(n, cap) entries and returns n, the launch's grid size; 0
@@ -164,7 +164,7 @@ int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* 
 int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, int causal, int cus,
                             unsigned short* out, int cap);
 
-/* Work plan of the grouped dK/dV tiling (MM1_TILES_DKDV tiling 2; diagnostic,
+/* Work plan of the grouped dK/dV tiling (MM1_TILES_DKDV tiling 0; diagnostic,
  * no counterpart in the reference).  A workgroup of that launch owns one
  * 128-key tile of one (batch, KV head) and walks the 32-query tiles of all
  * G = H / Hkv query heads of the group, so K and V are read once per group

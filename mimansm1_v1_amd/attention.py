@@ -103,9 +103,9 @@ def tile_index(kind, config):
 AUTOTUNE = True
 # Index 0 of each kernel (the library's defaults), spelled out so that the
 # module imports without the library; the CPU tests check they agree.
-FWD_TILES = dict(block_M=128, block_N=64, waves=4, stages=2, schedule="ring")
+FWD_TILES = dict(block_M=256, block_N=64, waves=8, stages=2, schedule="pingpong")
 BWD_TILES = dict(dkdv_block_M=128, dkdv_block_N=32, dkdv_waves=8, dkdv_stages=7,
-                 dkdv_schedule="pipelined",
+                 dkdv_schedule="group",
                  dq_block_M=128, dq_block_N=64, dq_waves=4, dq_stages=2, dq_schedule="ring")
 
 

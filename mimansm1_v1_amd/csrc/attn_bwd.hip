@@ -950,7 +950,7 @@ TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, 
   red.ws_dv = red.ws_dk + (long)G * red.n;
   red.dk = static_cast<__bf16*>(dk);
   red.dv = static_cast<__bf16*>(dv);
-  if (dkdv_variant == 2) {
+  if (dkdv_variant == 0) {
     const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
     red.chunk_tiles = plan.L;
     red.max_chunks = plan.C;
@@ -960,11 +960,11 @@ TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, 
   return red;
 }
 
-// variant: 0 = attn_dkdv_pipe_kernel (7-slot ring of 32-query tiles, one
+// variant: 0 = attn_dkdv_pipe_kernel over the whole GQA group per key tile
+//              (chunked by dkdv_plan),
+//          1 = attn_dkdv_pipe_kernel (7-slot ring of 32-query tiles, one
 //              workgroup per (key tile, query head)),
-//          1 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries),
-//          2 = attn_dkdv_pipe_kernel over the whole GQA group per key tile
-//              (chunked by dkdv_plan).
+//          2 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries).
 hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
                            const float* lse2, const float* delta, void* dk, void* dv,
                            void* workspace, int B, int S, int H, int Hkv, bool causal,
@@ -983,7 +983,7 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
   const int n_ktiles = (S + 127) / 128;
   const KeyTileOrder order = key_tile_order(B * H);
   const bool ragged = S % 32 != 0;
-  if (variant == 2) {
+  if (variant == 0) {
     const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
     const dim3 grid(plan.order.n ? plan.order.n : plan.n_items);
 #define MM1_DKDV_GROUP(CS, RG)                                                                  \
@@ -1001,7 +1001,7 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
     return hipGetLastError();
   }
   const dim3 grid(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
-  if (variant == 1) {
+  if (variant == 2) {
 #define MM1_DKDV_PAIRED(KERNEL)                                                               \
   hipLaunchKernelGGL(KERNEL, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta, ws_dk, \
                      ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, order)
@@ -1071,7 +1071,7 @@ hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void
   auto dqp = static_cast<__bf16*>(dq);
   // with n_red = 1 << 30 every workgroup of the grid takes a slice
   const TailReduce red = make_reduce(workspace, dk, dv, B, S, H, Hkv, causal, dkdv_variant);
-  const DispatchOrder& ord = dispatch_order(row_block_grid(variant, B, S, H, Hkv), causal);
+  const DispatchOrder& ord = dispatch_order(dq_grid(variant, B, S, H, Hkv), causal);
   if (variant == 1)
     launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
   else

@@ -67,14 +67,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // and the streamed block: query rows x key rows for the forward and dQ, key
 // rows x query rows for dK/dV.
 const char* const kFwdTiles[] = {
+    "block_M=256 block_N=64 waves=8 stages=2 schedule=pingpong",
     "block_M=128 block_N=64 waves=4 stages=2 schedule=ring",
     "block_M=256 block_N=64 waves=8 stages=3 schedule=ring",
-    "block_M=256 block_N=64 waves=8 stages=2 schedule=pingpong",
 };
 const char* const kDkdvTiles[] = {
+    "block_M=128 block_N=32 waves=8 stages=7 schedule=group",
     "block_M=128 block_N=32 waves=8 stages=7 schedule=pipelined",
     "block_M=128 block_N=64 waves=8 stages=3 schedule=paired",
-    "block_M=128 block_N=32 waves=8 stages=7 schedule=group",
 };
 const char* const kDqTiles[] = {
     "block_M=128 block_N=64 waves=4 stages=2 schedule=ring",
@@ -272,11 +272,11 @@ int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, i
   if (const int rc = check_shape(B, S, H, Hkv, mm1::HD)) return rc;
   if (cus < 1 || cap < 0) return MM1_E_SHAPE;
   if (cap > 0 && !out) return MM1_E_NULL;
-  if (kind == MM1_TILES_DKDV && variant != 2) return 0;   // per-head grids: default order
+  if (kind == MM1_TILES_DKDV && variant != 0) return 0;   // per-head grids: default order
   const mm1::DispatchOrder& ord =
-      kind == MM1_TILES_DKDV
-          ? mm1::dkdv_plan_for(B, S, H, Hkv, causal != 0, cus).order
-          : mm1::dispatch_order_for(mm1::row_block_grid(variant, B, S, H, Hkv), causal != 0, cus);
+      kind == MM1_TILES_DKDV ? mm1::dkdv_plan_for(B, S, H, Hkv, causal != 0, cus).order
+      : kind == MM1_TILES_DQ ? mm1::dispatch_order_for(mm1::dq_grid(variant, B, S, H, Hkv), causal != 0, cus)
+                             : mm1::dispatch_order_for(mm1::row_block_grid(variant, B, S, H, Hkv), causal != 0, cus);
   for (int i = 0; i < ord.n && i < cap; ++i) out[i] = ord.item[i];
   return ord.n;
 }

@@ -423,9 +423,9 @@ static void launch_fwd_t(const __bf16* q, const __bf16* k, const __bf16* v, __bf
     hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, false>), grid, block, 0, stream, q, k, v, o, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
 }
 
-// variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
-//          1 = 8 waves x 3-stage ring (one workgroup per CU),
-//          2 = attn_fwd_pp_kernel (8 waves, two groups half a tile apart).
+// variant: 0 = attn_fwd_pp_kernel (8 waves, two groups half a tile apart),
+//          1 = 4 waves x 2-stage ring (two workgroups per CU),
+//          2 = 8 waves x 3-stage ring (one workgroup per CU).
 hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
                       int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                       hipStream_t stream) {
@@ -435,7 +435,7 @@ hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, floa
   auto vp = static_cast<const __bf16*>(v);
   auto op = static_cast<__bf16*>(o);
   const DispatchOrder& ord = dispatch_order(row_block_grid(variant, B, S, H, Hkv), causal);
-  if (variant == 2) {
+  if (variant == 0) {
     const int G = H / Hkv;
     const int n_tiles = (G * S + 255) / 256;
     dim3 grid(ord.n ? ord.n : n_tiles * B * Hkv), block(512);
@@ -443,7 +443,7 @@ hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, floa
       hipLaunchKernelGGL(attn_fwd_pp_kernel<true>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
     else
       hipLaunchKernelGGL(attn_fwd_pp_kernel<false>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
-  } else if (variant == 1)
+  } else if (variant == 2)
     launch_fwd_t<8, 3>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
   else
     launch_fwd_t<4, 2>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, ord, stream);

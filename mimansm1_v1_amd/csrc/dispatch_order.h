@@ -57,9 +57,11 @@ struct GridShape {
   int wg_per_cu;
 };
 
-// The grid of the forward / dQ launchers for a tiling index (0 = 128 rows,
-// 2 workgroups per CU; 1, 2 = 256 rows, 1 per CU).
+// The grid of the forward launcher for a tiling index (1 = 128 rows, 2
+// workgroups per CU; 0, 2 = 256 rows, 1 per CU) and of the dQ launcher
+// (0 = 128 rows, 2 per CU; 1 = 256 rows, 1 per CU).
 GridShape row_block_grid(int variant, int B, int S, int H, int Hkv);
+GridShape dq_grid(int variant, int B, int S, int H, int Hkv);
 
 // Cached order for the current device (its CU count); a table with n == 0
 // when the default order applies (see above, or the MM1_DISPATCH_ORDER=0

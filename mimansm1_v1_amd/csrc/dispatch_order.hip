@@ -294,6 +294,10 @@ const DispatchOrder& default_order() {
 }  // namespace
 
 GridShape row_block_grid(int variant, int B, int S, int H, int Hkv) {
+  return {B, S, H, Hkv, variant == 1 ? 128 : 256, variant == 1 ? 2 : 1};
+}
+
+GridShape dq_grid(int variant, int B, int S, int H, int Hkv) {
   return {B, S, H, Hkv, variant == 0 ? 128 : 256, variant == 0 ? 2 : 1};
 }
 

@@ -262,10 +262,10 @@ def _items_and_costs(kind, tiles, B, S, H=10, Hkv=2):
     tiles (32 or 64 queries); the kernels' own index arithmetic."""
     G = H // Hkv
     if kind == 1:
-        bq = 64 if tiles == 1 else 32
+        bq = 64 if tiles == 2 else 32
         nbh, nkt = B * H, (S + 127) // 128
         return [((S - (j // nbh) * 128 + bq - 1) // bq) * (bq // 32) for j in range(nkt * nbh)]
-    bm = 128 if tiles == 0 else 256
+    bm = 128 if tiles == (1 if kind == 0 else 0) else 256
     nbg, R = B * Hkv, G * S
     nt = (R + bm - 1) // bm
     out = []
@@ -293,7 +293,9 @@ def _makespan(order, costs, slots_per_se):
     return worst
 
 
-GRIDS = [(0, 0), (0, 1), (0, 2), (1, 0), (1, 1), (2, 0), (2, 1)]
+# (kind, tiling): forward 0-2, the per-head dK/dV tilings 1-2 (the grouped
+# tiling 0 has its own plan test below), dQ 0-1
+GRIDS = [(0, 0), (0, 1), (0, 2), (1, 1), (1, 2), (2, 0), (2, 1)]
 SHAPES = [(2, 8192), (8, 2048), (4, 4096), (1, 1000), (3, 777)]
 
 
@@ -309,7 +311,7 @@ def test_dispatch_order_is_a_balanced_permutation(lib, kind, tiles, B, S):
     items = [i for i in order if i != 0xFFFF]
     assert sorted(items) == list(range(len(costs)))          # every item exactly once
     assert all(i % 8 == b % 8 for b, i in enumerate(order) if i != 0xFFFF)   # XCD kept
-    slots = 8 * (2 if (kind != 1 and tiles == 0) else 1)
+    slots = 8 * (2 if (kind == 0 and tiles == 1) or (kind == 2 and tiles == 0) else 1)
     default = list(range(len(costs)))
     new_span, old_span = _makespan(order, costs, slots), _makespan(default, costs, slots)
     bound = max(max(costs), -(-sum(c + 1 for c in costs) // (8 * 4 * slots)))
@@ -321,22 +323,22 @@ def test_dispatch_order_is_a_balanced_permutation(lib, kind, tiles, B, S):
 def test_dispatch_order_defaults_and_errors(lib, monkeypatch):
     import ctypes
     # non-causal grids (equal items) and grids beyond the table run in the default order
-    assert lib.mm1_attn_dispatch_order(0, 2, 2, 8192, 10, 2, 0, 256, None, 0) == 0
-    assert lib.mm1_attn_dispatch_order(0, 2, 16, 8192, 10, 2, 1, 256, None, 0) == 0   # 5120 blocks
-    assert lib.mm1_attn_dispatch_order(1, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0    # dK/dV
+    assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 0, 256, None, 0) == 0
+    assert lib.mm1_attn_dispatch_order(0, 0, 16, 8192, 10, 2, 1, 256, None, 0) == 0   # 5120 blocks
+    assert lib.mm1_attn_dispatch_order(1, 1, 2, 8192, 10, 2, 1, 256, None, 0) == 0    # per-head dK/dV
     monkeypatch.setenv("MM1_DISPATCH_ORDER", "0")
-    assert lib.mm1_attn_dispatch_order(0, 2, 2, 8192, 10, 2, 1, 256, None, 0) == 0
+    assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0
     monkeypatch.delenv("MM1_DISPATCH_ORDER")
-    n = lib.mm1_attn_dispatch_order(0, 2, 2, 8192, 10, 2, 1, 256, None, 0)
+    n = lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 256, None, 0)
     assert n >= 640
     buf = (ctypes.c_ushort * 8)()
-    assert lib.mm1_attn_dispatch_order(0, 2, 2, 8192, 10, 2, 1, 256, buf, 8) == n
-    _, full = _order(lib, 0, 2, 2, 8192)
+    assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 256, buf, 8) == n
+    _, full = _order(lib, 0, 0, 2, 8192)
     assert list(buf) == full[:8]
     # a device with fewer CUs gets its own table; two workgroups per CU: default order
-    _, small = _order(lib, 0, 2, 2, 8192, cus=128)
+    _, small = _order(lib, 0, 0, 2, 8192, cus=128)
     assert small != full and sorted(small) == sorted(full)
-    assert lib.mm1_attn_dispatch_order(0, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0
+    assert lib.mm1_attn_dispatch_order(0, 1, 2, 8192, 10, 2, 1, 256, None, 0) == 0
     assert lib.mm1_attn_dispatch_order(2, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0
     E_TILES, E_SHAPE, E_NULL, E_HEAD = -7, -2, -1, -3
     assert lib.mm1_attn_dispatch_order(3, 0, 2, 8192, 10, 2, 1, 256, None, 0) == E_TILES
@@ -395,7 +397,7 @@ def test_grouped_dkdv_plan(lib, B, S, H, Hkv, causal):
         ln = items[(kt * C) * B * Hkv + bg][2]
         assert sorted(tiles) == list(range(ln))
     assert split_keys % 128 == 0 or split_keys == S
-    n, order = _order(lib, 1, 2, B, S, H=H, Hkv=Hkv, causal=causal)
+    n, order = _order(lib, 1, 0, B, S, H=H, Hkv=Hkv, causal=causal)
     assert n == n_table
     live = [j for j, it in enumerate(items) if it[4] is not None]
     if n == 0:
@@ -415,7 +417,7 @@ def test_grouped_dkdv_plan_errors_and_override(lib, monkeypatch):
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 0, plan) == -2
     # the dK/dV tiling index is checked by the dispatch-order query
     assert lib.mm1_attn_dispatch_order(1, 3, 2, 8192, 10, 2, 1, 256, None, 0) == -7
-    assert lib.mm1_attn_dispatch_order(1, 0, 2, 8192, 10, 2, 1, 256, None, 0) == 0
+    assert lib.mm1_attn_dispatch_order(1, 1, 2, 8192, 10, 2, 1, 256, None, 0) == 0
     monkeypatch.setenv("MM1_DKDV_CHUNK", "300")
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, plan) == 0
     assert plan[0] == 300

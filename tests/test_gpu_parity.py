@@ -152,7 +152,7 @@ def test_env_variable_selects_tiling(hip_device, monkeypatch, env, kind, index):
 
 
 @pytest.mark.parametrize("B,S", [(8, 2048), (4, 4096)])
-@pytest.mark.parametrize("tiles", [(1, 0, 1), (2, 1, 1), (2, 0, 0)], ids=["t101", "t211", "t200"])
+@pytest.mark.parametrize("tiles", [(2, 1, 1), (0, 2, 1), (0, 0, 0)], ids=["t211", "t021", "t000"])
 def test_dispatch_order_is_bitwise_neutral(hip_device, monkeypatch, B, S, tiles):
     """The dispatch order only changes which workgroup runs which item: every
     output is bitwise the one of the default (longest-first) order, which the
@@ -272,7 +272,7 @@ def test_large_ragged_vs_gpu_oracle(hip_device, B, S, H, Hkv):
     the full configs, against the chunked closed form on the GPU."""
     from mimansm1_v1_amd import _lib
     lib = _lib.load()
-    tables = [lib.mm1_attn_dispatch_order(0, 2, B, S, H, Hkv, 1, 256, None, 0),
+    tables = [lib.mm1_attn_dispatch_order(0, 0, B, S, H, Hkv, 1, 256, None, 0),
               lib.mm1_attn_dispatch_order(2, 1, B, S, H, Hkv, 1, 256, None, 0)]
     log(f"[case] ragged B={B} S={S} H={H} Hkv={Hkv} dispatch tables {tables}")
     assert min(tables) > 0
@@ -330,7 +330,7 @@ def test_grouped_dkdv_vs_gpu_oracle(hip_device, B, S, H, Hkv, causal):
     log(f"[case] grouped dkdv B={B} S={S} H={H} Hkv={Hkv} causal={causal} plan {list(plan)}")
     G = H // Hkv
     q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S + B))
-    o, lse, dq, dk, dv = _capi_run(lib, q, k, v, do, H, Hkv, causal, 2, 1, hip_device)
+    o, lse, dq, dk, dv = _capi_run(lib, q, k, v, do, H, Hkv, causal, 0, 1, hip_device)
     wq, wk, wv = R.grads_analytic(q, k, v, do, causal, G)
     eq, ek, ev = R.grads_analytic(q, k, v, do, causal, G, bf16_products=True, o=o)
     assert_bf16_close("dQ", dq.cpu(), wq.cpu(), log, emulated=eq.cpu())
@@ -348,7 +348,7 @@ def test_grouped_dkdv_vs_gpu_oracle(hip_device, B, S, H, Hkv, causal):
     args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5, sp)
     os_env = __import__("os").environ
     old = os_env.get("MM1_DKDV_VARIANT")
-    os_env["MM1_DKDV_VARIANT"] = "2"
+    os_env["MM1_DKDV_VARIANT"] = "0"
     try:
         assert lib.mm1_attn_bwd_dkdv(p(q), p(k), p(v), p(do), p(lse), p(delta), p(sk), p(sv),
                                      p(ws), nws, *args) == 0
