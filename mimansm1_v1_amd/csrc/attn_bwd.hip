@@ -14,14 +14,19 @@
 // (sm_scale is applied to the fp32 accumulators instead of to dS.)
 //
 // The decomposition here is atomic-free and deterministic:
-//   * attn_delta_kernel   : Delta, one 16-lane group per (b, s, h) row.
-//   * attn_dkdv_pipe_kernel (default) / attn_dkdv_kernel : key-stationary,
-//     one workgroup per (128-key tile, query head).  Each wave pair keeps 32
-//     keys of K and V and their dK/dV accumulators in registers while it
-//     walks the head's query tiles, which arrive in LDS by DMA (row-major;
-//     transposed operands are read with the LDS transpose read).  With G > 1
-//     the per-head partial sums go to an fp32 workspace [G][B][S][Hkv][D] and
-//     attn_dkdv_reduce_kernel adds the G heads of each group and rounds once.
+//   * attn_delta_kernel   : Delta, one 16-lane group per two (b, s, h) rows.
+//   * attn_dkdv_pipe_kernel / attn_dkdv_kernel : key-stationary.  Each wave
+//     pair keeps 32 keys of K and V and their dK/dV accumulators in
+//     registers while it walks query tiles, which arrive in LDS by DMA
+//     (row-major; transposed operands are read with the LDS transpose read).
+//     The default (grouped) tiling gives a workgroup one 128-key tile of one
+//     KV head and walks the query tiles of all G heads of the group, so the
+//     group sum stays in registers; only the long key tiles of a causal grid
+//     are split into chunks, whose fp32 partials go to a workspace
+//     [chunk][B][S][Hkv][D].  The per-head tilings give a workgroup one
+//     (128-key tile, query head) and write a partial per head.  The partials
+//     are summed in a fixed order and rounded once (in the dQ launch's tail,
+//     or attn_dkdv_reduce_kernel).
 //   * attn_dq_kernel      : query-stationary over the packed GQA row space
 //     (as in the forward): K/V tiles in LDS serve all G heads of a group and
 //     dQ is written once in bf16 -- no fp32 scratch and no un-swizzle pass.
@@ -33,29 +38,42 @@
 namespace mm1 {
 
 // ---------------------------------------------------------------------------
-// Delta = rowsum(O * dO) in fp32.
+// Delta = rowsum(O * dO) in fp32.  A 16-lane group reads two consecutive
+// (b, s, h) rows (512 contiguous bytes of each tensor), so every lane has four
+// 16-byte loads in flight.
 __global__ __launch_bounds__(256) void attn_delta_kernel(
     const __bf16* __restrict__ o, const __bf16* __restrict__ dO, float* __restrict__ delta,
     int B, int S, int H) {
   const long nrows = (long)B * S * H;
-  const long row = ((long)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const long row0 = (((long)blockIdx.x * 256 + threadIdx.x) >> 4) * 2;
   const int c = threadIdx.x & 15;
-  if (row >= nrows) return;   // whole 16-lane groups leave together
-  const bf16x8 a = *reinterpret_cast<const bf16x8*>(o + row * HD + 8 * c);
-  const bf16x8 d = *reinterpret_cast<const bf16x8*>(dO + row * HD + 8 * c);
-  float acc = 0.f;
+  if (row0 >= nrows) return;   // whole 16-lane groups leave together
+  const long row1 = min(row0 + 1, nrows - 1);
+  const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(o + row0 * HD + 8 * c);
+  const bf16x8 d0 = *reinterpret_cast<const bf16x8*>(dO + row0 * HD + 8 * c);
+  const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(o + row1 * HD + 8 * c);
+  const bf16x8 d1 = *reinterpret_cast<const bf16x8*>(dO + row1 * HD + 8 * c);
+  float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) acc = fmaf((float)a[t], (float)d[t], acc);
-  acc += __shfl_xor(acc, 8);
-  acc += __shfl_xor(acc, 4);
-  acc += __shfl_xor(acc, 2);
-  acc += __shfl_xor(acc, 1);
+  for (int t = 0; t < 8; ++t) {
+    acc0 = fmaf((float)a0[t], (float)d0[t], acc0);
+    acc1 = fmaf((float)a1[t], (float)d1[t], acc1);
+  }
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) {
+    acc0 += __shfl_xor(acc0, m);
+    acc1 += __shfl_xor(acc1, m);
+  }
   if (c == 0) {
-    const int hh = (int)(row % H);
-    const long bs = row / H;
-    const int s = (int)(bs % S);
-    const int b = (int)(bs / S);
-    delta[((long)b * H + hh) * S + s] = acc;
+    auto put = [&](long row, float v) {
+      const int hh = (int)(row % H);
+      const long bs = row / H;
+      const int sp = (int)(bs % S);
+      const int bb = (int)(bs / S);
+      delta[((long)bb * H + hh) * S + sp] = v;
+    };
+    put(row0, acc0);
+    if (row0 + 1 < nrows) put(row0 + 1, acc1);
   }
 }
 
@@ -922,7 +940,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
 hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int S, int H,
                         hipStream_t stream) {
   const long rows = (long)B * S * H;
-  const long blocks = (rows * 16 + 255) / 256;
+  const long blocks = ((rows + 1) / 2 * 16 + 255) / 256;   // 16 lanes per pair of rows
   hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                      static_cast<const __bf16*>(o), static_cast<const __bf16*>(dO), delta, B, S, H);
   return hipGetLastError();

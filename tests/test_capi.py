@@ -355,7 +355,7 @@ def test_dispatch_order_defaults_and_errors(lib, monkeypatch):
 
 GROUPED = [(2, 8192, 10, 2, 1), (8, 2048, 10, 2, 1), (4, 4096, 10, 2, 1), (2, 7777, 10, 2, 1),
            (3, 1000, 10, 2, 1), (2, 2048, 10, 2, 0), (1, 4096, 8, 1, 1), (1, 333, 6, 3, 0),
-           (1, 16384, 10, 2, 1), (1, 64, 10, 2, 1)]
+           (1, 16384, 10, 2, 1), (1, 64, 10, 2, 1), (1, 3001, 16, 1, 1), (2, 1111, 16, 1, 0)]
 
 
 def _grouped_items(B, S, H, Hkv, causal, L, C):

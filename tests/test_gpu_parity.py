@@ -312,7 +312,8 @@ def _capi_run(lib, q, k, v, do, H, Hkv, causal, dkdv_tiles, dq_tiles, device):
 
 
 GROUPED = [(8, 2048, 10, 2, True), (2, 8192, 10, 2, True), (2, 7777, 10, 2, True),
-           (3, 1000, 10, 2, True), (2, 2048, 10, 2, False), (1, 4096, 8, 1, True)]
+           (3, 1000, 10, 2, True), (2, 2048, 10, 2, False), (1, 4096, 8, 1, True),
+           (1, 3001, 16, 1, True), (2, 1111, 16, 1, False)]
 
 
 @pytest.mark.parametrize("B,S,H,Hkv,causal", GROUPED,
