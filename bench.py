@@ -224,8 +224,9 @@ def time_sublayer(batch, seq, device, steps, warmup):
     projection, QK-norm + RoPE, causal flash attention, wo) forward + backward
     under bf16 autocast, x ~ N(0,1), weights ~ N(0, 0.02^2).  Besides the whole
     step, its parts are timed on the same tensors: the attention kernels (fwd +
-    bwd), the hipBLASLt GEMMs (QKV and wo, fwd + both backward products) and the
-    QK-norm + RoPE kernels (fwd + bwd)."""
+    bwd), the projection GEMMs (QKV and wo, fwd + both backward products, as
+    BF16Linear runs them on hipBLASLt) and the QK-norm + RoPE kernels (fwd +
+    bwd)."""
     import torch
     import torch.nn.functional as F
     from mimansm1_v1_amd import attention as A
@@ -292,9 +293,10 @@ def time_sublayer(batch, seq, device, steps, warmup):
                                            ws_bytes, batch, seq, H, Hkv, D, rot, cfg.norm_eps, sp), "qknorm bwd")
 
     def gemms():
+        # the projections as the step runs them (BF16Linear under autocast)
         with ac():
-            a = F.linear(x, w_cat)
-            b = F.linear(o, wo)
+            a = A.BF16Linear.apply(x, w_cat)
+            b = A.BF16Linear.apply(o, wo)
         torch.autograd.backward((a, b), (dqkv, dy))
         x.grad = w_cat.grad = o.grad = wo.grad = None
 
@@ -314,7 +316,8 @@ def time_sublayer(batch, seq, device, steps, warmup):
         "gemm_tflops": round(gemm_flops / (parts["gemm"] * 1e-3) / 1e12, 2),
         "flops": {"attention": attn_flops, "gemm": gemm_flops},
         "note": "bf16 autocast; attention = flash_attention fwd+bwd kernels, gemm = QKV (1280->1792) and "
-                "wo (1280->1280) fwd + dX + dW via torch (hipBLASLt), qknorm_rope = fwd+bwd kernels; "
+                "wo (1280->1280) fwd + dX + dW as the step runs them (BF16Linear: hipBLASLt GEMMs, dW over 8 "
+                "token chunks with fp32 outputs), qknorm_rope = fwd+bwd kernels; "
                 "other = casts, weight concatenation and autograd bookkeeping of the whole step",
     }
 

@@ -446,6 +446,70 @@ def apply_rope(x, cos, sin):
 _HIP_BACKENDS = ("hip", "tilelang")
 
 
+# Token chunks of the weight-gradient GEMM: dW = dY^T X sums over all B*S
+# tokens but has only N x K outputs (1792 x 1280 for wq|wk|wv), too few tiles
+# to fill 256 CUs; 8 chunks with fp32 outputs, summed in fp32, measured
+# 113-129 us against 157 us for the single bf16 GEMM at 16,384 tokens.
+PROJ_DW_CHUNKS = 8
+
+
+class BF16Linear(torch.autograd.Function):
+    """y = x W^T of the sublayer's projections under bf16 autocast, with the
+    weight gradient in the GEMM form hipBLASLt runs fastest on gfx950:
+      dX = dY W, as autograd computes it;
+      dW = sum over PROJ_DW_CHUNKS token chunks of dY_c^T X_c, each a GEMM with
+           fp32 outputs, summed in fp32 (the reference's autocast graph rounds
+           the one bf16 GEMM's dW to bf16 before its fp32 cast, AT:470-472,
+           :518; this dW is the same sum without that rounding).
+    x may be fp32 or bf16 (cast here, as autocast would); w is the fp32
+    parameter (cast here; its gradient is returned in fp32).  The forward is
+    the same F.linear on the same bf16 operands as the module's."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        xb, wb = x.to(DTYPE), w.to(DTYPE)
+        ctx.save_for_backward(xb, wb)
+        ctx.x_dtype, ctx.w_dtype = x.dtype, w.dtype
+        return F.linear(xb, wb)
+
+    @staticmethod
+    def backward(ctx, dy):
+        xb, wb = ctx.saved_tensors
+        n, k = wb.shape
+        dy2 = dy.reshape(-1, n).to(DTYPE)
+        x2 = xb.reshape(-1, k)
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            dx = (dy2 @ wb).reshape(*dy.shape[:-1], k).to(ctx.x_dtype)
+        if ctx.needs_input_grad[1]:
+            t = x2.shape[0]
+            c = PROJ_DW_CHUNKS
+            if t % c == 0 and t >= 64 * c:
+                dw = torch.bmm(dy2.reshape(c, t // c, n).transpose(1, 2), x2.reshape(c, t // c, k).contiguous(),
+                               out_dtype=torch.float32).sum(0)
+            else:
+                dw = torch.mm(dy2.t(), x2, out_dtype=torch.float32)
+            dw = dw.to(ctx.w_dtype)
+        return dx, dw
+
+
+def _autocast_bf16() -> bool:
+    return torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == DTYPE
+
+
+def _bf16_linear_applies(x) -> bool:
+    """The hip backend's projections run through BF16Linear where autocast
+    would run them in bf16 on the GPU."""
+    return x.is_cuda and _autocast_bf16()
+
+
+def _skip_attn_out_cast() -> bool:
+    """Under bf16 autocast wo casts its input back to bf16, so the reference's
+    cast of the attention output to x.dtype (AT:494) is a bf16 -> fp32 -> bf16
+    round trip, exact both ways (its gradient too): the hip backend skips it."""
+    return _autocast_bf16()
+
+
 class QKNormRope(torch.autograd.Function):
     """QK-RMSNorm + RoPE of the fused projection on the gfx950 kernels
     (mm1_qknorm_rope_fwd / _bwd): qkv [B, S, (H + 2*Hkv) * D] bf16 ->
@@ -550,7 +614,7 @@ class Attention(nn.Module):
         batch, seq_len, _ = x.shape
         cfg = self.cfg
         w = torch.cat((self.wq.weight, self.wk.weight, self.wv.weight), dim=0)
-        qkv = F.linear(x, w)
+        qkv = BF16Linear.apply(x, w) if _bf16_linear_applies(x) else F.linear(x, w)
         if qkv.dtype != DTYPE or not qkv.is_cuda or cfg.head_dim != 128:
             return None
         qn = self.q_norm.weight if cfg.qk_norm else None
@@ -568,10 +632,7 @@ class Attention(nn.Module):
         if backend in _HIP_BACKENDS:
             out = flash_attention(q.to(DTYPE).contiguous(), k.to(DTYPE).contiguous(),
                                   v.to(DTYPE).contiguous(), True, cfg.groups)
-            # Under bf16 autocast wo casts its input back to bf16, so the
-            # reference's cast to x.dtype (AT:494) is a bf16 -> fp32 -> bf16
-            # round trip, exact both ways (its gradient too): skipped there.
-            if not (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == DTYPE):
+            if not _skip_attn_out_cast():
                 out = out.to(x.dtype)
         else:
             qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))
@@ -596,7 +657,10 @@ class Attention(nn.Module):
                 raise ValueError(f"unknown backend {backend!r}")
             out = out.transpose(1, 2)
 
-        return self.wo(out.reshape(batch, seq_len, cfg.n_heads * cfg.head_dim))
+        out = out.reshape(batch, seq_len, cfg.n_heads * cfg.head_dim)
+        if backend in _HIP_BACKENDS and _bf16_linear_applies(out):
+            return BF16Linear.apply(out, self.wo.weight)
+        return self.wo(out)
 
 
 # ---------------------------------------------------------------------------

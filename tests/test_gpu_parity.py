@@ -12,6 +12,7 @@ import sys
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import reference as R
 from tests.parity import assert_bf16_close, assert_lse_close
@@ -550,7 +551,7 @@ def test_sublayer_skipped_cast_is_bitwise_neutral(hip_device, monkeypatch):
         return [y.detach().cpu(), xi.grad.cpu()] + [p.grad.cpu() for p in mod.parameters() if p.grad is not None]
 
     skipped = run()
-    monkeypatch.setattr(A.torch, "is_autocast_enabled", lambda *a: False)   # take the reference's cast
+    monkeypatch.setattr(A, "_skip_attn_out_cast", lambda: False)   # take the reference's cast
     cast = run()
     assert len(skipped) == len(cast)
     for i, (a, b) in enumerate(zip(skipped, cast)):
@@ -591,3 +592,37 @@ def test_sublayer_hip_matches_reference_backend(hip_device):
         log(f"  {name}: rel_l2 {err:.2e}")
         assert torch.isfinite(got).all(), name
         assert err < 1e-2, name
+
+
+@pytest.mark.parametrize("shape", [(2, 2048, 1280, 1792), (1, 100, 256, 384), (3, 77, 128, 128)],
+                         ids=["T4096chunks", "T100plain", "T231plain"])
+def test_bf16_linear_projection(hip_device, shape):
+    """The sublayer projections' autograd Function: forward bitwise equal to
+    autocast's F.linear; dX and dW against fp64 products of the same bf16
+    operands (dX within bf16 rounding; dW in fp32, no less accurate than the
+    bf16 dW of autograd through F.linear)."""
+    from mimansm1_v1_amd import attention as A
+    B, S, K, N = shape
+    log(f"[case] BF16Linear {shape}")
+    gen = torch.Generator().manual_seed(K + N)
+    x = torch.randn(B, S, K, generator=gen).to(hip_device)
+    w = (torch.randn(N, K, generator=gen) * 0.02).to(hip_device)
+    dy = torch.randn(B, S, N, generator=gen).to(hip_device)
+    outs = {}
+    for kind in ("fn", "autograd"):
+        xi, wi = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = A.BF16Linear.apply(xi, wi) if kind == "fn" else F.linear(xi, wi)
+        y.backward(dy.to(y.dtype))
+        torch.cuda.synchronize()
+        outs[kind] = (y.detach(), xi.grad, wi.grad)
+    assert torch.equal(outs["fn"][0], outs["autograd"][0])
+    xb, wb, dyb = (t.to(torch.bfloat16).double() for t in (x, w, dy))
+    want_dx = (dyb @ wb).float()
+    want_dw = torch.einsum("bsn,bsk->nk", dyb, xb).float()
+    rel = lambda a, b: ((a.float() - b).norm() / b.norm()).item()
+    e_dx, e_dx_ag = rel(outs["fn"][1], want_dx), rel(outs["autograd"][1], want_dx)
+    e_dw, e_dw_ag = rel(outs["fn"][2], want_dw), rel(outs["autograd"][2], want_dw)
+    log(f"    dX rel_l2 {e_dx:.2e} (autograd {e_dx_ag:.2e}); dW rel_l2 {e_dw:.2e} (autograd {e_dw_ag:.2e})")
+    assert outs["fn"][1].dtype == x.dtype and outs["fn"][2].dtype == w.dtype
+    assert e_dx < 5e-3 and e_dw < 1e-4 and e_dw <= e_dw_ag + 1e-6
