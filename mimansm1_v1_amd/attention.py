@@ -35,6 +35,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
+from .wgrad import wgrad
 from . import tuned
 
 DTYPE = torch.bfloat16
@@ -446,10 +447,8 @@ def apply_rope(x, cos, sin):
 _HIP_BACKENDS = ("hip", "tilelang")
 
 
-# Token chunks of the weight-gradient GEMM: dW = dY^T X sums over all B*S
-# tokens but has only N x K outputs (1792 x 1280 for wq|wk|wv), too few tiles
-# to fill 256 CUs; 8 chunks with fp32 outputs, summed in fp32, measured
-# 113-129 us against 157 us for the single bf16 GEMM at 16,384 tokens.
+# Token chunks of the projections' weight-gradient GEMMs (wgrad.py): 8
+# measured fastest for wq|wk|wv and wo at 16,384 tokens.
 PROJ_DW_CHUNKS = 8
 
 
@@ -482,14 +481,7 @@ class BF16Linear(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = (dy2 @ wb).reshape(*dy.shape[:-1], k).to(ctx.x_dtype)
         if ctx.needs_input_grad[1]:
-            t = x2.shape[0]
-            c = PROJ_DW_CHUNKS
-            if t % c == 0 and t >= 64 * c:
-                dw = torch.bmm(dy2.reshape(c, t // c, n).transpose(1, 2), x2.reshape(c, t // c, k).contiguous(),
-                               out_dtype=torch.float32).sum(0)
-            else:
-                dw = torch.mm(dy2.t(), x2, out_dtype=torch.float32)
-            dw = dw.to(ctx.w_dtype)
+            dw = wgrad(dy2, x2, PROJ_DW_CHUNKS).to(ctx.w_dtype)
         return dx, dw
 
 
