@@ -241,3 +241,34 @@ def test_profsum_tables(tmp_path, capsys):
     assert "attn_fwd_kernel<4, 2, true>" in text and "| 3 | 10.0 |" in text
     # mean fetch 20 KiB x 2 (copy read 512 KiB for 1 MiB) + 4 KiB writes x 1
     assert json.loads(out.read_text())["fwd"] == (20 * 2 + 4) * 1024
+
+
+@pytest.mark.parametrize("t,chunks", [(512, 2), (4096, 8), (1000, 8), (100, 2), (256, 1)])
+def test_wgrad_chunking_equals_one_product(monkeypatch, t, chunks):
+    """wgrad's token chunking (reshape per chunk, transpose of the left
+    operand, fp32 sum) equals the one product a^T b; uneven or short token
+    counts take the single product.  Run in fp32 on the CPU, where the
+    fp32-output GEMM forms are stood in by plain fp32 products."""
+    import torch
+    from mimansm1_v1_amd import wgrad as W
+    calls = []
+    bmm, mm = torch.bmm, torch.mm
+
+    def bmm32(x, y, out_dtype=None):
+        calls.append("bmm")
+        return bmm(x.double(), y.double()).float()
+
+    def mm32(x, y, out_dtype=None):
+        calls.append("mm")
+        return mm(x.double(), y.double()).float()
+
+    monkeypatch.setattr(W.torch, "bmm", bmm32)
+    monkeypatch.setattr(W.torch, "mm", mm32)
+    gen = torch.Generator().manual_seed(t)
+    a, b = torch.randn(t, 7, generator=gen), torch.randn(t, 5, generator=gen)
+    got = W.wgrad(a, b, chunks)
+    want = (a.double().t() @ b.double()).float()
+    assert got.shape == (7, 5)
+    assert torch.allclose(got, want, atol=1e-4, rtol=1e-5)
+    chunked = chunks > 1 and t % chunks == 0 and t >= 64 * chunks
+    assert calls == (["bmm"] if chunked else ["mm"])
