@@ -31,6 +31,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// k-steps by which rows_chain2's operand reads run ahead of their products
+// (1 measured faster than 0; 2 no faster than 1).
+#ifndef MM1_FWD_PREFETCH
+#define MM1_FWD_PREFETCH 1
+#endif
+
 namespace mm1 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -258,18 +264,22 @@ __device__ __forceinline__ bf16x8 rows_a(const char* tile, const LdsBases& lb, i
 // product pair would wait for the full LDS latency.
 __device__ __forceinline__ void rows_chain2(const char* tile, const LdsBases& lb, const bf16x8 (&b)[8],
                                             f32x16 (&acc)[2]) {
-  bf16x8 fa[2][2];
-  fa[0][0] = rows_a(tile, lb, 0, 0);
-  fa[0][1] = rows_a(tile, lb, 1, 0);
+  constexpr int PF = MM1_FWD_PREFETCH;
+  bf16x8 fa[PF + 1][2];
+#pragma unroll
+  for (int ks = 0; ks < PF; ++ks) {
+    fa[ks][0] = rows_a(tile, lb, 0, ks);
+    fa[ks][1] = rows_a(tile, lb, 1, ks);
+  }
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    if (ks + 1 < 8) {
-      fa[(ks + 1) & 1][0] = rows_a(tile, lb, 0, ks + 1);
-      fa[(ks + 1) & 1][1] = rows_a(tile, lb, 1, ks + 1);
+    if (ks + PF < 8) {
+      fa[(ks + PF) % (PF + 1)][0] = rows_a(tile, lb, 0, ks + PF);
+      fa[(ks + PF) % (PF + 1)][1] = rows_a(tile, lb, 1, ks + PF);
     }
     __builtin_amdgcn_sched_barrier(0);
-    acc[0] = mfma32(fa[ks & 1][0], b[ks], acc[0]);
-    acc[1] = mfma32(fa[ks & 1][1], b[ks], acc[1]);
+    acc[0] = mfma32(fa[ks % (PF + 1)][0], b[ks], acc[0]);
+    acc[1] = mfma32(fa[ks % (PF + 1)][1], b[ks], acc[1]);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
