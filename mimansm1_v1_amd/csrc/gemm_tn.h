@@ -234,11 +234,15 @@ __device__ __forceinline__ void run(const Problem& p, char* smem, Pro&& pro, Epi
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
           if (kk + 1 < 4) load_frags(xs, ws, kk + 1, nxt);
+          // keep the next k step's reads ahead of this one's products: the
+          // scheduler would otherwise sink them and wait on each pair
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             acc[0][i] = mfma32(cur.w[0], cur.xb[i], acc[0][i]);
             acc[1][i] = mfma32(cur.w[1], cur.xb[i], acc[1][i]);
           }
+          __builtin_amdgcn_sched_barrier(0);
           if (kk + 1 < 4) cur = nxt;
         }
       }
