@@ -41,6 +41,13 @@
 #define MM1_DQ_PREFETCH 1
 #endif
 
+// 1: the dK/dV kernel's S / dP products read each Q / dO row fragment one
+// k-step ahead of its product (dK/dV 0.2% faster than 0, a repeatable
+// near-tie: the kernel waits on the LDS queue, not on read latency).
+#ifndef MM1_DKDV_PREFETCH
+#define MM1_DKDV_PREFETCH 1
+#endif
+
 namespace mm1 {
 
 // ---------------------------------------------------------------------------
@@ -516,8 +523,22 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // 8*(r/4) + 4*h + (r%4) of the tile, lane l32 holds key kw0 + l32)
   auto product = [&](const char* t) {
     f32x16 sacc = zero16();
+#if MM1_DKDV_PREFETCH
+    // the next fragment's read is issued before this product; VALU work
+    // (the P wave's exp of the previous tile) may still move in between
+    bf16x8 fa[2];
+    fa[0] = rows_a(t, lb, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      if (ks + 1 < 8) fa[(ks + 1) & 1] = rows_a(t, lb, 0, ks + 1);
+      __builtin_amdgcn_sched_barrier(0x406);
+      sacc = mfma32(fa[ks & 1], breg[ks], sacc);
+      __builtin_amdgcn_sched_barrier(0x406);
+    }
+#else
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) sacc = mfma32(rows_a(t, lb, 0, ks), breg[ks], sacc);
+#endif
     return sacc;
   };
   if (pwave) snext = product(smem);
