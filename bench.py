@@ -13,10 +13,11 @@ is measured live over the timed region.
 
 Printed: one JSON line.  ``value`` is algorithmic TFLOP/s of the whole step
 (7 * B * H * S^2 * D for causal fwd+bwd: fwd 2 GEMMs + bwd 5 GEMMs of
-2*S^2*D/2 each per head); ``roofline`` is the dominant kernel's algorithmic
-TFLOP/s against the bf16 dense MFMA peak; ``cpu_baseline`` is the fp32
-reference math (oracle, torch autograd) timed on this host's cores on one KV
-group of one batch element of the same workload.
+2*S^2*D/2 each per head), from the median of --repeats timed loops of
+--steps steps; ``roofline`` is the dominant kernel's algorithmic TFLOP/s
+against the bf16 dense MFMA peak; ``cpu_baseline`` is the fp32 reference math
+(oracle, torch autograd) timed on this host's cores on the same workload (or
+one batch element of it when host RAM is short).
 """
 from __future__ import annotations
 
@@ -52,8 +53,13 @@ def parse(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
-    ap.add_argument("--also", type=int, nargs="*", default=[2, 5],
+    ap.add_argument("--also", type=int, nargs="*", default=[2, 4, 5],
                     help="extra configs reported beside the main one (5 = the attention sublayer)")
+    ap.add_argument("--repeats", type=int, default=5,
+                    help="timed loops of --steps steps; the reported figures are their median")
+    ap.add_argument("--tiles", default=None, metavar="FWD,DKDV,DQ",
+                    help="tiling indices (mm1_attn_tile_desc) for the stage calls instead of the "
+                         "tile table's choice for the workload (A/B runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-ffn", action="store_true",
                     help="skip the SwiGLU feed-forward leg (reported beside the attention line)")
@@ -73,17 +79,19 @@ def parse(argv=None):
 
 # Kernel launched by each tiling index of a stage (mm1_attn_tile_desc order).
 KERNEL_NAMES = {"fwd": ("attn_fwd_pp_kernel", "attn_fwd_kernel", "attn_fwd_kernel"),
-                "dkdv": ("attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel", "attn_dkdv_kernel"),
+                "dkdv": ("attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel", "attn_dkdv_kernel",
+                         "attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel"),
                 "dq": ("attn_dq_kernel", "attn_dq_kernel")}
-TILE_ENV = {"fwd": "MM1_FWD_VARIANT", "dkdv": "MM1_DKDV_VARIANT", "dq": "MM1_DQ_VARIANT"}
-USER_TILE_ENV = {k: os.environ[v] for k, v in TILE_ENV.items() if v in os.environ}
 
 
-def select_tiles(batch, seq):
+def select_tiles(batch, seq, override=None):
     """The tilings the tile record (this machine's store, then the shipped
     gfx950 table) holds for this workload -- what get_kernel's handles launch
-    -- applied to the stage calls through their per-call environment switch.
-    A switch the caller set explicitly wins.  Returns {stage: index}."""
+    -- or `override` ("FWD,DKDV,DQ").  Returns {stage: index}; the stage
+    calls pass them explicitly."""
+    if override:
+        f, k, q = (int(x) for x in override.split(","))
+        return {"fwd": f, "dkdv": k, "dq": q}
     from mimansm1_v1_amd import attention as A
     from mimansm1_v1_amd import tuned
     shape = (batch, HEADS, seq, DIM, True, HEADS // KV_HEADS)
@@ -91,25 +99,48 @@ def select_tiles(batch, seq):
     bwd_cfg = tuned.lookup("attention_bwd", shape)
     fwd = A.tile_index("fwd", fwd_cfg) if fwd_cfg else None
     bwd = A.tile_index("bwd", bwd_cfg) if bwd_cfg else None
-    chosen = {"fwd": fwd or 0, "dkdv": (bwd or (0, 0))[0], "dq": (bwd or (0, 0))[1]}
-    for stage, env in TILE_ENV.items():
-        if stage in USER_TILE_ENV:
-            chosen[stage] = int(USER_TILE_ENV[stage])
-        os.environ[env] = str(chosen[stage])
-    return chosen
+    return {"fwd": fwd or 0, "dkdv": (bwd or (0, 0))[0], "dq": (bwd or (0, 0))[1]}
+
+
+def rope_rotate(x, theta=10_000.0):
+    """Rotate-half RoPE in fp32 at positions 0..S-1: pair (x_i, x_{i+D/2})
+    turned by angle pos * theta^(-2i/D) (the form of AT:533-541)."""
+    import torch
+    B, S, H, D = x.shape
+    half = D // 2
+    inv = theta ** (-2.0 * torch.arange(half, dtype=torch.float64) / D)
+    ang = torch.arange(S, dtype=torch.float64)[:, None] * inv[None, :]
+    c = ang.cos().float().view(1, S, 1, half)
+    sn = ang.sin().float().view(1, S, 1, half)
+    lo, hi = x[..., :half], x[..., half:]
+    return torch.cat([lo * c - hi * sn, lo * sn + hi * c], dim=-1)
 
 
 class Workload:
-    def __init__(self, lib, batch, seq, device, seed=0):
+    """One batch of a BASELINE.json config resident in HBM, and the stage
+    calls of one fwd+bwd step.  Inputs are drawn on the CPU from one seeded
+    generator in the order Q, K, V, dO; with rope_sigma (config 4) a scale
+    sigma ~ U(0.5, 3) per query head and per KV head follows, Q and K are
+    scaled by it and rotated by RoPE (base 10000) in fp32, then all are cast
+    to bf16."""
+
+    def __init__(self, lib, batch, seq, device, tiles, seed=0, rope_sigma=False):
         import torch
         self.lib, self.B, self.S = lib, batch, seq
         self.H, self.Hkv, self.D = HEADS, KV_HEADS, DIM
+        self.tiles = tiles
         gen = torch.Generator().manual_seed(seed)
-        mk = lambda *shape: torch.randn(*shape, generator=gen).to(torch.bfloat16).to(device)
-        self.q = mk(batch, seq, HEADS, DIM)
-        self.k = mk(batch, seq, KV_HEADS, DIM)
-        self.v = mk(batch, seq, KV_HEADS, DIM)
-        self.do = mk(batch, seq, HEADS, DIM)
+        q = torch.randn(batch, seq, HEADS, DIM, generator=gen)
+        k = torch.randn(batch, seq, KV_HEADS, DIM, generator=gen)
+        v = torch.randn(batch, seq, KV_HEADS, DIM, generator=gen)
+        do = torch.randn(batch, seq, HEADS, DIM, generator=gen)
+        if rope_sigma:
+            sq = torch.empty(HEADS).uniform_(0.5, 3.0, generator=gen)
+            sk = torch.empty(KV_HEADS).uniform_(0.5, 3.0, generator=gen)
+            q = rope_rotate(q * sq.view(1, 1, HEADS, 1))
+            k = rope_rotate(k * sk.view(1, 1, KV_HEADS, 1))
+        dev = lambda t: t.to(torch.bfloat16).to(device)
+        self.q, self.k, self.v, self.do = dev(q), dev(k), dev(v), dev(do)
         self.o = torch.empty_like(self.q)
         self.lse = torch.empty(batch, HEADS, seq, dtype=torch.float32, device=device)
         self.delta = torch.empty_like(self.lse)
@@ -132,52 +163,63 @@ class Workload:
             if rc != 0:
                 raise RuntimeError(f"{name}: {L.mm1_attn_strerror(rc).decode()}")
 
-        chk(L.mm1_attn_fwd(p(self.q), p(self.k), p(self.v), p(self.o), p(self.lse),
-                           B, S, H, Hkv, D, 1, self.scale, sp), "fwd")
+        t = self.tiles
+        chk(L.mm1_attn_fwd_tiles(p(self.q), p(self.k), p(self.v), p(self.o), p(self.lse),
+                                 B, S, H, Hkv, D, 1, self.scale, t["fwd"], sp), "fwd")
         if marks is not None:
             marks[0].record(self.stream)
         chk(L.mm1_attn_delta(p(self.o), p(self.do), p(self.delta), B, S, H, D, sp), "delta")
         if marks is not None:
             marks[1].record(self.stream)
-        chk(L.mm1_attn_bwd_dkdv(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
-                                p(self.delta), p(self.dk), p(self.dv), p(self.ws), self.ws_bytes,
-                                B, S, H, Hkv, D, 1, self.scale, sp), "dkdv")
+        chk(L.mm1_attn_bwd_dkdv_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
+                                      p(self.delta), p(self.dk), p(self.dv), p(self.ws), self.ws_bytes,
+                                      B, S, H, Hkv, D, 1, self.scale, t["dkdv"], sp), "dkdv")
         if marks is not None:
             marks[2].record(self.stream)
         # dQ, with the dK/dV group sum folded into the same launch (what
         # mm1_attn_bwd runs after mm1_attn_bwd_dkdv)
-        chk(L.mm1_attn_bwd_dq_reduce(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
-                                     p(self.delta), p(self.dq), p(self.dk), p(self.dv),
-                                     p(self.ws), self.ws_bytes, B, S, H, Hkv, D, 1, self.scale, sp),
+        chk(L.mm1_attn_bwd_dq_reduce_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
+                                           p(self.delta), p(self.dq), p(self.dk), p(self.dv),
+                                           p(self.ws), self.ws_bytes, B, S, H, Hkv, D, 1, self.scale,
+                                           t["dkdv"], t["dq"], sp),
             "dq")
         if marks is not None:
             marks[3].record(self.stream)
 
 
-def time_workload(wl, steps, warmup):
+def time_workload(wl, steps, warmup, repeats=5):
+    """W warm-up steps, then `repeats` timed loops of exactly `steps` steps,
+    each bracketed by a device synchronisation, with HIP events on the launch
+    stream after every stage.  Returns the median loop's ms per step, its
+    per-stage ms, and every loop's ms per step."""
     import torch
     for _ in range(warmup):
         wl.step()
     torch.cuda.synchronize()
     ev = lambda: torch.cuda.Event(enable_timing=True)
-    start = ev()
-    marks = [[ev() for _ in Workload.STAGES] for _ in range(steps)]
-    begins = [ev() for _ in range(steps)]
-    start.record(wl.stream)
-    for i in range(steps):
-        begins[i].record(wl.stream)
-        wl.step(marks[i])
-    end = ev()
-    end.record(wl.stream)
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    per_stage = {name: 0.0 for name in Workload.STAGES}
-    for i in range(steps):
-        prev = begins[i]
-        for name, mk in zip(Workload.STAGES, marks[i]):
-            per_stage[name] += prev.elapsed_time(mk)
-            prev = mk
-    return total_ms / steps, {k: v / steps for k, v in per_stage.items()}
+    loops = []
+    for _ in range(repeats):
+        start = ev()
+        marks = [[ev() for _ in Workload.STAGES] for _ in range(steps)]
+        begins = [ev() for _ in range(steps)]
+        torch.cuda.synchronize()
+        start.record(wl.stream)
+        for i in range(steps):
+            begins[i].record(wl.stream)
+            wl.step(marks[i])
+        end = ev()
+        end.record(wl.stream)
+        torch.cuda.synchronize()
+        per_stage = {name: 0.0 for name in Workload.STAGES}
+        for i in range(steps):
+            prev = begins[i]
+            for name, mk in zip(Workload.STAGES, marks[i]):
+                per_stage[name] += prev.elapsed_time(mk)
+                prev = mk
+        loops.append((start.elapsed_time(end) / steps, {k: v / steps for k, v in per_stage.items()}))
+    order = sorted(range(repeats), key=lambda i: loops[i][0])
+    ms, stages = loops[order[repeats // 2]]
+    return ms, stages, [round(x[0], 4) for x in loops]
 
 
 def time_autograd(batch, seq, device, steps, warmup):
@@ -442,26 +484,37 @@ def time_lm_head(tokens, device, steps, warmup):
     }
 
 
-def cpu_baseline(seq):
-    """fp32 reference math (oracle restatement of AT:521-530, autograd backward)
-    on one KV group (5 query heads, 1 KV head) of one batch element, full seq."""
+def cpu_baseline(config):
+    """The reference's CPU attention path: the fp32 reference math (the
+    oracle's restatement of AT:521-530, autograd for the backward) on this
+    host's cores, on the bench workload itself when host RAM allows (autograd
+    keeps about four fp32 [B, H, S, S] score-sized tensors), else on one batch
+    element (reported per batch element).  One warm-up run, then the median of
+    three timed runs."""
     import torch
     from oracle import reference as R
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    q, k, v, do = R.make_inputs(1, seq, HEADS // KV_HEADS, 1, DIM, seed=0, dtype=torch.float32)
+    B, S = CONFIGS[config]["batch"], CONFIGS[config]["seq"]
+    need = 4 * 4.0 * B * HEADS * S * S + (16 << 30)
+    try:
+        import psutil
+        avail = psutil.virtual_memory().available
+    except ImportError:
+        avail = 0
+    full = avail >= need
+    batch = B if full else 1
+    q, k, v, do = R.make_inputs(batch, S, HEADS, KV_HEADS, DIM, seed=0, dtype=torch.float32,
+                                rope_sigma=(config == 4))
+    flops = 7 * gemm_unit(batch, S)       # algorithmic 7*B*H*S^2*D (gemm_unit holds the causal 1/2)
     groups = HEADS // KV_HEADS
-    flops = 7 * gemm_unit(1, seq, heads=groups) / 2
+    R.grads(q, k, v, do, True, groups)    # warm-up
     times = []
-    budget = 30.0
-    t_start = time.perf_counter()
-    while True:
+    for _ in range(3):
         t0 = time.perf_counter()
         R.grads(q, k, v, do, True, groups)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 3 or time.perf_counter() - t_start + times[-1] > budget:
-            break
-    best = sorted(times)[len(times) // 2]
+    med = sorted(times)[1]
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -470,15 +523,18 @@ def cpu_baseline(seq):
                 break
     except OSError:
         pass
+    what = (f"the full config {config} workload (batch {B})" if full else
+            f"batch 1 of config {config} (host RAM {avail / 2**30:.0f} GiB < {need / 2**30:.0f} GiB "
+            f"for the full batch of {B}; the rate is per batch element)")
     return {
-        "value": round(flops / best / 1e12, 5),
+        "value": round(flops / med / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"fp32 torch autograd of the reference math (oracle/reference.py) on batch 1 x "
-                   f"1 KV group (5 query heads) x seq {seq} x d 128, causal fwd+bwd; median of "
-                   f"{len(times)} runs, {best:.2f} s each; algorithmic flops 7*B*H*S^2*D with "
-                   f"B*H = 5; CPU: {model}"),
+        "sample": (f"fp32 torch autograd of the reference math (oracle/reference.py, AT:521-530) on "
+                   f"{what}: seq {S}, 10 query / 2 KV heads, d 128, causal fwd+bwd; 1 warm-up run, "
+                   f"median of 3 runs = {med:.2f} s per fwd+bwd; algorithmic flops 7*B*H*S^2*D "
+                   f"(causal halves counted) = {flops / 1e9:.1f} GFLOP; CPU: {model}"),
     }
 
 
@@ -518,9 +574,9 @@ def main(argv=None):
                   f"parts {res['part_ms']}, other {res['other_ms']:.3f}", file=sys.stderr, flush=True)
             continue
         B, S = CONFIGS[cfg]["batch"], CONFIGS[cfg]["seq"]
-        tiles = select_tiles(B, S)
-        wl = Workload(lib, B, S, device)
-        ms, stages = time_workload(wl, args.steps, args.warmup)
+        tiles = select_tiles(B, S, args.tiles)
+        wl = Workload(lib, B, S, device, tiles, rope_sigma=(cfg == 4))
+        ms, stages, loops = time_workload(wl, args.steps, args.warmup, args.repeats)
         unit = gemm_unit(B, S)
         flops = {"fwd": 2 * unit, "dkdv": 4 * unit, "dq": 3 * unit}
         res = {
@@ -532,6 +588,7 @@ def main(argv=None):
             "kernel_tflops": {k: flops[k] / (stages[k] * 1e-3) / 1e12 for k in flops},
             "kernel_flops": flops,
             "tiles": tiles,
+            "loops_ms_per_step": loops,
         }
         if not args.no_autograd:
             res["ms_per_step_autograd"] = time_autograd(B, S, device, args.steps, args.warmup)
@@ -596,6 +653,8 @@ def main(argv=None):
         "bwd_tflops": round(main_res["bwd_tflops"], 2),
         "stage_ms": {k: round(v, 4) for k, v in main_res["stage_ms"].items()},
         "tiles": main_res["tiles"],
+        "repeats": args.repeats,
+        "loops_ms_per_step": main_res["loops_ms_per_step"],
         "reference_flop_count_tflops": round(main_res["tflops"] * 5 / 7, 2),
         "roofline": {
             "bound": "mfma",
@@ -624,13 +683,18 @@ def main(argv=None):
             "ms_per_step": round(res["ms_per_step"], 4),
             "fwd_tflops": round(res["fwd_tflops"], 2), "bwd_tflops": round(res["bwd_tflops"], 2),
             "stage_ms": {k: round(v, 4) for k, v in res["stage_ms"].items()},
+            "tiles": res["tiles"],
+            "loops_ms_per_step": res["loops_ms_per_step"],
         }
+        if cfg == 4:
+            out[f"config{cfg}"]["inputs"] = ("RoPE-rotated Q, K with sigma ~ U(0.5, 3) per head (BASELINE.json "
+                                             "config 4), V, dO ~ N(0,1)")
     if ffn_res is not None:
         out["swiglu"] = ffn_res
     if head_res is not None:
         out["lm_head"] = head_res
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(S)
+        out["cpu_baseline"] = cpu_baseline(args.config)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -5,8 +5,10 @@
  * as `void*`, fp32 tensors as `float*`, the HIP stream as `void*`
  * (a hipStream_t; NULL = the default stream).  The caller owns every buffer;
  * the library allocates no device memory, never synchronises and is safe to
- * call from several host threads.  Its only state is a host-side cache of
- * per-shape workgroup dispatch tables (mm1_attn_dispatch_order).
+ * call from several host threads.  Its only state is host-side: a cache of
+ * per-shape workgroup dispatch tables (mm1_attn_dispatch_order) and, per
+ * backward workspace, the layout of the dK/dV partial sums the last
+ * mm1_attn_bwd_dkdv* call on it wrote (checked by the calls that sum them).
  *
  * Layouts (all contiguous, last dimension stride 1):
  *   q, o, dO, dq : [B, S, H,   D] bf16
@@ -26,7 +28,7 @@
 extern "C" {
 #endif
 
-#define MM1_ATTN_VERSION 2
+#define MM1_ATTN_VERSION 3
 
 #define MM1_OK 0
 #define MM1_E_NULL (-1)        /* a required pointer is NULL */
@@ -36,6 +38,8 @@ extern "C" {
 #define MM1_E_SCALE (-5)       /* sm_scale not a positive finite number */
 #define MM1_E_ALIGN (-6)       /* a tensor pointer is not 16-byte aligned */
 #define MM1_E_TILES (-7)       /* tiling index out of range (see mm1_attn_tile_count) */
+#define MM1_E_LAYOUT (-8)      /* the workspace holds no dK/dV partial sums of this shape and
+                                  dK/dV tiling (see mm1_attn_bwd_dkdv_reduce) */
 
 /* Kernel kinds for the tiling queries below. */
 #define MM1_TILES_FWD 0
@@ -52,6 +56,14 @@ int mm1_attn_version(void);
 int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                  void* stream);
+
+/* The forward with fp32 o [B, S, H, D]: the values mm1_attn_fwd rounds to
+ * bf16 (its 4-wave tiling; lse2 as mm1_attn_fwd).  No counterpart in the
+ * reference, whose forward writes bf16 O (attention_tilelang.py:182-185): for
+ * callers that check O where one bf16 half-ulp of |O| is already more than
+ * their tolerance. */
+int mm1_attn_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2,
+                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream);
 
 /* Backward preprocess: delta[b,h,i] = sum_d o[b,i,h,d] * dO[b,i,h,d] (fp32).
  * Replaces flash_delta(B, H, S, D)(O, dO) -> Delta
@@ -80,16 +92,21 @@ int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
  * mm1_attn_bwd_dkdv then mm1_attn_bwd_dq_reduce; mm1_attn_bwd_dkdv_reduce
  * followed by mm1_attn_bwd_dq is the same result in two launches.
  *  - mm1_attn_bwd_dkdv: dK/dV.  With H == Hkv it writes bf16 dk, dv directly.
- *    Otherwise, with the per-head tilings (1, 2) it writes the per-query-head
- *    fp32 partial sums into `workspace` ([2][G][B][S][Hkv][D], G = H / Hkv)
- *    and leaves dk/dv untouched; with the grouped tiling (0) it writes bf16
- *    dk, dv directly for the key tiles one workgroup covers and fp32 partials
- *    (one slot per chunk, see mm1_attn_dkdv_plan) for the others.
+ *    Otherwise, with the per-head tilings (1, 2, 4) it writes the
+ *    per-query-head fp32 partial sums into `workspace`
+ *    ([2][G][B][S][Hkv][D], G = H / Hkv) and leaves dk/dv untouched; with the
+ *    grouped tilings (0, 3) it writes bf16 dk, dv directly for the key tiles
+ *    one workgroup covers and fp32 partials (one slot per chunk, see
+ *    mm1_attn_dkdv_plan) for the others.
  *  - mm1_attn_bwd_dkdv_reduce: sums the partials of each KV head and writes
- *    bf16 dk, dv (no-op when H == Hkv).  It follows the layout of the default
- *    dK/dV tiling (MM1_DKDV_VARIANT, read per call), so it must see the same
- *    environment and `causal` as the mm1_attn_bwd_dkdv call before it; the
- *    same holds for mm1_attn_bwd_dq_reduce.
+ *    bf16 dk, dv (no-op when H == Hkv).  The layout it reads is the one the
+ *    default dK/dV tiling writes; mm1_attn_bwd_dkdv_reduce_tiles names the
+ *    tiling.  The partials must come from a mm1_attn_bwd_dkdv* call on the
+ *    same workspace with the same shape, `causal` and dK/dV tiling: the
+ *    library records, per workspace address, the layout that call wrote, and
+ *    the summing calls return MM1_E_LAYOUT (launching nothing) when the
+ *    record is missing or differs.  The same holds for
+ *    mm1_attn_bwd_dq_reduce*.
  *  - mm1_attn_bwd_dq: bf16 dq.
  *  - mm1_attn_bwd_dq_reduce: bf16 dq, and the group sum of
  *    mm1_attn_bwd_dkdv_reduce done by the tail of the same launch (must run
@@ -113,6 +130,43 @@ int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const vo
                            int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                            void* stream);
 
+/* The stages with an explicit tiling (indices of mm1_attn_tile_desc, -1 =
+ * the default): what a tuned kernel handle that stages the backward calls.
+ * A summing call must name the dK/dV tiling of the mm1_attn_bwd_dkdv_tiles
+ * call that filled the workspace (else MM1_E_LAYOUT). */
+int mm1_attn_bwd_dkdv_tiles(const void* q, const void* k, const void* v, const void* dO,
+                            const float* lse2, const float* delta, void* dk, void* dv,
+                            void* workspace, size_t workspace_bytes,
+                            int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                            int dkdv_tiles, void* stream);
+int mm1_attn_bwd_dkdv_reduce_tiles(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
+                                   int B, int S, int H, int Hkv, int D, int causal, int dkdv_tiles,
+                                   void* stream);
+int mm1_attn_bwd_dq_tiles(const void* q, const void* k, const void* v, const void* dO,
+                          const float* lse2, const float* delta, void* dq,
+                          int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                          int dq_tiles, void* stream);
+int mm1_attn_bwd_dq_reduce_tiles(const void* q, const void* k, const void* v, const void* dO,
+                                 const float* lse2, const float* delta, void* dq, void* dk, void* dv,
+                                 const void* workspace, size_t workspace_bytes,
+                                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                                 int dkdv_tiles, int dq_tiles, void* stream);
+
+/* The backward with fp32 gradients: dq, dk, dv as fp32 [B,S,H,D] /
+ * [B,S,Hkv,D], the values mm1_attn_bwd rounds to bf16 (up to the fp32
+ * summation order of the dK/dV tiling: this call sums per-head fp32 partials
+ * in head order).  Needs mm1_attn_bwd_f32_workspace_size() bytes of scratch
+ * (2 * G slots of [B,S,Hkv,D] fp32, also for G == 1).  Replaces the fp32
+ * dQ / dK / dV buffers that get_kernel("bwd", ...) fills
+ * (attention_tilelang.py:258-260, :381-387) before flash_unswizzle and the
+ * casts: a caller that wants the unrounded gradients (a parity check, an
+ * fp32 master-gradient path) uses it. */
+size_t mm1_attn_bwd_f32_workspace_size(int B, int S, int H, int Hkv, int D);
+int mm1_attn_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
+                     const float* lse2, const float* delta, float* dq, float* dk, float* dv,
+                     void* workspace, size_t workspace_bytes,
+                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream);
+
 /* Tilings compiled into the library.  The reference autotunes each TileLang
  * kernel over a space of (block_M, block_N, threads, num_stages)
  * (attention_tilelang.py:61-98) and remembers the winner per (device, kernel,
@@ -123,9 +177,8 @@ int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const vo
  *    MM1_TILES_DKDV or MM1_TILES_DQ (0 for another kind);
  *  - mm1_attn_tile_desc(kind, i): static "key=value ..." description of
  *    tiling i (block_M, block_N, waves, stages, schedule), NULL if out of range.
- * Index 0 is each kind's default.  The calls without a tiling argument use
- * the default unless the environment variable MM1_FWD_VARIANT,
- * MM1_DKDV_VARIANT or MM1_DQ_VARIANT names another index (read per call). */
+ * Index 0 is each kind's default, which the calls without a tiling argument
+ * use. */
 int mm1_attn_tile_count(int kind);
 const char* mm1_attn_tile_desc(int kind, int index);
 

@@ -20,6 +20,8 @@ SIGNATURES = {
                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_attn_fwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                     _c_int, _c_int, _c_float, _c_int, _vp]),
+    "mm1_attn_fwd_f32": (_c_int, [_vp, _vp, _vp, _vp, _vp,
+                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_attn_tile_count": (_c_int, [_c_int]),
     "mm1_attn_tile_desc": (ctypes.c_char_p, [_c_int, _c_int]),
     "mm1_attn_delta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
@@ -29,6 +31,9 @@ SIGNATURES = {
     "mm1_attn_bwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
                                     _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
                                     _c_int, _c_int, _vp]),
+    "mm1_attn_bwd_f32_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "mm1_attn_bwd_f32": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
+                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_attn_dispatch_order": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                          _c_int, _vp, _c_int]),
     "mm1_attn_bwd_dkdv": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
@@ -40,6 +45,16 @@ SIGNATURES = {
                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_attn_bwd_dq_reduce": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
                                         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_bwd_dkdv_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
+                                         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                         _c_int, _vp]),
+    "mm1_attn_bwd_dkdv_reduce_tiles": (_c_int, [_vp, _c_size, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
+                                                _c_int, _c_int, _c_int, _vp]),
+    "mm1_attn_bwd_dq_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                       _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _vp]),
+    "mm1_attn_bwd_dq_reduce_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
+                                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                              _c_int, _c_int, _vp]),
     "mm1_qknorm_rope_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_qknorm_rope_bwd_workspace_size": (_c_size, []),

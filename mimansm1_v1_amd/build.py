@@ -35,6 +35,15 @@ DEVICE_FLAGS = [
 ]
 
 
+# Per-source extra flags.  attn_bwd.hip holds kernels with one wave per SIMD
+# whose long-lived accumulators sit in AGPRs (inline-asm MFMAs); the
+# compiler's own MFMAs there must stay in the VGPR form, where the VALU reads
+# their results without copies.
+EXTRA_FLAGS = {
+    "attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -56,7 +65,7 @@ def build(verbose: bool = False, resource_usage: bool = False) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = obj_dir / (src.stem + ".o")
-        cmd = [cc, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [cc, *DEVICE_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
         if resource_usage:
             cmd.insert(1, "-Rpass-analysis=kernel-resource-usage")
         res = subprocess.run(cmd, capture_output=True, text=True)

@@ -8,10 +8,12 @@
 //   P_ij    = exp2(s_ij * scale2 - lse2_i)         (:297), zero above the diagonal (:298-301)
 //   dP_ij   = dO_i . V_j                           (:304)
 //   dV_j   += sum_i P_ij dO_i                      (:307)
-//   dS_ij   = P_ij (dP_ij - Delta_i)               (:310, rounded to bf16 for the products)
-//   dK_j   += sm_scale * sum_i dS_ij Q_i            (:311)
-//   dQ_i   += sm_scale * sum_j dS_ij K_j            (:314)
-// (sm_scale is applied to the fp32 accumulators instead of to dS.)
+//   dS_ij   = bf16(P_ij (dP_ij - Delta_i) sm_scale)  (:310, rounded to bf16 for the products)
+//   dK_j   += sum_i dS_ij Q_i                       (:311)
+//   dQ_i   += sum_j dS_ij K_j                       (:314)
+// with the bf16 roundings at the reference's points: P before dV^T, and
+// P (dP - Delta) sm_scale before dK^T and dQ (the dQ kernel takes sm_scale
+// into P through its lse2: exp2(s scale2 - lse2 + log2 sm_scale) = P sm_scale).
 //
 // The decomposition here is atomic-free and deterministic:
 //   * attn_delta_kernel   : Delta, one 16-lane group per two (b, s, h) rows.
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
             const f32x4 dl4 = *reinterpret_cast<const f32x4*>(dll + i0);
             const f32x4 p4 = *reinterpret_cast<const f32x4*>(mbox + 256 * a4);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) dsv[4 * a4 + c] = p4[c] * (sv[4 * a4 + c] - dl4[c]);
+            for (int c = 0; c < 4; ++c) dsv[4 * a4 + c] = p4[c] * (sv[4 * a4 + c] - dl4[c]) * sm_scale;
           }
 #pragma unroll
           for (int kh = 0; kh < 2; ++kh) {
@@ -318,7 +320,6 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
   if (key >= S) return;
   // D layout of dK^T / dV^T: register r of block db holds column
   // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
-  const float scale_out = pwave ? 1.f : sm_scale;
   if (G == 1) {
     __bf16* row = (pwave ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
@@ -327,7 +328,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
       for (int a4 = 0; a4 < 4; ++a4) {
         bf16x4 o4;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) o4[c] = (__bf16)(acc[db][4 * a4 + c] * scale_out);
+        for (int c = 0; c < 4; ++c) o4[c] = (__bf16)acc[db][4 * a4 + c];
         *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
       }
     }
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
       for (int a4 = 0; a4 < 4; ++a4) {
         f32x4 o4;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) o4[c] = acc[db][4 * a4 + c] * scale_out;
+        for (int c = 0; c < 4; ++c) o4[c] = acc[db][4 * a4 + c];
         *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
       }
     }
@@ -359,16 +360,27 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // dK, dV, software-pipelined across the two roles of a pair.
 //
 // Same decomposition and roles as attn_dkdv_kernel (one workgroup per
-// (128-key tile, query head), pair i owns keys kt*128 + 32i .. +31, P wave
-// keeps K and dV^T, dS wave keeps V and dK^T), but the query tiles are 32
-// rows and the work on a tile is spread over four segments:
+// 128-key tile; a pair of waves owns 32 * KB keys of it, the P wave keeping K
+// and dV^T, the dS wave V and dK^T), but the query tiles are 32 rows and the
+// work on a tile is spread over four segments:
 //   segment s, P wave : S(s+1) = Q(s+1) K^T | P(s) = exp2(S(s) scale2 - lse2) -> mailbox | dV^T += dO(s-1)^T P(s-1)
 //   segment s, dS wave: dP(s) = dO(s) V^T   | dS(s-1) = P(s-1) (dP(s-1) - Delta)          | dK^T += Q(s-2)^T dS(s-2)
 // Within a segment each wave's VALU work (middle column) depends on no
-// product of the same segment, so it runs under the wave's own 16 products
-// and the other wave's, and the pair meets at one barrier per segment, which
-// also publishes the DMA ring.  S(s+1), P(s-1) (bf16) stay in the P wave's
-// registers, dP(s-1) and dS(s-2) (bf16) in the dS wave's.
+// product of the same segment, so it runs under the wave's own products
+// (and, with two waves per SIMD, the other wave's), and the pair meets at one
+// barrier per segment, which also publishes the DMA ring.  S(s+1), P(s-1)
+// (bf16) stay in the P wave's registers, dP(s-1) and dS(s-2) (bf16) in the
+// dS wave's.
+//
+// KB = 32-key blocks per wave:
+//   KB = 1: 8 waves (4 pairs x 32 keys), two waves per SIMD (a pair shares
+//           one SIMD), 256 registers per wave;
+//   KB = 2: 4 waves (2 pairs x 64 keys), one wave per SIMD, 512 registers
+//           per wave.  Every LDS operand fragment (a Q / dO row fragment of S
+//           and dP, a transposed dO / Q fragment of dV^T and dK^T) feeds two
+//           products instead of one, which halves the LDS instructions per
+//           product: the LDS pipe (about one instruction per 4 cycles per
+//           CU) is what bounds KB = 1, at 2 LDS instructions per product.
 //
 // Tile x of the ring lives in slot x % NSTAGE; it is first read in segment
 // x-1 and last in segment x+2, so segment s refills slot (s-3) % NSTAGE with
@@ -376,25 +388,29 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // segments of lead).  Tiles whose queries all precede a pair's keys (causal)
 // are computed with the mask (P = 0): the pair would otherwise only wait at
 // the barrier.
-template <int NSTAGE, bool CAUSAL, bool GROUP, bool RAGGED>
-__global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
+template <int NSTAGE, bool CAUSAL, bool GROUP, bool RAGGED, int KB>
+__global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
     float* __restrict__ ws_dk, float* __restrict__ ws_dv,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order,
-    int chunk_tiles, int max_chunks, const DispatchOrder ord) {
+    int chunk_tiles, int max_chunks, const DispatchOrder ord, int force_partials) {
   static_assert(NSTAGE >= 6, "ring depth: at least 6");
+  static_assert(KB == 1 || KB == 2, "32 or 64 keys per wave");
+  constexpr int NW = 8 / KB;              // waves per workgroup
+  constexpr int NP = NW / 2;              // pairs
+  constexpr int QPW = 8 / NW;             // row quads of a 32-row tile each wave copies
   constexpr int BQ = 32;                  // query positions per tile
   constexpr int QT = BQ * HD * 2;         // one 32 x 128 bf16 operand tile
   constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse2 x 32 | Delta x 32], 1 KiB aligned
   constexpr int MBOX = 32 * 32 * 4;       // one 32 x 32 fp32 P block
-  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + 4 * 2 * MBOX];
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + NP * 2 * KB * MBOX];
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
-  const int pair = w & 3;
-  const bool pwave = w < 4;
+  const int pair = w % NP;
+  const bool pwave = w < NP;
   const int n_kt = (S + 127) / 128;
   // The work of this workgroup: key tile kt of (b, g) and the n_u query
   // tiles u0, u0 + ustep, u0 + 2*ustep, ... of the position-major walk over
@@ -402,7 +418,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // head hbase + u % HW of the group).  The chunks of a split key tile
   // interleave, so every workgroup starts at the sequence end and those that
   // run together stream the same rows.  The sums go to partial slot `part`
-  // of `nparts`, or straight to dk/dv when nparts == 1.
+  // of `nparts`, or straight to dk/dv when nparts == 1 (unless
+  // force_partials: fp32 partials in every case, for the fp32 backward).
   int b, g, kt, n_qt, u0, n_u, ustep, part, nparts, hbase, HW;
   if constexpr (GROUP) {
     const int j = dispatch_item(ord);
@@ -443,11 +460,11 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     hbase = hh;
     HW = 1;
   }
-  const int kw0 = kt * 128 + 32 * pair;   // this pair's first key
-  const int key = kw0 + l32;
-  // mailbox of this pair, two slots; [register group a4][lane] x 4 floats so
-  // each 16-byte access of a wave is one contiguous 1 KiB row
-  float* const mbox = reinterpret_cast<float*>(smem + NSTAGE * BUF + pair * 2 * MBOX) + lane * 4;
+  const int kw0 = kt * 128 + 32 * KB * pair;   // this pair's first key
+  // mailbox of this pair: two slots of KB blocks; a block is
+  // [register group a4][lane] x 4 floats, so each 16-byte access of a wave
+  // is one contiguous 1 KiB row
+  float* const mbox = reinterpret_cast<float*>(smem + NSTAGE * BUF + pair * 2 * KB * MBOX) + lane * 4;
 
   const int q_begin = CAUSAL ? kt * 128 : 0;
   const long qstride = (long)H * HD;
@@ -460,35 +477,46 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // workgroups that start together read the same rows together; the first
   // position tile can be partial (S % 32 != 0).  Tile cursors (walk head,
   // position tile) advance one tile at a time.
-  auto tile_p0 = [&](int t) { return q_begin + (n_qt - 1 - t) * BQ; };
-  auto advance = [&](int& hh, int& t) {
+  auto tile_p0 = [&](int t) MM1_INLINE { return q_begin + (n_qt - 1 - t) * BQ; };
+  auto advance = [&](int& hh, int& t) MM1_INLINE {
     hh += ustep;
     if (hh >= HW) {
       hh -= HW;
       ++t;
     }
   };
-  // LDS DMA, per wave and tile: row quad w of Q and of dO; wave 0 adds the
-  // lse2 | Delta vector.
+  // LDS DMA, per wave and tile: row quads w, w + NW, ... of Q and of dO;
+  // wave 0 adds the lse2 | Delta vector.  (quad & 3) == (w & 3) for every quad
+  // of the wave, so one per-lane offset serves all of them.
   const uint32_t dma_off = tile_lane_off(qstride, tid);
   const uint32_t lds_smem = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-  const uint32_t lds_quad = lds_smem + w * 1024;       // this wave's row quad in slot 0
-  const long quad_rows = (long)(4 * w) * qstride;      // its first row, in elements
   // Only position tile 0 can be partial, and only when S % 32 != 0
   // (RAGGED); the walks without partial tiles carry no code for them.
-  auto issue = [&](int slot, int hh, int t, auto may_be_partial) {
+  auto issue = [&](int slot, int hh, int t, auto may_be_partial) MM1_INLINE {
     const int p0 = tile_p0(t);
     const long rows = grp_rows + (long)hh * HD + (long)p0 * qstride;
     const float* vs = vec_src + (long)hh * S;
+    const uint32_t l = lds_smem + slot * BUF;
     if (!decltype(may_be_partial)::value || p0 + BQ <= S) {
-      const uint32_t l = lds_quad + slot * BUF;
-      dma16_sbase(dma_off, q + rows + quad_rows, l);
-      dma16_sbase(dma_off, dO + rows + quad_rows, l + QT);
-      if (w == 0) dma4(vs + p0, lds_smem + slot * BUF + 2 * QT);
+#pragma unroll
+      for (int i = 0; i < QPW; ++i) {
+        const int quad = w + NW * i;
+        dma16_sbase(dma_off, q + rows + (long)(4 * quad) * qstride, l + quad * 1024);
+        dma16_sbase(dma_off, dO + rows + (long)(4 * quad) * qstride, l + QT + quad * 1024);
+      }
+      if (w == 0) dma4(vs + p0, l + 2 * QT);
     } else {   // same DMA count per wave as a full tile
-      tile32_dma(smem + slot * BUF, q + rows, qstride, S - p0, dma_off, tid);
-      tile32_dma(smem + slot * BUF + QT, dO + rows, qstride, S - p0, dma_off, tid);
-      if (w == 0) dma4(vs + min(p0, S - 1 - l32), lds_smem + slot * BUF + 2 * QT);
+      const int L = tid & 63;
+#pragma unroll
+      for (int i = 0; i < QPW; ++i) {
+        const int quad = w + NW * i;
+        const int row = 4 * quad + (L >> 4);
+        const int chunk = (L & 15) ^ swz(row);
+        const long src = rows + (long)min(row, S - p0 - 1) * qstride + 8 * chunk;
+        dma16(q + src, l + quad * 1024);
+        dma16(dO + src, l + QT + quad * 1024);
+      }
+      if (w == 0) dma4(vs + min(p0, S - 1 - l32), l + 2 * QT);
     }
   };
   int itl = u0 / HW, ih = u0 - itl * HW;      // issue cursor
@@ -498,50 +526,74 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     advance(ih, itl);
   }
 
-  // This lane's key row of K (P wave) or V (dS wave) as the B operand.
-  bf16x8 breg[8];
-  {
-    const int kk = min(key, S - 1);
+  // This lane's key rows of K (P wave) or V (dS wave) as the B operands,
+  // one per key block.
+  bf16x8 breg[KB][8];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int kk = min(kw0 + 32 * kb + l32, S - 1);
     const __bf16* src = (pwave ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) breg[ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) pin(breg[ks]);
+    for (int ks = 0; ks < 8; ++ks) pin(breg[kb][ks]);
   }
 
-  f32x16 acc[4];   // dV^T (P wave) or dK^T (dS wave)
+  f32x16 acc[KB][4];   // dV^T (P wave) or dK^T (dS wave), per key block
 #pragma unroll
-  for (int db = 0; db < 4; ++db) acc[db] = zero16();
-  bf16x8 pb[2];    // P wave: P(s-1) as the B operand of dV^T
-  f32x16 snext;    // P wave: S(s), computed one segment ahead
-  f32x16 dpp;      // dS wave: dP(s-1)
-  bf16x8 sbp[2];   // dS wave: dS(s-2) as the B operand of dK^T
+  for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[kb][db] = zero16();
+  }
+  // KB = 2: the 128 accumulator registers live in AGPRs (mfma32_acc), the
+  // rest of the wave's state in the 256 VGPRs
+  auto accumulate = [&](f32x16& c, const bf16x8& a, const bf16x8& bb) MM1_INLINE {
+    if constexpr (KB == 2) mfma32_acc(a, bb, c);
+    else c = mfma32(a, bb, c);
+  };
+  // KB = 1 computes S one segment ahead (snext) and keeps dP of two
+  // segments (dpn, dpp), so that a wave's VALU work has products of its own
+  // to run under; KB = 2 has no registers for that and relies on the
+  // accumulation products of the previous tiles instead.
+  constexpr bool AHEAD = KB == 1;
+  bf16x8 pb[KB][2];    // P wave: P(s-1) as the B operand of dV^T
+  f32x16 snext[KB];    // P wave: S(s), computed one segment ahead (AHEAD)
+  f32x16 dpp[KB];      // dS wave: dP(s-1)
+  bf16x8 sbp[KB][2];   // dS wave: dS(s-2) as the B operand of dK^T
   const LdsBases lb = make_lds_bases(lane);
   wait_dma();
   __syncthreads();
-  // S = Q K^T / dP = dO V^T of one tile (D layout: register r holds query
-  // 8*(r/4) + 4*h + (r%4) of the tile, lane l32 holds key kw0 + l32)
-  auto product = [&](const char* t) {
-    f32x16 sacc = zero16();
+  // S = Q K^T / dP = dO V^T of one tile, per key block (D layout: register r
+  // holds query 8*(r/4) + 4*h + (r%4) of the tile, lane l32 holds key
+  // kw0 + 32*kb + l32); each row fragment is read once for all key blocks
+  auto product = [&](const char* t, f32x16 (&sacc)[KB]) MM1_INLINE {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) sacc[kb] = zero16();
 #if MM1_DKDV_PREFETCH
-    // the next fragment's read is issued before this product; VALU work
-    // (the P wave's exp of the previous tile) may still move in between
+    // the next fragment's read is issued before this step's products; VALU
+    // work (the P wave's exp of the previous tile) may still move in between
     bf16x8 fa[2];
     fa[0] = rows_a(t, lb, 0, 0);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       if (ks + 1 < 8) fa[(ks + 1) & 1] = rows_a(t, lb, 0, ks + 1);
       __builtin_amdgcn_sched_barrier(0x406);
-      sacc = mfma32(fa[ks & 1], breg[ks], sacc);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32(fa[ks & 1], breg[kb][ks], sacc[kb]);
       __builtin_amdgcn_sched_barrier(0x406);
     }
 #else
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) sacc = mfma32(rows_a(t, lb, 0, ks), breg[ks], sacc);
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8 fa = rows_a(t, lb, 0, ks);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32(fa, breg[kb][ks], sacc[kb]);
+    }
 #endif
-    return sacc;
   };
-  if (pwave) snext = product(smem);
+  if constexpr (AHEAD) {
+    if (pwave) product(smem, snext);
+  }
 
   // Segment s.  tn, tc, tp, tp2: ring slots of tiles s+1, s, s-1, s-2.
   // CUR: s < n_u; PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a
@@ -549,7 +601,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // segment with CUR, S(s+1) reads a slot holding another tile (or nothing
   // yet) and is discarded: every read stays inside the ring.
   auto segment = [&](const char* tn, const char* tc, const char* tp, const char* tp2, int refill,
-                     int s, auto role, auto cur, auto prev, auto prev2, auto sync) {
+                     int s, auto role, auto cur, auto prev, auto prev2, auto sync) MM1_INLINE {
     constexpr bool PW = decltype(role)::value;
     constexpr bool CUR = decltype(cur)::value, PREV = decltype(prev)::value;
     constexpr bool PREV2 = decltype(prev2)::value, SYNC = decltype(sync)::value;
@@ -559,88 +611,126 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
       advance(ih, itl);
     }
     if constexpr (PW) {
-      f32x16 sv;
+      f32x16 sv[KB];
       if constexpr (CUR) {
         const float* lsel = reinterpret_cast<const float*>(tc + 2 * QT);
         f32x4 lse4[4];
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) lse4[a4] = *reinterpret_cast<const f32x4*>(lsel + 8 * a4 + 4 * h);
-        sv = snext;
-        snext = product(tn);
+        if constexpr (AHEAD) {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) sv[kb] = snext[kb];
+          product(tn, snext);
+        } else {
+          product(tc, sv);
+        }
         // P = exp2(S*scale2 - lse2)
 #pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
+        for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) sv[4 * a4 + c] = exp2_fast(fmaf(sv[4 * a4 + c], scale2, -lse4[a4][c]));
+          for (int a4 = 0; a4 < 4; ++a4) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              sv[kb][4 * a4 + c] = exp2_fast(fmaf(sv[kb][4 * a4 + c], scale2, -lse4[a4][c]));
+          }
         }
       }
       if constexpr (PREV) {
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
 #pragma unroll
-          for (int db = 0; db < 4; ++db) acc[db] = mfma32(tr_a(tp + QT, lb, db, kh), pb[kh], acc[db]);
+          for (int db = 0; db < 4; ++db) {
+            const bf16x8 a = tr_a(tp + QT, lb, db, kh);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) accumulate(acc[kb][db], a, pb[kb][kh]);
+          }
         }
       }
       if constexpr (CUR) {
         // causal / past-the-end mask, only in the tiles that need it
         const int p0 = tile_p0(ctl);
-        if ((CAUSAL && p0 < kw0 + 31) || p0 + BQ > S) {
+        if ((CAUSAL && p0 < kw0 + 32 * KB - 1) || p0 + BQ > S) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int qpos = p0 + 8 * (r >> 2) + 4 * h + (r & 3);
-            sv[r] = ((CAUSAL && key > qpos) || qpos >= S) ? 0.f : sv[r];
+          for (int kb = 0; kb < KB; ++kb) {
+            const int key = kw0 + 32 * kb + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int qpos = p0 + 8 * (r >> 2) + 4 * h + (r & 3);
+              sv[kb][r] = ((CAUSAL && key > qpos) || qpos >= S) ? 0.f : sv[kb][r];
+            }
           }
         }
-        float* mb = mbox + (s & 1) * (MBOX / 4);
+        float* mb = mbox + (s & 1) * (KB * MBOX / 4);
 #pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-          f32x4 v4;
+        for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) v4[c] = sv[4 * a4 + c];
-          *reinterpret_cast<f32x4*>(mb + 256 * a4) = v4;
+          for (int a4 = 0; a4 < 4; ++a4) {
+            f32x4 v4;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c];
+            *reinterpret_cast<f32x4*>(mb + kb * (MBOX / 4) + 256 * a4) = v4;
+          }
+          pb[kb][0] = pack8(sv[kb], 0);
+          pb[kb][1] = pack8(sv[kb], 8);
+          // keep the conversion in this segment (it would otherwise sink to
+          // its first use, in the next one, where it runs before any product)
+          pin(pb[kb][0]);
+          pin(pb[kb][1]);
         }
-        pb[0] = pack8(sv, 0);
-        pb[1] = pack8(sv, 8);
-        // keep the conversion in this segment (it would otherwise sink to
-        // its first use, in the next one, where it runs before any product)
-        pin(pb[0]);
-        pin(pb[1]);
       }
     } else {
-      f32x16 dpn;
-      if constexpr (CUR) dpn = product(tc + QT);
+      f32x16 dpn[KB];
+      if constexpr (CUR && AHEAD) product(tc + QT, dpn);
       if constexpr (PREV2) {
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
 #pragma unroll
-          for (int db = 0; db < 4; ++db) acc[db] = mfma32(tr_a(tp2, lb, db, kh), sbp[kh], acc[db]);
+          for (int db = 0; db < 4; ++db) {
+            const bf16x8 a = tr_a(tp2, lb, db, kh);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) accumulate(acc[kb][db], a, sbp[kb][kh]);
+          }
         }
       }
       if constexpr (PREV) {
-        const float* mb = mbox + ((s - 1) & 1) * (MBOX / 4);
+        const float* mb = mbox + ((s - 1) & 1) * (KB * MBOX / 4);
         const float* dll = reinterpret_cast<const float*>(tp + 2 * QT) + BQ;
-        f32x16 dsv;
+        f32x4 dl4[4];
 #pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-          const f32x4 dl4 = *reinterpret_cast<const f32x4*>(dll + 8 * a4 + 4 * h);
-          const f32x4 p4 = *reinterpret_cast<const f32x4*>(mb + 256 * a4);
+        for (int a4 = 0; a4 < 4; ++a4) dl4[a4] = *reinterpret_cast<const f32x4*>(dll + 8 * a4 + 4 * h);
 #pragma unroll
-          for (int c = 0; c < 4; ++c) dsv[4 * a4 + c] = p4[c] * (dpp[4 * a4 + c] - dl4[c]);
+        for (int kb = 0; kb < KB; ++kb) {
+          f32x16 dsv;
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4) {
+            const f32x4 p4 = *reinterpret_cast<const f32x4*>(mb + kb * (MBOX / 4) + 256 * a4);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              dsv[4 * a4 + c] = p4[c] * (dpp[kb][4 * a4 + c] - dl4[a4][c]) * sm_scale;
+          }
+          sbp[kb][0] = pack8(dsv, 0);
+          sbp[kb][1] = pack8(dsv, 8);
+          // keep dS in this segment, under the products (see above)
+          pin(sbp[kb][0]);
+          pin(sbp[kb][1]);
         }
-        sbp[0] = pack8(dsv, 0);
-        sbp[1] = pack8(dsv, 8);
-        // keep dS in this segment, under the products (see above)
-        pin(sbp[0]);
-        pin(sbp[1]);
       }
-      if constexpr (CUR) dpp = dpn;
+      if constexpr (CUR) {
+        if constexpr (AHEAD) {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) dpp[kb] = dpn[kb];
+        } else {
+          product(tc + QT, dpp);
+        }
+      }
     }
     if constexpr (CUR) advance(ch, ctl);
     if constexpr (SYNC) {
       // tile s+2 must have landed; the newer prefetches stay in flight
+      // (2 * QPW copies per tile and wave, wave 0 one more)
       if (s + NSTAGE - 3 < n_u) {
-        if (w == 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (NSTAGE - 5)) : "memory");
-        else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (NSTAGE - 5)) : "memory");
+        if (w == 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"((2 * QPW + 1) * (NSTAGE - 5)) : "memory");
+        else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * QPW * (NSTAGE - 5)) : "memory");
       } else {
         wait_dma();
       }
@@ -653,8 +743,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // slot, and so every LDS offset, is a compile-time constant.
   using T = std::true_type;
   using F = std::false_type;
-  auto slot = [&](int c) { return smem + c * BUF; };
-  auto run = [&](auto role) {
+  auto slot = [&](int c) MM1_INLINE { return smem + c * BUF; };
+  auto run = [&](auto role) MM1_INLINE {
     const char* s0p = slot(0);
     const char* s1p = slot(1);
     if (n_u == 1) {
@@ -666,7 +756,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     segment(s1p, s0p, s0p, s0p, NSTAGE - 3, 0, role, T{}, F{}, F{}, T{});
     segment(slot(2), s1p, s0p, s0p, NSTAGE - 2, 1, role, T{}, T{}, F{}, T{});
     for (int b0 = 2; b0 < n_u; b0 += NSTAGE) {
-      unroll_while<0, NSTAGE>([&](auto j) {
+      unroll_while<0, NSTAGE>([&](auto j) MM1_INLINE {
         constexpr int C = (2 + decltype(j)::value) % NSTAGE;
         const int s = b0 + decltype(j)::value;
         if (s >= n_u) return false;
@@ -682,34 +772,41 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   };
   if (pwave) run(std::true_type{});
   else run(std::false_type{});
+  if constexpr (KB == 2) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) agpr_fence(acc[kb]);
+  }
 
-  if (key >= S) return;
   // D layout of dK^T / dV^T: register r of block db holds column
   // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
-  const float scale_out = pwave ? 1.f : sm_scale;
-  if (nparts == 1) {
-    __bf16* row = (pwave ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+  for (int kb = 0; kb < KB; ++kb) {
+    const int key = kw0 + 32 * kb + l32;
+    if (key >= S) continue;
+    if (nparts == 1 && !force_partials) {
+      __bf16* row = (pwave ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        bf16x4 o4;
+      for (int db = 0; db < 4; ++db) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) o4[c] = (__bf16)(acc[db][4 * a4 + c] * scale_out);
-        *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+        for (int a4 = 0; a4 < 4; ++a4) {
+          bf16x4 o4;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) o4[c] = (__bf16)acc[kb][db][4 * a4 + c];
+          *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+        }
       }
-    }
-  } else {
-    const long slot = (long)part * B * S * Hkv * HD;
-    float* row = (pwave ? ws_dv : ws_dk) + slot + ((long)(b * S + key) * Hkv + g) * HD;
+    } else {
+      const long slot = (long)part * B * S * Hkv * HD;
+      float* row = (pwave ? ws_dv : ws_dk) + slot + ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+      for (int db = 0; db < 4; ++db) {
 #pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        f32x4 o4;
+        for (int a4 = 0; a4 < 4; ++a4) {
+          f32x4 o4;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) o4[c] = acc[db][4 * a4 + c] * scale_out;
-        *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+          for (int c = 0; c < 4; ++c) o4[c] = acc[kb][db][4 * a4 + c];
+          *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+        }
       }
     }
   }
@@ -731,6 +828,8 @@ struct TailReduce {
   const float* ws_dv;
   __bf16* dk;
   __bf16* dv;
+  float* dk32;      // non-null: write the sums in fp32 here instead (fp32 backward)
+  float* dv32;
   long n;           // elements of one slot: B*S*Hkv*D
   int G;
   int n_red;        // 0: no reduction in this launch
@@ -767,6 +866,11 @@ __device__ __forceinline__ void reduce_at(const TailReduce& red, long i) {
     sk += *reinterpret_cast<const f32x4*>(red.ws_dk + (long)j * red.n + e);
     sv += *reinterpret_cast<const f32x4*>(red.ws_dv + (long)j * red.n + e);
   }
+  if (red.dk32) {
+    *reinterpret_cast<f32x4*>(red.dk32 + e) = sk;
+    *reinterpret_cast<f32x4*>(red.dv32 + e) = sv;
+    return;
+  }
   bf16x4 ok, ov;
 #pragma unroll
   for (int c = 0; c < 4; ++c) { ok[c] = (__bf16)sk[c]; ov[c] = (__bf16)sv[c]; }
@@ -794,11 +898,12 @@ __device__ __forceinline__ void tail_reduce(const TailReduce& red, int tid, int 
 // dQ: one workgroup per NW*32 packed query rows (32 per wave); K and V tiles
 // of 64 keys arrive by LDS DMA (row-major) in an NSTAGE-deep ring; K^T for
 // dQ^T = K^T dS^T is read transposed from the same K tile.
-template <int NW, int NSTAGE, bool CAUSAL>
+// F32OUT: dq is fp32 (the fp32 backward), else bf16.
+template <int NW, int NSTAGE, bool CAUSAL, bool F32OUT = false>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
-    __bf16* __restrict__ dq,
+    void* __restrict__ dq_out,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles, TailReduce red,
     const DispatchOrder ord) {
   constexpr int BM = NW * 32;
@@ -856,7 +961,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
       doreg[ks] = *reinterpret_cast<const bf16x8*>(dO + roff + 16 * ks + 8 * h);
     }
     const long li = ((long)b * H + g * G + hh) * S + qp;
-    lse_i = lse2[li];
+    // P sm_scale = exp2(s scale2 - (lse2 - log2 sm_scale)): dS comes out
+    // scaled, and is rounded to bf16 with the scale in it, as the reference's
+    lse_i = lse2[li] - log2f(sm_scale);
     dl_i = delta[li];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) { pin(qreg[ks]); pin(doreg[ks]); }
@@ -950,15 +1057,21 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
   }
 
   if (row_valid) {
-    __bf16* dst = dq + roff;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int a4 = 0; a4 < 4; ++a4) {
-        bf16x4 val;
+        if constexpr (F32OUT) {
+          f32x4 val;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) val[c] = (__bf16)(dqacc[db][4 * a4 + c] * sm_scale);
-        *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * a4 + 4 * h) = val;
+          for (int c = 0; c < 4; ++c) val[c] = dqacc[db][4 * a4 + c];
+          *reinterpret_cast<f32x4*>(static_cast<float*>(dq_out) + roff + 32 * db + 8 * a4 + 4 * h) = val;
+        } else {
+          bf16x4 val;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) val[c] = (__bf16)dqacc[db][4 * a4 + c];
+          *reinterpret_cast<bf16x4*>(static_cast<__bf16*>(dq_out) + roff + 32 * db + 8 * a4 + 4 * h) = val;
+        }
       }
     }
   }
@@ -999,7 +1112,7 @@ TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, 
   red.ws_dv = red.ws_dk + (long)G * red.n;
   red.dk = static_cast<__bf16*>(dk);
   red.dv = static_cast<__bf16*>(dv);
-  if (dkdv_variant == 0) {
+  if (dkdv_grouped(dkdv_variant)) {
     const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
     red.chunk_tiles = plan.L;
     red.max_chunks = plan.C;
@@ -1009,11 +1122,53 @@ TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, 
   return red;
 }
 
+// The pipelined dK/dV kernel for one tiling: GROUP (one workgroup per key
+// tile over the G heads of its KV group, chunked by dkdv_plan) or per head;
+// KB key blocks per wave.
+template <bool GROUP, int KB>
+static void launch_dkdv_pipe(const __bf16* qp, const __bf16* kp, const __bf16* vp, const __bf16* dop,
+                             const float* lse2, const float* delta, float* ws_dk, float* ws_dv,
+                             __bf16* dkp, __bf16* dvp, int B, int S, int H, int Hkv, bool causal,
+                             float scale2, float sm_scale, hipStream_t stream, int force_partials = 0) {
+  const int G = H / Hkv;
+  const bool ragged = S % 32 != 0;
+  const KeyTileOrder order = key_tile_order(B * H);
+  dim3 grid;
+  int L = 0, C = G;
+  const DispatchOrder* ord;
+  if constexpr (GROUP) {
+    const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
+    grid = dim3(plan.order.n ? plan.order.n : plan.n_items);
+    L = plan.L;
+    C = plan.C;
+    ord = &plan.order;
+  } else {
+    const int n_ktiles = (S + 127) / 128;
+    grid = dim3(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
+    ord = &dispatch_order(row_block_grid(0, B, S, H, Hkv), false);   // unused: default order
+  }
+  const dim3 block(512 / KB);
+#define MM1_DKDV_PIPE(CS, RG)                                                                      \
+  hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, GROUP, RG, KB>), grid, block, 0, stream, qp, kp, vp, \
+                     dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale,      \
+                     order, L, C, *ord, force_partials)
+  if (causal) {
+    if (ragged) MM1_DKDV_PIPE(true, true);
+    else MM1_DKDV_PIPE(true, false);
+  } else {
+    if (ragged) MM1_DKDV_PIPE(false, true);
+    else MM1_DKDV_PIPE(false, false);
+  }
+#undef MM1_DKDV_PIPE
+}
+
 // variant: 0 = attn_dkdv_pipe_kernel over the whole GQA group per key tile
-//              (chunked by dkdv_plan),
-//          1 = attn_dkdv_pipe_kernel (7-slot ring of 32-query tiles, one
-//              workgroup per (key tile, query head)),
-//          2 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries).
+//              (chunked by dkdv_plan), 8 waves x 32 keys,
+//          1 = attn_dkdv_pipe_kernel, one workgroup per (key tile, query
+//              head), 8 waves x 32 keys,
+//          2 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries),
+//          3 = as 0 with 4 waves x 64 keys (one wave per SIMD),
+//          4 = as 1 with 4 waves x 64 keys.
 hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
                            const float* lse2, const float* delta, void* dk, void* dv,
                            void* workspace, int B, int S, int H, int Hkv, bool causal,
@@ -1029,48 +1184,34 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
   auto dop = static_cast<const __bf16*>(dO);
   auto dkp = static_cast<__bf16*>(dk);
   auto dvp = static_cast<__bf16*>(dv);
-  const int n_ktiles = (S + 127) / 128;
-  const KeyTileOrder order = key_tile_order(B * H);
-  const bool ragged = S % 32 != 0;
-  if (variant == 0) {
-    const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
-    const dim3 grid(plan.order.n ? plan.order.n : plan.n_items);
-#define MM1_DKDV_GROUP(CS, RG)                                                                  \
-  hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, true, RG>), grid, dim3(512), 0, stream, qp, kp, vp, \
-                     dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale,   \
-                     order, plan.L, plan.C, plan.order)
-    if (causal) {
-      if (ragged) MM1_DKDV_GROUP(true, true);
-      else MM1_DKDV_GROUP(true, false);
-    } else {
-      if (ragged) MM1_DKDV_GROUP(false, true);
-      else MM1_DKDV_GROUP(false, false);
+  switch (variant) {
+    case 0:
+      launch_dkdv_pipe<true, 1>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
+                                scale2, sm_scale, stream);
+      break;
+    case 1:
+      launch_dkdv_pipe<false, 1>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
+                                 scale2, sm_scale, stream);
+      break;
+    case 3:
+      launch_dkdv_pipe<true, 2>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
+                                scale2, sm_scale, stream);
+      break;
+    case 4:
+      launch_dkdv_pipe<false, 2>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
+                                 scale2, sm_scale, stream);
+      break;
+    default: {
+      const KeyTileOrder order = key_tile_order(B * H);
+      const int n_ktiles = (S + 127) / 128;
+      const dim3 grid(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
+      if (causal)
+        hipLaunchKernelGGL(attn_dkdv_kernel<true>, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta,
+                           ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, order);
+      else
+        hipLaunchKernelGGL(attn_dkdv_kernel<false>, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta,
+                           ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, order);
     }
-#undef MM1_DKDV_GROUP
-    return hipGetLastError();
-  }
-  const dim3 grid(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
-  if (variant == 2) {
-#define MM1_DKDV_PAIRED(KERNEL)                                                               \
-  hipLaunchKernelGGL(KERNEL, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta, ws_dk, \
-                     ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, order)
-    if (causal) MM1_DKDV_PAIRED(attn_dkdv_kernel<true>);
-    else MM1_DKDV_PAIRED(attn_dkdv_kernel<false>);
-#undef MM1_DKDV_PAIRED
-  } else {
-    const DispatchOrder& none = dispatch_order(row_block_grid(0, B, S, H, Hkv), false);
-#define MM1_DKDV_HEAD(CS, RG)                                                                   \
-  hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, false, RG>), grid, dim3(512), 0, stream, qp, kp, vp, \
-                     dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale,    \
-                     order, 0, G, none)
-    if (causal) {
-      if (ragged) MM1_DKDV_HEAD(true, true);
-      else MM1_DKDV_HEAD(true, false);
-    } else {
-      if (ragged) MM1_DKDV_HEAD(false, true);
-      else MM1_DKDV_HEAD(false, false);
-    }
-#undef MM1_DKDV_HEAD
   }
   return hipGetLastError();
 }
@@ -1084,9 +1225,9 @@ hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, i
   return hipGetLastError();
 }
 
-template <int NW, int NSTAGE>
+template <int NW, int NSTAGE, bool F32OUT = false>
 static void launch_dq_t(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* dO,
-                        const float* lse2, const float* delta, __bf16* dq, int B, int S, int H,
+                        const float* lse2, const float* delta, void* dq, int B, int S, int H,
                         int Hkv, bool causal, float scale2, float sm_scale, TailReduce red,
                         const DispatchOrder& ord, hipStream_t stream) {
   const int G = H / Hkv;
@@ -1096,11 +1237,11 @@ static void launch_dq_t(const __bf16* q, const __bf16* k, const __bf16* v, const
   if (red.n_red > 0) red.n_red = min(red.n_red, n_blocks);
   dim3 grid(n_blocks), block(NW * 64);
   if (causal)
-    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, true>), grid, block, 0, stream, q, k, v, dO, lse2, delta, dq,
-                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
+    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, true, F32OUT>), grid, block, 0, stream, q, k, v, dO, lse2,
+                       delta, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
   else
-    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, false>), grid, block, 0, stream, q, k, v, dO, lse2, delta, dq,
-                       B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
+    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, false, F32OUT>), grid, block, 0, stream, q, k, v, dO, lse2,
+                       delta, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
 }
 
 // variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
@@ -1117,14 +1258,56 @@ hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void
   auto kp = static_cast<const __bf16*>(k);
   auto vp = static_cast<const __bf16*>(v);
   auto dop = static_cast<const __bf16*>(dO);
-  auto dqp = static_cast<__bf16*>(dq);
   // with n_red = 1 << 30 every workgroup of the grid takes a slice
   const TailReduce red = make_reduce(workspace, dk, dv, B, S, H, Hkv, causal, dkdv_variant);
   const DispatchOrder& ord = dispatch_order(dq_grid(variant, B, S, H, Hkv), causal);
   if (variant == 1)
-    launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
+    launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dq, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
   else
-    launch_dq_t<4, 2>(qp, kp, vp, dop, lse2, delta, dqp, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
+    launch_dq_t<4, 2>(qp, kp, vp, dop, lse2, delta, dq, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
+  return hipGetLastError();
+}
+
+// Bytes of fp32 scratch of the fp32 backward: G >= 1 slots of dK and dV
+// partials (the per-head layout, also for G == 1).
+size_t bwd_f32_workspace_bytes(int B, int S, int H, int Hkv) {
+  return (size_t)2 * (H / Hkv) * B * S * Hkv * HD * sizeof(float);
+}
+
+// fp32 gradients: the per-head dK/dV tiling with fp32 partials for every
+// head, their sum in slot order written in fp32, and dQ written in fp32 --
+// the values the bf16 backward rounds (up to the order of the fp32 sums of
+// the grouped tiling), as the reference kernel's fp32 dQ / dK / dV buffers
+// hold them before its casts.
+hipError_t launch_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
+                          const float* lse2, const float* delta, float* dq, float* dk, float* dv,
+                          void* workspace, int B, int S, int H, int Hkv, bool causal, float sm_scale,
+                          hipStream_t stream) {
+  const int G = H / Hkv;
+  const float scale2 = sm_scale * 1.4426950408889634f;
+  auto qp = static_cast<const __bf16*>(q);
+  auto kp = static_cast<const __bf16*>(k);
+  auto vp = static_cast<const __bf16*>(v);
+  auto dop = static_cast<const __bf16*>(dO);
+  const long n_kv = (long)B * S * Hkv * HD;
+  float* ws_dk = static_cast<float*>(workspace);
+  float* ws_dv = ws_dk + (long)G * n_kv;
+  launch_dkdv_pipe<false, 1>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, nullptr, nullptr, B, S, H, Hkv, causal,
+                             scale2, sm_scale, stream, 1);
+  TailReduce red{};
+  red.ws_dk = ws_dk;
+  red.ws_dv = ws_dv;
+  red.dk32 = dk;
+  red.dv32 = dv;
+  red.n = n_kv;
+  red.G = G;
+  red.S = S;
+  red.Hkv = Hkv;
+  red.causal = causal ? 1 : 0;
+  hipLaunchKernelGGL(attn_dkdv_reduce_kernel, dim3((unsigned)((n_kv / 4 + 255) / 256)), dim3(256), 0, stream, red);
+  TailReduce none{};
+  launch_dq_t<4, 2, true>(qp, kp, vp, dop, lse2, delta, dq, B, S, H, Hkv, causal, scale2, sm_scale, none,
+                          dispatch_order(dq_grid(0, B, S, H, Hkv), causal), stream);
   return hipGetLastError();
 }
 

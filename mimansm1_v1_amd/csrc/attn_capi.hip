@@ -3,6 +3,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "../../include/mm1_attn.h"
 #include "../../include/mm1_swiglu.h"
 #include "../../include/mm1_lm_head.h"
@@ -13,6 +15,8 @@ namespace mm1 {
 hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
                       int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                       hipStream_t stream);
+hipError_t launch_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2,
+                          int B, int S, int H, int Hkv, bool causal, float sm_scale, hipStream_t stream);
 hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int S, int H,
                         hipStream_t stream);
 size_t bwd_workspace_bytes(int B, int S, int H, int Hkv);
@@ -27,6 +31,11 @@ hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void
                          const void* workspace, void* dk, void* dv,
                          int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                          int dkdv_variant, hipStream_t stream);
+size_t bwd_f32_workspace_bytes(int B, int S, int H, int Hkv);
+hipError_t launch_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
+                          const float* lse2, const float* delta, float* dq, float* dk, float* dv,
+                          void* workspace, int B, int S, int H, int Hkv, bool causal, float sm_scale,
+                          hipStream_t stream);
 size_t qknorm_bwd_workspace_bytes();
 hipError_t launch_qknorm_fwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
                              const float* sin_t, void* q, void* k, void* v, int B, int S, int H, int Hkv,
@@ -75,6 +84,8 @@ const char* const kDkdvTiles[] = {
     "block_M=128 block_N=32 waves=8 stages=7 schedule=group",
     "block_M=128 block_N=32 waves=8 stages=7 schedule=pipelined",
     "block_M=128 block_N=64 waves=8 stages=3 schedule=paired",
+    "block_M=128 block_N=32 waves=4 stages=7 schedule=group",
+    "block_M=128 block_N=32 waves=4 stages=7 schedule=pipelined",
 };
 const char* const kDqTiles[] = {
     "block_M=128 block_N=64 waves=4 stages=2 schedule=ring",
@@ -93,17 +104,67 @@ int tile_count(int kind) {
   }
 }
 
-const char* const kTileEnv[] = {"MM1_FWD_VARIANT", "MM1_DKDV_VARIANT", "MM1_DQ_VARIANT"};
-
-// The tiling to launch: `tiles` itself when >= 0, else the default -- the
-// kind's environment variable if set (read on every call, so a process can
-// switch between launches), otherwise 0.  -1 when out of range.
+// The tiling to launch: `tiles` itself when >= 0, index 0 (the default) for
+// -1; -1 when out of range.
 int pick_tiles(int kind, int tiles) {
-  if (tiles == -1) {
-    const char* e = getenv(kTileEnv[kind]);
-    tiles = e ? atoi(e) : 0;
-  }
+  if (tiles == -1) tiles = 0;
   return (tiles >= 0 && tiles < tile_count(kind)) ? tiles : -1;
+}
+
+// ---------------------------------------------------------------------------
+// Layout of the dK/dV partial sums a workspace holds.  mm1_attn_bwd_dkdv*
+// records, per workspace address, the layout its launch wrote; the calls that
+// sum the partials (mm1_attn_bwd_dkdv_reduce*, mm1_attn_bwd_dq_reduce*) work
+// out the layout their own tiling and shape read and refuse (MM1_E_LAYOUT) a
+// workspace whose record differs or is missing, instead of summing the wrong
+// slots.  The record is host state only (nothing is written to the device);
+// it holds the last few workspaces in use.
+struct WsLayout {
+  const void* ws;
+  int grouped;                 // chunked (grouped tilings) or one slot per head
+  int L, C, split_keys;        // grouped: the chunk plan (dkdv_plan)
+  int B, S, H, Hkv, causal;
+  bool same(const WsLayout& o) const {
+    return grouped == o.grouped && L == o.L && C == o.C && split_keys == o.split_keys && B == o.B &&
+           S == o.S && H == o.H && Hkv == o.Hkv && causal == o.causal;
+  }
+};
+
+WsLayout layout_of(const void* ws, int dkdv_variant, int B, int S, int H, int Hkv, bool causal) {
+  WsLayout l{};
+  l.ws = ws;
+  l.B = B, l.S = S, l.H = H, l.Hkv = Hkv;
+  if (mm1::dkdv_grouped(dkdv_variant)) {
+    const mm1::DkdvPlan& plan = mm1::dkdv_plan(B, S, H, Hkv, causal);
+    l.grouped = 1;
+    l.L = plan.L, l.C = plan.C, l.split_keys = plan.split_keys;
+    l.causal = causal ? 1 : 0;
+  }
+  return l;
+}
+
+constexpr int kLayoutSlots = 64;
+std::mutex g_layout_mu;
+WsLayout g_layouts[kLayoutSlots];
+int g_layout_next = 0;
+
+void record_layout(const WsLayout& l) {
+  std::lock_guard<std::mutex> lock(g_layout_mu);
+  for (WsLayout& e : g_layouts) {
+    if (e.ws == l.ws) {
+      e = l;
+      return;
+    }
+  }
+  g_layouts[g_layout_next] = l;
+  g_layout_next = (g_layout_next + 1) % kLayoutSlots;
+}
+
+bool layout_matches(const WsLayout& want) {
+  std::lock_guard<std::mutex> lock(g_layout_mu);
+  for (const WsLayout& e : g_layouts)
+    if (e.ws == want.ws) return e.same(want);
+  return false;
 }
 
 int from_hip(hipError_t e) { return e == hipSuccess ? MM1_OK : static_cast<int>(e); }
@@ -132,6 +193,17 @@ int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                  void* stream) {
   return mm1_attn_fwd_tiles(q, k, v, o, lse2, B, S, H, Hkv, D, causal, sm_scale, -1, stream);
+}
+
+int mm1_attn_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2,
+                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream) {
+  if (!q || !k || !v || !o || !lse2) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MM1_E_ALIGN;
+  return from_hip(mm1::launch_fwd_f32(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale,
+                                      static_cast<hipStream_t>(stream)));
 }
 
 int mm1_attn_tile_count(int kind) { return tile_count(kind); }
@@ -175,9 +247,11 @@ static int bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
     return MM1_E_ALIGN;
   const int variant = pick_tiles(MM1_TILES_DKDV, tiles);
   if (variant < 0) return MM1_E_TILES;
-  return from_hip(mm1::launch_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, need > 0 ? workspace : nullptr,
-                                       B, S, H, Hkv, causal != 0, sm_scale, variant,
-                                       static_cast<hipStream_t>(stream)));
+  rc = from_hip(mm1::launch_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, need > 0 ? workspace : nullptr,
+                                     B, S, H, Hkv, causal != 0, sm_scale, variant,
+                                     static_cast<hipStream_t>(stream)));
+  if (rc == MM1_OK && need > 0) record_layout(layout_of(workspace, variant, B, S, H, Hkv, causal != 0));
+  return rc;
 }
 
 // dq, and with dk/dv the group sum of the dK/dV partials in the same launch.
@@ -199,10 +273,37 @@ static int bwd_dq(const void* q, const void* k, const void* v, const void* dO,
   const int variant = pick_tiles(MM1_TILES_DQ, tiles);
   const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, dkdv_tiles);
   if (variant < 0 || dkdv_variant < 0) return MM1_E_TILES;
+  if (need > 0 && !layout_matches(layout_of(workspace, dkdv_variant, B, S, H, Hkv, causal != 0)))
+    return MM1_E_LAYOUT;
   return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, need > 0 ? workspace : nullptr,
                                      reduce ? dk : nullptr, reduce ? dv : nullptr,
                                      B, S, H, Hkv, causal != 0, sm_scale, variant, dkdv_variant,
                                      static_cast<hipStream_t>(stream)));
+}
+
+static int bwd_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
+                      int B, int S, int H, int Hkv, int D, int causal, int dkdv_tiles, void* stream) {
+  if (!dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, dkdv_tiles);
+  if (dkdv_variant < 0) return MM1_E_TILES;
+  const size_t need = mm1::bwd_workspace_bytes(B, S, H, Hkv);
+  if (need == 0) return MM1_OK;
+  if (!workspace || workspace_bytes < need) return MM1_E_WORKSPACE;
+  if (!aligned16(workspace) || !aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
+  if (!layout_matches(layout_of(workspace, dkdv_variant, B, S, H, Hkv, causal != 0))) return MM1_E_LAYOUT;
+  return from_hip(mm1::launch_bwd_reduce(workspace, dk, dv, B, S, H, Hkv, causal != 0, dkdv_variant,
+                                         static_cast<hipStream_t>(stream)));
+}
+
+int mm1_attn_bwd_dkdv_tiles(const void* q, const void* k, const void* v, const void* dO,
+                            const float* lse2, const float* delta, void* dk, void* dv,
+                            void* workspace, size_t workspace_bytes,
+                            int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                            int dkdv_tiles, void* stream) {
+  return bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes, B, S, H, Hkv, D,
+                  causal, sm_scale, dkdv_tiles, stream);
 }
 
 int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
@@ -214,19 +315,23 @@ int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* d
                   causal, sm_scale, -1, stream);
 }
 
+int mm1_attn_bwd_dkdv_reduce_tiles(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
+                                   int B, int S, int H, int Hkv, int D, int causal, int dkdv_tiles,
+                                   void* stream) {
+  return bwd_reduce(workspace, workspace_bytes, dk, dv, B, S, H, Hkv, D, causal, dkdv_tiles, stream);
+}
+
 int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
                              int B, int S, int H, int Hkv, int D, int causal, void* stream) {
-  if (!dk || !dv) return MM1_E_NULL;
-  int rc = check_shape(B, S, H, Hkv, D);
-  if (rc) return rc;
-  const size_t need = mm1::bwd_workspace_bytes(B, S, H, Hkv);
-  if (need == 0) return MM1_OK;
-  if (!workspace || workspace_bytes < need) return MM1_E_WORKSPACE;
-  if (!aligned16(workspace) || !aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
-  const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, -1);
-  if (dkdv_variant < 0) return MM1_E_TILES;
-  return from_hip(mm1::launch_bwd_reduce(workspace, dk, dv, B, S, H, Hkv, causal != 0, dkdv_variant,
-                                         static_cast<hipStream_t>(stream)));
+  return bwd_reduce(workspace, workspace_bytes, dk, dv, B, S, H, Hkv, D, causal, -1, stream);
+}
+
+int mm1_attn_bwd_dq_tiles(const void* q, const void* k, const void* v, const void* dO,
+                          const float* lse2, const float* delta, void* dq,
+                          int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                          int dq_tiles, void* stream) {
+  return bwd_dq(q, k, v, dO, lse2, delta, dq, nullptr, nullptr, nullptr, 0, false, B, S, H, Hkv, D,
+                causal, sm_scale, dq_tiles, -1, stream);
 }
 
 int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
@@ -235,6 +340,15 @@ int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
                     void* stream) {
   return bwd_dq(q, k, v, dO, lse2, delta, dq, nullptr, nullptr, nullptr, 0, false, B, S, H, Hkv, D,
                 causal, sm_scale, -1, -1, stream);
+}
+
+int mm1_attn_bwd_dq_reduce_tiles(const void* q, const void* k, const void* v, const void* dO,
+                                 const float* lse2, const float* delta, void* dq, void* dk, void* dv,
+                                 const void* workspace, size_t workspace_bytes,
+                                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                                 int dkdv_tiles, int dq_tiles, void* stream) {
+  return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
+                D, causal, sm_scale, dq_tiles, dkdv_tiles, stream);
 }
 
 int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const void* dO,
@@ -264,6 +378,27 @@ int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* 
                 D, causal, sm_scale, dq_tiles, dkdv_tiles, stream);
 }
 
+size_t mm1_attn_bwd_f32_workspace_size(int B, int S, int H, int Hkv, int D) {
+  if (check_shape(B, S, H, Hkv, D) != MM1_OK) return 0;
+  return mm1::bwd_f32_workspace_bytes(B, S, H, Hkv);
+}
+
+int mm1_attn_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
+                     const float* lse2, const float* delta, float* dq, float* dk, float* dv,
+                     void* workspace, size_t workspace_bytes,
+                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream) {
+  if (!q || !k || !v || !dO || !lse2 || !delta || !dq || !dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
+  if (!workspace || workspace_bytes < mm1::bwd_f32_workspace_bytes(B, S, H, Hkv)) return MM1_E_WORKSPACE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) || !aligned16(dk) ||
+      !aligned16(dv) || !aligned16(workspace))
+    return MM1_E_ALIGN;
+  return from_hip(mm1::launch_bwd_f32(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, B, S, H, Hkv,
+                                      causal != 0, sm_scale, static_cast<hipStream_t>(stream)));
+}
+
 int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, int causal, int cus,
                             unsigned short* out, int cap) {
   if (kind < MM1_TILES_FWD || kind > MM1_TILES_DQ) return MM1_E_TILES;
@@ -272,7 +407,7 @@ int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, i
   if (const int rc = check_shape(B, S, H, Hkv, mm1::HD)) return rc;
   if (cus < 1 || cap < 0) return MM1_E_SHAPE;
   if (cap > 0 && !out) return MM1_E_NULL;
-  if (kind == MM1_TILES_DKDV && variant != 0) return 0;   // per-head grids: default order
+  if (kind == MM1_TILES_DKDV && !mm1::dkdv_grouped(variant)) return 0;   // per-head grids: default order
   const mm1::DispatchOrder& ord =
       kind == MM1_TILES_DKDV ? mm1::dkdv_plan_for(B, S, H, Hkv, causal != 0, cus).order
       : kind == MM1_TILES_DQ ? mm1::dispatch_order_for(mm1::dq_grid(variant, B, S, H, Hkv), causal != 0, cus)
@@ -428,6 +563,9 @@ const char* mm1_attn_strerror(int code) {
     case MM1_E_SCALE: return "mm1_attn: sm_scale must be a positive finite number";
     case MM1_E_ALIGN: return "mm1_attn: tensor pointers must be 16-byte aligned";
     case MM1_E_TILES: return "mm1_attn: tiling index out of range (see mm1_attn_tile_count)";
+    case MM1_E_LAYOUT:
+      return "mm1_attn: the workspace holds no dK/dV partial sums of this shape and dK/dV tiling "
+             "(run mm1_attn_bwd_dkdv with the same arguments first)";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -31,10 +31,11 @@ namespace mm1 {
 constexpr float kRescaleThreshold = 8.0f;   // log2 units
 
 // NW waves x 32 packed query rows per workgroup; NSTAGE-deep K/V ring.
-template <int NW, int NSTAGE, bool CAUSAL>
+// F32OUT: O is written in fp32 (the values the bf16 output rounds).
+template <int NW, int NSTAGE, bool CAUSAL, bool F32OUT = false>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    __bf16* __restrict__ o, float* __restrict__ lse2,
+    void* __restrict__ o_out, float* __restrict__ lse2,
     int B, int S, int H, int Hkv, int G, float scale2, int n_tiles, const DispatchOrder ord) {
   constexpr int BM = NW * 32;     // packed rows per workgroup
   constexpr int BN = TILE_ROWS;   // keys per iteration
@@ -183,15 +184,22 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.f / l_tot;
   if (rr < R) {
-    __bf16* dst = o + ((long)(b * S + qpos) * H + g * G + hq) * HD;
+    const long row = ((long)(b * S + qpos) * H + g * G + hq) * HD;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int a4 = 0; a4 < 4; ++a4) {
-        bf16x4 val;
+        if constexpr (F32OUT) {
+          f32x4 val;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) val[c] = (__bf16)(oacc[db][4 * a4 + c] * inv);
-        *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * a4 + 4 * h) = val;
+          for (int c = 0; c < 4; ++c) val[c] = oacc[db][4 * a4 + c] * inv;
+          *reinterpret_cast<f32x4*>(static_cast<float*>(o_out) + row + 32 * db + 8 * a4 + 4 * h) = val;
+        } else {
+          bf16x4 val;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) val[c] = (__bf16)(oacc[db][4 * a4 + c] * inv);
+          *reinterpret_cast<bf16x4*>(static_cast<__bf16*>(o_out) + row + 32 * db + 8 * a4 + 4 * h) = val;
+        }
       }
     }
     if (h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
@@ -409,8 +417,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   }
 }
 
-template <int NW, int NSTAGE>
-static void launch_fwd_t(const __bf16* q, const __bf16* k, const __bf16* v, __bf16* o, float* lse2,
+template <int NW, int NSTAGE, bool F32OUT = false>
+static void launch_fwd_t(const __bf16* q, const __bf16* k, const __bf16* v, void* o, float* lse2,
                          int B, int S, int H, int Hkv, bool causal, float scale2, const DispatchOrder& ord,
                          hipStream_t stream) {
   const int G = H / Hkv;
@@ -418,9 +426,23 @@ static void launch_fwd_t(const __bf16* q, const __bf16* k, const __bf16* v, __bf
   const int n_tiles = (G * S + BM - 1) / BM;
   dim3 grid(ord.n ? ord.n : n_tiles * B * Hkv), block(NW * 64);
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, true>), grid, block, 0, stream, q, k, v, o, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
+    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, true, F32OUT>), grid, block, 0, stream, q, k, v, o, lse2, B, S,
+                       H, Hkv, G, scale2, n_tiles, ord);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, false>), grid, block, 0, stream, q, k, v, o, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
+    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, false, F32OUT>), grid, block, 0, stream, q, k, v, o, lse2, B, S,
+                       H, Hkv, G, scale2, n_tiles, ord);
+}
+
+// The forward with fp32 O (the 4-wave ring tiling): the values a bf16
+// forward rounds, for parity checks of O where one bf16 half-ulp of |O|
+// already exceeds the tolerance.
+hipError_t launch_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2,
+                          int B, int S, int H, int Hkv, bool causal, float sm_scale, hipStream_t stream) {
+  const float scale2 = sm_scale * 1.4426950408889634f;
+  launch_fwd_t<4, 2, true>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
+                           static_cast<const __bf16*>(v), o, lse2, B, S, H, Hkv, causal, scale2,
+                           dispatch_order(row_block_grid(1, B, S, H, Hkv), causal), stream);
+  return hipGetLastError();
 }
 
 // variant: 0 = attn_fwd_pp_kernel (8 waves, two groups half a tile apart),
@@ -433,20 +455,19 @@ hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, floa
   auto qp = static_cast<const __bf16*>(q);
   auto kp = static_cast<const __bf16*>(k);
   auto vp = static_cast<const __bf16*>(v);
-  auto op = static_cast<__bf16*>(o);
   const DispatchOrder& ord = dispatch_order(row_block_grid(variant, B, S, H, Hkv), causal);
   if (variant == 0) {
     const int G = H / Hkv;
     const int n_tiles = (G * S + 255) / 256;
     dim3 grid(ord.n ? ord.n : n_tiles * B * Hkv), block(512);
     if (causal)
-      hipLaunchKernelGGL(attn_fwd_pp_kernel<true>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
+      hipLaunchKernelGGL(attn_fwd_pp_kernel<true>, grid, block, 0, stream, qp, kp, vp, static_cast<__bf16*>(o), lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
     else
-      hipLaunchKernelGGL(attn_fwd_pp_kernel<false>, grid, block, 0, stream, qp, kp, vp, op, lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
+      hipLaunchKernelGGL(attn_fwd_pp_kernel<false>, grid, block, 0, stream, qp, kp, vp, static_cast<__bf16*>(o), lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
   } else if (variant == 2)
-    launch_fwd_t<8, 3>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
+    launch_fwd_t<8, 3>(qp, kp, vp, o, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
   else
-    launch_fwd_t<4, 2>(qp, kp, vp, op, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
+    launch_fwd_t<4, 2>(qp, kp, vp, o, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
   return hipGetLastError();
 }
 

@@ -101,6 +101,11 @@ __host__ __device__ inline int dkdv_chunks(int len, int L, int C) {
   return n < 1 ? 1 : (n > C ? C : n);
 }
 
+// dK/dV tilings (mm1_attn_tile_desc order) that run the grouped grid and so
+// leave the chunked partial-sum layout: 0 (8 waves x 32 keys) and 3 (4 waves
+// x 64 keys).
+__host__ __device__ inline bool dkdv_grouped(int variant) { return variant == 0 || variant == 3; }
+
 struct DkdvPlan {
   int L;            // target query tiles per chunk
   int C;            // chunks per key tile at most (<= G: the workspace holds G slots)

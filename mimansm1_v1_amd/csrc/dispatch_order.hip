@@ -229,7 +229,7 @@ std::vector<int> dkdv_costs(int B, int S, int G, int Hkv, bool causal, int L, in
 // Chunk length: the candidate (fractions of the per-CU share of the work,
 // and no split at all) whose order the dispatch model rates fastest; on a
 // tie the one with fewer split key tiles.
-void build_dkdv(int B, int S, int H, int Hkv, bool causal, int cus, int forced_L, DkdvPlan& plan) {
+void build_dkdv(int B, int S, int H, int Hkv, bool causal, int cus, DkdvPlan& plan) {
   const int G = H / Hkv, n_kt = (S + 127) / 128, nbg = B * Hkv;
   const int C = G;
   long total = 0;
@@ -242,7 +242,6 @@ void build_dkdv(int B, int S, int H, int Hkv, bool causal, int cus, int forced_L
   const long share = std::max<long>(1, (total + cus - 1) / std::max(1, cus));
   const int slots_per_se = std::max(1, cus / (8 * kSe));
   std::vector<long> cands = {share / 3, share / 2, (2 * share) / 3, share, (4 * share) / 3, longest};
-  if (forced_L > 0) cands = {forced_L};
   long best_span = -1;
   plan.C = C;
   for (long cand : cands) {
@@ -323,20 +322,19 @@ const DispatchOrder& dispatch_order(const GridShape& g, bool causal) {
 }
 
 const DkdvPlan& dkdv_plan_for(int B, int S, int H, int Hkv, bool causal, int cus) {
+  // The chunk length (and so the partial-sum layout) depends on the shape and
+  // the CU count only; the dispatch-order switch changes which launch slot
+  // runs which item, not the items.
   const bool ordered = order_enabled();
-  // MM1_DKDV_CHUNK=<tiles>: a fixed chunk length instead of the modelled
-  // choice (tuning experiments; read per call)
-  const char* e = getenv("MM1_DKDV_CHUNK");
-  const int forced_L = e ? std::max(0, atoi(e)) : 0;
-  using Key = std::tuple<int, int, int, int, bool, int, bool, int>;
-  const Key key{B, S, H, Hkv, causal, cus, ordered, forced_L};
+  using Key = std::tuple<int, int, int, int, bool, int, bool>;
+  const Key key{B, S, H, Hkv, causal, cus, ordered};
   static std::mutex mu;
   static std::map<Key, std::unique_ptr<DkdvPlan>> cache;
   std::lock_guard<std::mutex> lock(mu);
   auto it = cache.find(key);
   if (it == cache.end()) {
     auto plan = std::make_unique<DkdvPlan>();
-    build_dkdv(B, S, H, Hkv, causal, std::max(1, cus), forced_L, *plan);
+    build_dkdv(B, S, H, Hkv, causal, std::max(1, cus), *plan);
     if (!ordered) plan->order.n = 0;
     it = cache.emplace(key, std::move(plan)).first;
   }

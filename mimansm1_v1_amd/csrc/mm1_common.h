@@ -37,6 +37,9 @@
 #define MM1_FWD_PREFETCH 1
 #endif
 
+// Forces a lambda or helper inline (large kernel bodies otherwise get real calls).
+#define MM1_INLINE __attribute__((always_inline))
+
 namespace mm1 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -53,6 +56,27 @@ constexpr int TILE_BYTES = TILE_ROWS * HD * 2;   // 16 KiB
 
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// acc += A B with the accumulator held in AGPRs (a 16-register accumulator
+// tuple the compiler keeps in the accumulation registers for the whole loop).
+// For kernels with one wave per SIMD whose long-lived accumulators exceed the
+// 256 architectural VGPRs: the compiler's own MFMAs (built with VGPR-form
+// MFMA selection) keep the short-lived products in VGPRs, where the VALU
+// reads them.  Dependent accumulations into the same tuple are interlocked
+// by the hardware, as for the compiler's own chains.  The compiler does not
+// see this as an MFMA, so before the accumulators are read by any other
+// instruction the caller runs agpr_fence() (the MFMA write -> read wait states).
+__device__ __forceinline__ void mfma32_acc(const bf16x8& a, const bf16x8& b, f32x16& acc) {
+  __asm__("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// 32 wait states, ordered before every later use of the fenced accumulators.
+template <int N>
+__device__ __forceinline__ void agpr_fence(f32x16 (&acc)[N]) {
+  __asm__ volatile("s_nop 15\n\ts_nop 15" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) __asm__ volatile("" : "+a"(acc[i]));
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -25,7 +25,10 @@ def load():
         lib = ctypes.CDLL(str(LIB))
         dp, ci, cd = ctypes.POINTER(ctypes.c_double), ctypes.c_int, ctypes.c_double
         lib.brute_attn_fwd.argtypes = [dp] * 5 + [ci] * 6 + [cd]
-        lib.brute_attn_bwd.argtypes = [dp] * 7 + [ci] * 6 + [cd]
+        lib.brute_attn_bwd.argtypes = [dp] * 8 + [ci] * 6 + [cd]
+        lib.brute_attn_bwd_emul.argtypes = [dp] * 8 + [ci] * 6 + [cd]
+        lib.brute_bf16.argtypes = [cd]
+        lib.brute_bf16.restype = cd
         _lib = lib
     return _lib
 
@@ -47,12 +50,31 @@ def fwd(q, k, v, causal, sm_scale=None):
     return o, lse
 
 
-def bwd(q, k, v, do, causal, sm_scale=None):
+def _bwd(fn, q, k, v, do, causal, sm_scale):
     q, k, v, do = (np.ascontiguousarray(x, dtype=np.float64) for x in (q, k, v, do))
     B, S, H, D = q.shape
     Hkv = k.shape[2]
     sm_scale = D ** -0.5 if sm_scale is None else sm_scale
     dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
-    load().brute_attn_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(dq), _ptr(dk), _ptr(dv),
-                          B, S, H, Hkv, D, int(causal), sm_scale)
-    return dq, dk, dv
+    delta = np.zeros((B, H, S))
+    fn(_ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
+       B, S, H, Hkv, D, int(causal), sm_scale)
+    return dq, dk, dv, delta
+
+
+def bwd(q, k, v, do, causal, sm_scale=None, with_delta=False):
+    """Exact fp64 backward -> (dq, dk, dv[, delta]); delta_i = sum_j P_ij dP_ij."""
+    dq, dk, dv, delta = _bwd(load().brute_attn_bwd, q, k, v, do, causal, sm_scale)
+    return (dq, dk, dv, delta) if with_delta else (dq, dk, dv)
+
+
+def bwd_emul(q, k, v, do, causal, sm_scale=None):
+    """fp64 backward with the reference kernel's bf16 rounding points (P before
+    dV, P (dP - Delta) sm_scale before dK / dQ, Delta from the bf16 forward
+    output) -> (dq, dk, dv, delta)."""
+    return _bwd(load().brute_attn_bwd_emul, q, k, v, do, causal, sm_scale)
+
+
+def bf16(x: float) -> float:
+    """Round-to-nearest-even to bfloat16 precision (the C routine the emulation uses)."""
+    return load().brute_bf16(float(x))

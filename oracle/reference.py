@@ -18,7 +18,9 @@ What it restates (all citations are to /root/reference):
   ``attention`` (the method of AT:654-656).
 * ``grads_analytic(...)`` -- the same gradients from the closed-form
   softmax-attention backward, computed per (batch, head) chunk so that the
-  full-size configs fit (usable on a GPU device for the large parity tests).
+  full-size configs fit (usable on a GPU device for the large parity tests);
+  with ``bf16_products=True`` the reference kernel's bf16 rounding points
+  (P before dV, dS * sm_scale before dK / dQ, Delta from the bf16 output O).
 * ``rope(x, theta)`` -- explicit pairwise rotation (AT:533-541).
 * ``rope_tables``, ``rmsnorm``, ``apply_rope``, ``qknorm_rope`` -- the
   sublayer prologue (config 5): the Rotary cos/sin tables (AT:438-444), the
@@ -31,8 +33,11 @@ What it restates (all citations are to /root/reference):
   bf16 cast).
 
 How it is pinned (tests/test_oracle.py): against the plain-C fp64 brute force
-in ``oracle/brute_attn.c`` (forward, lse2 and an independent derivation of the
-backward), against torch's ``scaled_dot_product_attention`` (a library
+in ``oracle/brute_attn.c`` (forward, lse2, an independent derivation of the
+backward, Delta through the identity rowsum(O * dO) = sum_j P_ij dP_ij, and
+the backward with the reference kernel's bf16 rounding points, which pins
+``grads_analytic(bf16_products=True)``), against torch's
+``scaled_dot_product_attention`` (a library
 routine), against closed forms (S=1, constant V, constant K, lse2 lower bound)
 and invariants (causal no-leak, batch permutation, identical heads), and
 against the committed fixtures in ``tests/golden/``.  No function here is left
@@ -111,7 +116,7 @@ def forward_chunked(q, k, v, causal, groups, dtype=torch.float32):
 
 
 @torch.no_grad()
-def grads_analytic(q, k, v, do, causal, groups, dtype=torch.float32, bf16_products=False, o=None):
+def grads_analytic(q, k, v, do, causal, groups, dtype=torch.float32, bf16_products=False):
     """Closed-form backward of softmax attention, one (batch, head) at a time:
         P = softmax(s), dP = dO V^T, Delta_i = sum_j P_ij dP_ij,
         dS = P * (dP - Delta), dQ = dS K / sqrt(D), dK = dS^T Q / sqrt(D),
@@ -119,12 +124,13 @@ def grads_analytic(q, k, v, do, causal, groups, dtype=torch.float32, bf16_produc
     Returns fp32 (dq, dk, dv).
 
     bf16_products=True emulates the rounding points of the reference's
-    TileLang backward (AT:297-314): P rounded to bf16 before dV = P^T dO
-    (:306-307), dS * sm_scale rounded to bf16 before dK and dQ (:310-314),
-    Delta from the bf16 forward output `o` (:380, :212-214).  The distance of
-    that emulation from the exact fp32 math is the error the reference's own
-    kernel arithmetic costs; the parity gates allow it on top of their
-    tolerance."""
+    TileLang backward (AT:297-314), everything else in `dtype`: P rounded to
+    bf16 before dV = P^T dO (:306-307); dS * sm_scale rounded to bf16 before
+    dK and dQ (:310-314); Delta = rowsum(bf16(O) * dO) from this function's
+    own forward output O = P V rounded to bf16, as the reference's flash_delta
+    reads the forward's bf16 O (:380, :212-214).  The distance of that
+    emulation from the exact math is the error the reference's own kernel
+    arithmetic costs."""
     B, S, H, D = q.shape
     Hkv = k.shape[2]
     scale = 1.0 / math.sqrt(D)
@@ -143,7 +149,8 @@ def grads_analytic(q, k, v, do, causal, groups, dtype=torch.float32, bf16_produc
             p = s.softmax(-1)
             dp = torch.matmul(doh, vh.t().contiguous())
             if bf16_products:
-                dlt = (o[b, :, h].to(torch.bfloat16).to(dtype) * doh).sum(-1, keepdim=True)
+                ob = torch.matmul(p, vh).to(torch.bfloat16).to(dtype)
+                dlt = (ob * doh).sum(-1, keepdim=True)
                 dsb = (p * (dp - dlt) * scale).to(torch.bfloat16).to(dtype)
                 pb = p.to(torch.bfloat16).to(dtype)
                 dq[b, :, h] = torch.matmul(dsb, kh)

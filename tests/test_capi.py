@@ -54,7 +54,7 @@ def test_version_matches_header(lib):
 
 def test_error_codes_and_messages(lib):
     codes = dict(re.findall(r"#define (MM1_E_\w+) \((-\d+)\)", HEADER.read_text()))
-    assert len(codes) == 7
+    assert len(codes) == 8
     for name, code in codes.items():
         msg = lib.mm1_attn_strerror(int(code)).decode()
         assert msg.startswith("mm1_attn:") and "unknown" not in msg, name
@@ -110,6 +110,49 @@ def test_bwd_argument_errors(lib):
     assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 10, 2, 128, 1, None) == -4
     # nothing to reduce without groups: success without a device call
     assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 4, 4, 128, 1, None) == 0
+
+
+def test_reduce_refuses_a_workspace_without_matching_partials(lib):
+    """The calls that sum dK/dV partials check the layout record of the
+    workspace (written by a successful mm1_attn_bwd_dkdv* launch) and return
+    MM1_E_LAYOUT, launching nothing, when there is none for that address --
+    here no dK/dV call ever ran on it.  On the GPU the mismatched-tiling and
+    mismatched-shape cases are checked after real dK/dV launches."""
+    E_LAYOUT = -8
+    need = lib.mm1_attn_bwd_workspace_size(2, 100, 10, 2, 128)
+    ws = FAKE + (1 << 20)
+    for t in range(lib.mm1_attn_tile_count(1)):
+        assert lib.mm1_attn_bwd_dkdv_reduce_tiles(ws, need, FAKE, FAKE, 2, 100, 10, 2, 128, 1, t, None) == E_LAYOUT
+        assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, need,
+                                                2, 100, 10, 2, 128, 1, 0.1, t, 0, None) == E_LAYOUT
+    assert lib.mm1_attn_bwd_dkdv_reduce(ws, need, FAKE, FAKE, 2, 100, 10, 2, 128, 1, None) == E_LAYOUT
+    assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, need,
+                                      2, 100, 10, 2, 128, 1, 0.1, None) == E_LAYOUT
+    # argument errors still come first, and a tiling out of range is MM1_E_TILES
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(ws, need, FAKE, FAKE, 2, 100, 10, 2, 128, 1, 99, None) == -7
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(None, 0, FAKE, FAKE, 2, 100, 10, 2, 128, 1, 0, None) == -4
+    # the dQ call without the sum needs no workspace and no record
+    assert lib.mm1_attn_bwd_dq_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None,
+                                     2, 100, 10, 2, 128, 1, 0.1, 0, None) == -1
+    assert lib.mm1_attn_bwd_dq_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                     2, 100, 10, 2, 128, 1, 0.1, 9, None) == -7
+    assert lib.mm1_attn_bwd_dkdv_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, need,
+                                       2, 100, 10, 2, 128, 1, 0.1, 9, None) == -7
+
+
+def test_no_environment_switch_changes_the_tiling(lib, monkeypatch):
+    """The library reads no tiling or chunk switch from the environment: the
+    chunk plan and the layout of the partial sums depend on the shape, the
+    tiling argument and the CU count only."""
+    import ctypes
+    plan = (ctypes.c_int * 5)()
+    assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, plan) == 0
+    before = list(plan)
+    for name, val in (("MM1_DKDV_CHUNK", "300"), ("MM1_DKDV_VARIANT", "1"), ("MM1_DQ_VARIANT", "1"),
+                      ("MM1_FWD_VARIANT", "2")):
+        monkeypatch.setenv(name, val)
+    assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, plan) == 0
+    assert list(plan) == before
     assert lib.mm1_attn_delta(FAKE, None, FAKE, 1, 64, 10, 128, None) == -1
     assert lib.mm1_attn_delta(FAKE, FAKE, FAKE, 1, 64, 10, 64, None) == -3
 
@@ -409,18 +452,15 @@ def test_grouped_dkdv_plan(lib, B, S, H, Hkv, causal):
     assert _makespan(order, costs, 8) <= _makespan(default, costs, 8) * 1.01 + 8
 
 
-def test_grouped_dkdv_plan_errors_and_override(lib, monkeypatch):
+def test_grouped_dkdv_plan_errors_and_dispatch_switch(lib, monkeypatch):
     import ctypes
     plan = (ctypes.c_int * 5)()
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, None) == -1
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 3, 1, 256, plan) == -2
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 0, plan) == -2
     # the dK/dV tiling index is checked by the dispatch-order query
-    assert lib.mm1_attn_dispatch_order(1, 3, 2, 8192, 10, 2, 1, 256, None, 0) == -7
+    assert lib.mm1_attn_dispatch_order(1, 5, 2, 8192, 10, 2, 1, 256, None, 0) == -7
     assert lib.mm1_attn_dispatch_order(1, 1, 2, 8192, 10, 2, 1, 256, None, 0) == 0
-    monkeypatch.setenv("MM1_DKDV_CHUNK", "300")
-    assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, plan) == 0
-    assert plan[0] == 300
     monkeypatch.setenv("MM1_DISPATCH_ORDER", "0")
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, plan) == 0
     assert plan[4] == 0

@@ -128,12 +128,111 @@ def test_identical_heads_in_a_group_give_identical_outputs():
     assert not torch.allclose(o[:, :, 7], o[:, :, 0])
 
 
-def test_delta_closed_form():
-    q, k, v, do = R.make_inputs(1, 16, 10, 2, 128, seed=10)
-    o = R.attention(q, k, v, True, 5)
-    d = R.delta(o, do)
-    want = torch.einsum("bshd,bshd->bhs", o.float(), do.float())
-    assert (d - want).abs().max() < 1e-5
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_delta_identity_against_brute_force(shape, causal):
+    """Delta = rowsum(O * dO) (AT:212-214) is pinned by the identity
+    sum_d O_id dO_id = sum_j P_ij (dO_i . V_j) = sum_j P_ij dP_ij: R.delta on
+    the brute force's own O must give the brute force's sum over keys of
+    P * dP, which never forms O."""
+    B, S, H, Hkv = shape
+    q, k, v, do = R.make_inputs(B, S, H, Hkv, 128, seed=S + 40, dtype=torch.float64)
+    o_ref, _ = brute.fwd(_np(q), _np(k), _np(v), causal)
+    *_, want = brute.bwd(_np(q), _np(k), _np(v), _np(do), causal, with_delta=True)
+    # R.delta accumulates in fp32, as the reference's kernel does: agreement
+    # to fp32 accuracy over the 128-term sums
+    got = R.delta(torch.from_numpy(o_ref), do)
+    assert np.abs(_np(got) - want).max() < 1e-6 * max(1.0, np.abs(want).max()) * 8
+
+
+def test_delta_identity_catches_planted_mistakes():
+    """Plausible mistakes in Delta fail the identity: the wrong operand (O * O),
+    the sum over heads instead of head_dim, a dropped transpose to [B, H, S]."""
+    q, k, v, do = R.make_inputs(2, 9, 10, 2, 128, seed=44, dtype=torch.float64)
+    o_ref, _ = brute.fwd(_np(q), _np(k), _np(v), True)
+    *_, want = brute.bwd(_np(q), _np(k), _np(v), _np(do), True, with_delta=True)
+    o = torch.from_numpy(o_ref)
+    wrong = [
+        (o * o).sum(-1).permute(0, 2, 1),                                   # wrong operand
+        (o * do).sum(-1).sum(-1, keepdim=True).expand(2, 9, 10).permute(0, 2, 1),   # summed over heads too
+        (o * do).sum(-1).reshape(2, 10, 9),                                 # [B,S,H] read as [B,H,S]
+    ]
+    for w in wrong:
+        assert np.abs(_np(w) - want).max() > 1e-3
+
+
+EMUL_SHAPES = [(1, 1, 10, 2), (2, 7, 10, 2), (1, 19, 4, 4), (2, 13, 6, 3), (1, 24, 8, 1), (1, 48, 10, 2)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", EMUL_SHAPES)
+def test_emulated_rounding_matches_brute_force(shape, causal):
+    """grads_analytic(bf16_products=True) -- the reference kernel's rounding
+    points, whose distance from the exact math the GPU parity gates report
+    and allow -- is pinned to the fp64 C brute force with the same rounding
+    points (brute_attn_bwd_emul: bf16(P) before dV, bf16(P (dP - Delta)
+    sm_scale) before dK / dQ, Delta from bf16(O)).  Both evaluate the values
+    they round in fp64, so every rounding decision agrees and the results
+    match to fp64 summation order; the emulation is also shown to differ from
+    the exact backward (else the pin would not see the rounding points)."""
+    B, S, H, Hkv = shape
+    q, k, v, do = R.make_inputs(B, S, H, Hkv, 128, seed=S + 60, dtype=torch.float64)
+    want = brute.bwd_emul(_np(q), _np(k), _np(v), _np(do), causal)[:3]
+    exact = brute.bwd(_np(q), _np(k), _np(v), _np(do), causal)
+    got = R.grads_analytic(q, k, v, do, causal, H // Hkv, torch.float64, bf16_products=True)
+    for name, g, w, e in zip(("dq", "dk", "dv"), got, want, exact):
+        scale = max(1.0, np.abs(w).max())
+        assert np.abs(_np(g) - w).max() < 1e-10 * scale, name
+        if S > 1:
+            assert np.abs(w - e).max() > 1e-5 * scale, name
+    # the fp32 evaluation the GPU tests use: the same formulas; near a
+    # rounding boundary its fp32 values may round to the other neighbour,
+    # which moves a result by about one bf16 ulp of one product term
+    got32 = R.grads_analytic(q.float(), k.float(), v.float(), do.float(), causal, H // Hkv,
+                             bf16_products=True)
+    for name, g, w in zip(("dq", "dk", "dv"), got32, want):
+        assert np.abs(_np(g) - w).max() < 1e-2 * max(1.0, np.abs(w).max()), name
+
+
+def test_emulated_rounding_pin_catches_planted_mistakes():
+    """Emulations with a rounding point dropped, moved or added fail the pin
+    by orders of magnitude: no bf16 on dS; bf16 of dS before the sm_scale
+    product; Delta from the exact O; P rounded for dS as well; dV from the
+    unrounded P."""
+    B, S, H, Hkv = 1, 48, 10, 2
+    q, k, v, do = R.make_inputs(B, S, H, Hkv, 128, seed=99, dtype=torch.float64)
+    want = brute.bwd_emul(_np(q), _np(k), _np(v), _np(do), True)[:3]
+    scale = 1 / math.sqrt(128)
+    bf = lambda t: t.to(torch.bfloat16).double()
+
+    def emul(variant):
+        dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+        keep = torch.ones(S, S, dtype=torch.bool).tril()
+        for h in range(H):
+            g = h // 5
+            qh, kh, vh, doh = q[0, :, h], k[0, :, g], v[0, :, g], do[0, :, h]
+            p = (qh @ kh.t() * scale).masked_fill(~keep, float("-inf")).softmax(-1)
+            dp = doh @ vh.t()
+            o = p @ vh
+            dlt = ((o if variant == "exact_o" else bf(o)) * doh).sum(-1, keepdim=True)
+            pp = bf(p) if variant == "p_rounded" else p
+            if variant == "no_ds_round":
+                dsb = pp * (dp - dlt) * scale
+            elif variant == "round_before_scale":
+                dsb = bf(pp * (dp - dlt)) * scale
+            else:
+                dsb = bf(pp * (dp - dlt) * scale)
+            dq[0, :, h] = dsb @ kh
+            dk[0, :, g] += dsb.t() @ qh
+            dv[0, :, g] += (p if variant == "exact_p_dv" else bf(p)).t() @ doh
+        return dq, dk, dv
+
+    def err(got):
+        return max(np.abs(_np(g) - w).max() / max(1.0, np.abs(w).max()) for g, w in zip(got, want))
+
+    assert err(emul("reference")) < 1e-10
+    for variant in ("no_ds_round", "round_before_scale", "exact_o", "p_rounded", "exact_p_dv"):
+        assert err(emul(variant)) > 1e-5, variant
 
 
 def test_golden_fixtures_reproduce():
