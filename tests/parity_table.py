@@ -1,0 +1,47 @@
+"""Formats the parity records a GPU test run leaves (MM1_PARITY_LOG, one JSON
+object per checked output, written by tests/parity.py) as a markdown table.
+
+    MM1_PARITY_LOG=gpurun_out/parity.jsonl python -m pytest tests -m gpu ...
+    python tests/parity_table.py gpurun_out/parity.jsonl [--cases config,golden,ragged]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+
+ORDER = {"O": 0, "lse2": 1, "dQ": 2, "dK": 3, "dV": 4, "delta": 5}
+
+
+def fmt(x):
+    return "" if x is None else f"{x:.2e}"
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("log")
+    ap.add_argument("--cases", default="config,golden,ragged,smoke",
+                    help="comma-separated prefixes of the case names to include")
+    args = ap.parse_args(argv)
+    prefixes = tuple(args.cases.split(","))
+    recs = [json.loads(line) for line in open(args.log) if line.strip()]
+    recs = [r for r in recs if r.get("case", "").startswith(prefixes)]
+    seen, rows = set(), []
+    for r in recs:
+        key = (r["case"], r["out"])
+        if key in seen:
+            continue
+        seen.add(key)
+        rows.append(r)
+    rows.sort(key=lambda r: (r["case"], ORDER.get(r["out"], 9)))
+    print("| case | out | max-abs | rel-L2 | floor | pre-cast max-abs | pre-cast rel-L2 | alg | alg rel-L2 "
+          "| vs emul max-abs | vs emul rel-L2 | gate |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|")
+    for r in rows:
+        print(f"| {r['case']} | {r['out']} | {fmt(r['max_abs'])} | {fmt(r['rel_l2'])} | {fmt(r.get('floor'))} "
+              f"| {fmt(r.get('precast_max_abs'))} | {fmt(r.get('precast_rel_l2'))} | {fmt(r.get('alg'))} "
+              f"| {fmt(r.get('alg_rel'))} | {fmt(r.get('vs_emul_max_abs'))} | {fmt(r.get('vs_emul_rel_l2'))} "
+              f"| {r.get('gate')} |")
+
+
+if __name__ == "__main__":
+    main()
