@@ -41,6 +41,7 @@ extern "C" {
 #define MM1_E_LAYOUT (-8)      /* the workspace holds no dK/dV partial sums of this shape and
                                   dK/dV tiling (see mm1_attn_bwd_dkdv_reduce) */
 
+
 /* Kernel kinds for the tiling queries below. */
 #define MM1_TILES_FWD 0
 #define MM1_TILES_DKDV 1

@@ -24,9 +24,9 @@ another implementation.
 """
 from __future__ import annotations
 
-import argparse
 import math
 import os
+import sys
 import time
 from dataclasses import dataclass
 
@@ -35,8 +35,10 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from .wgrad import wgrad
 from . import tuned
+from .harness import Report, compare, needs_gpu, time_cuda
+from .harness import main as harness_main
+from .wgrad import wgrad
 
 DTYPE = torch.bfloat16
 LOG2E = 1.4426950408889634
@@ -393,7 +395,10 @@ class AttnConfig:
 
 
 class RMSNorm(nn.Module):
-    """Per-head QK norm, computed in fp32 and cast back (AT:418-428)."""
+    """Per-head QK norm (AT:418-428): x / rms(x) * weight over the last axis,
+    evaluated in fp32 and returned in x's dtype.  The fp32 products happen in
+    the reference's order (normalise, then weight), which the bf16 kernel
+    path (mm1_qknorm_rope_fwd) reproduces bit for bit."""
 
     def __init__(self, dim, eps=1e-5):
         super().__init__()
@@ -401,15 +406,15 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x):
-        dtype = x.dtype
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return (xf * self.weight.float()).to(dtype)
+        wide = x.float()
+        inv_rms = wide.square().mean(dim=-1, keepdim=True).add(self.eps).rsqrt()
+        return (wide * inv_rms * self.weight.float()).to(x.dtype)
 
 
 class Rotary(nn.Module):
-    """cos/sin tables of rotate-half RoPE, angles duplicated over both halves
-    (AT:431-449)."""
+    """Rotate-half RoPE tables (AT:431-449): for position p and frequency
+    index i < D/2, the angle p * theta^(-2i/D) appears in columns i and
+    i + D/2 of the fp32 [max_seq_len, D] cos and sin buffers."""
 
     def __init__(self, head_dim, max_seq_len, theta):
         super().__init__()
@@ -417,30 +422,36 @@ class Rotary(nn.Module):
         self.max_seq_len = max_seq_len
         self.build(theta)
 
+    def _tables(self, theta, device=None):
+        exponent = torch.arange(0, self.head_dim, 2, device=device).float() / self.head_dim
+        inv_freq = (theta ** exponent).reciprocal()
+        angle = torch.arange(self.max_seq_len, device=device).float()[:, None] * inv_freq[None, :]
+        angle = angle.repeat(1, 2)                      # the same angle for both halves
+        return angle.cos(), angle.sin()
+
     def build(self, theta):
         self.theta = theta
-        inv = 1.0 / (theta ** (torch.arange(0, self.head_dim, 2).float() / self.head_dim))
-        ang = torch.arange(self.max_seq_len).float()[:, None] * inv[None, :]
-        table = torch.cat((ang, ang), dim=-1)
-        self.register_buffer("cos", table.cos(), persistent=False)
-        self.register_buffer("sin", table.sin(), persistent=False)
+        cos, sin = self._tables(theta)
+        self.register_buffer("cos", cos, persistent=False)
+        self.register_buffer("sin", sin, persistent=False)
 
     def set_theta(self, theta):
-        device = self.cos.device
-        self.build(theta)
-        self.cos, self.sin = self.cos.to(device), self.sin.to(device)
+        """New base frequency, tables rebuilt where the current ones live."""
+        self.theta = theta
+        self.cos, self.sin = (t.to(self.cos.device) for t in self._tables(theta))
 
 
 def rotate_half(x):
-    half = x.shape[-1] // 2
-    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+    """(a, b) -> (-b, a) over the two halves of the last axis."""
+    lo, hi = x.chunk(2, dim=-1)
+    return torch.cat((hi.neg(), lo), dim=-1)
 
 
 def apply_rope(x, cos, sin):
-    """x [B,S,H,D]; tables cast to x.dtype as in AT:457-461."""
-    seq_len = x.shape[1]
-    c = cos[:seq_len].to(x.dtype)[:, None, :]
-    s = sin[:seq_len].to(x.dtype)[:, None, :]
+    """x [B,S,H,D] rotated by the first S rows of the tables, which are cast to
+    x's dtype first (AT:457-461), so that a bf16 x is rotated in bf16 steps."""
+    rows = x.shape[1]
+    c, s = (t[:rows].to(x.dtype).unsqueeze(1) for t in (cos, sin))
     return x * c + rotate_half(x) * s
 
 
@@ -570,40 +581,38 @@ def qknorm_rope(qkv, wq, wk, cos, sin, heads, kv_heads, eps=1e-5):
 
 
 class Attention(nn.Module):
-    """GQA attention sublayer: wq/wk/wv, QK-RMSNorm, RoPE, causal attention, wo
-    (AT:464-518).  ``backend`` "hip" (also accepted under the reference's name
-    "tilelang") runs the gfx950 kernels; "sdpa", "flex" and "math" are the
-    reference's library/torch alternatives."""
+    """GQA attention sublayer (AT:464-518): projections wq / wk / wv to 10 query
+    and 2 KV heads of 128, QK-RMSNorm, RoPE, causal attention, projection wo
+    back to d_model; no biases.  ``backend`` "hip" (also accepted under the
+    reference's name "tilelang") runs the gfx950 kernels; "sdpa", "flex" and
+    "math" run torch's library attention, flex attention, and the fp32 math."""
 
     def __init__(self, cfg: AttnConfig, rope: Rotary):
         super().__init__()
         self.cfg = cfg
         self.rope = rope
-        heads, kv_heads, dim = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
-        self.wq = nn.Linear(cfg.d_model, heads * dim, bias=False)
-        self.wk = nn.Linear(cfg.d_model, kv_heads * dim, bias=False)
-        self.wv = nn.Linear(cfg.d_model, kv_heads * dim, bias=False)
-        self.wo = nn.Linear(heads * dim, cfg.d_model, bias=False)
-        self.q_norm = RMSNorm(dim, cfg.norm_eps) if cfg.qk_norm else nn.Identity()
-        self.k_norm = RMSNorm(dim, cfg.norm_eps) if cfg.qk_norm else nn.Identity()
-        self.scale = 1.0 / math.sqrt(dim)
+        q_width, kv_width = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+        linear = lambda n_in, n_out: nn.Linear(n_in, n_out, bias=False)
+        self.wq, self.wk, self.wv = (linear(cfg.d_model, w) for w in (q_width, kv_width, kv_width))
+        self.wo = linear(q_width, cfg.d_model)
+        norm = (lambda: RMSNorm(cfg.head_dim, cfg.norm_eps)) if cfg.qk_norm else nn.Identity
+        self.q_norm, self.k_norm = norm(), norm()
+        self.scale = 1.0 / math.sqrt(cfg.head_dim)
+
+    def _heads(self, t, n):
+        return t.unflatten(-1, (n, self.cfg.head_dim))
 
     def project(self, x):
         """QKV projections, QK-norm and RoPE: the inputs of the attention kernel."""
-        batch, seq_len, _ = x.shape
-        cfg = self.cfg
-        q = self.q_norm(self.wq(x).view(batch, seq_len, cfg.n_heads, cfg.head_dim))
-        k = self.k_norm(self.wk(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim))
-        v = self.wv(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim)
-        q = apply_rope(q, self.rope.cos, self.rope.sin)
-        k = apply_rope(k, self.rope.cos, self.rope.sin)
-        return q, k, v
+        cfg, rope = self.cfg, self.rope
+        q = apply_rope(self.q_norm(self._heads(self.wq(x), cfg.n_heads)), rope.cos, rope.sin)
+        k = apply_rope(self.k_norm(self._heads(self.wk(x), cfg.n_kv_heads)), rope.cos, rope.sin)
+        return q, k, self._heads(self.wv(x), cfg.n_kv_heads)
 
     def project_fused(self, x):
         """The same q, k, v from one GEMM against wq | wk | wv and the QK-norm +
         RoPE kernel; None when the projection is not bf16 (fp32 activations
         outside autocast keep the reference's fp32 norm and rotation)."""
-        batch, seq_len, _ = x.shape
         cfg = self.cfg
         w = torch.cat((self.wq.weight, self.wk.weight, self.wv.weight), dim=0)
         qkv = BF16Linear.apply(x, w) if _bf16_linear_applies(x) else F.linear(x, w)
@@ -614,188 +623,198 @@ class Attention(nn.Module):
         return qknorm_rope(qkv.contiguous(), qn, kn, self.rope.cos, self.rope.sin,
                            cfg.n_heads, cfg.n_kv_heads, cfg.norm_eps)
 
+    # the non-kernel backends, on BSHD q / k / v; each returns BSHD output
+    def _attend_sdpa(self, q, k, v, x):
+        to_bhsd = lambda t: t.transpose(1, 2)
+        out = F.scaled_dot_product_attention(to_bhsd(q), to_bhsd(k), to_bhsd(v), is_causal=True,
+                                             scale=self.scale, enable_gqa=True)
+        return out.transpose(1, 2)
+
+    def _attend_flex(self, q, k, v, x):
+        from torch.nn.attention.flex_attention import create_block_mask, flex_attention
+        n = q.shape[1]
+        causal = create_block_mask(lambda b, h, qi, ki: ki <= qi, None, None, n, n, device=x.device)
+        out = flex_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                             block_mask=causal, scale=self.scale, enable_gqa=True)
+        return out.transpose(1, 2)
+
+    def _attend_math(self, q, k, v, x):
+        # fp32 scores scaled by multiplication, as the reference's math branch
+        return _attention_fp32(q, k, v, True, self.cfg.groups, self.scale).to(x.dtype)
+
     def forward(self, x, backend=None):
-        batch, seq_len, _ = x.shape
         cfg = self.cfg
         backend = backend or cfg.backend
-        fused = self.project_fused(x) if backend in _HIP_BACKENDS and x.is_cuda else None
+        hip = backend in _HIP_BACKENDS
+        fused = self.project_fused(x) if hip and x.is_cuda else None
         q, k, v = fused if fused is not None else self.project(x)
-
-        if backend in _HIP_BACKENDS:
-            out = flash_attention(q.to(DTYPE).contiguous(), k.to(DTYPE).contiguous(),
-                                  v.to(DTYPE).contiguous(), True, cfg.groups)
+        if hip:
+            out = flash_attention(*(t.to(DTYPE).contiguous() for t in (q, k, v)), True, cfg.groups)
             if not _skip_attn_out_cast():
                 out = out.to(x.dtype)
         else:
-            qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))
-            if backend == "sdpa":
-                out = F.scaled_dot_product_attention(
-                    qh, kh, vh, is_causal=True, scale=self.scale, enable_gqa=True)
-            elif backend == "flex":
-                from torch.nn.attention.flex_attention import create_block_mask, flex_attention
-                mask = create_block_mask(lambda b, h, i, j: i >= j, B=None, H=None,
-                                         Q_LEN=seq_len, KV_LEN=seq_len, device=x.device)
-                out = flex_attention(qh, kh, vh, block_mask=mask, scale=self.scale,
-                                     enable_gqa=True)
-            elif backend == "math":
-                kh = kh.repeat_interleave(cfg.groups, dim=1)
-                vh = vh.repeat_interleave(cfg.groups, dim=1)
-                scores = torch.matmul(qh.float(), kh.float().transpose(-2, -1).contiguous())
-                scores = scores * self.scale
-                keep = torch.ones(seq_len, seq_len, dtype=torch.bool, device=x.device).tril()
-                probs = scores.masked_fill(~keep, float("-inf")).softmax(-1)
-                out = torch.matmul(probs, vh.float().contiguous()).to(x.dtype)
-            else:
+            attend = {"sdpa": self._attend_sdpa, "flex": self._attend_flex, "math": self._attend_math}
+            if backend not in attend:
                 raise ValueError(f"unknown backend {backend!r}")
-            out = out.transpose(1, 2)
-
-        out = out.reshape(batch, seq_len, cfg.n_heads * cfg.head_dim)
-        if backend in _HIP_BACKENDS and _bf16_linear_applies(out):
+            out = attend[backend](q, k, v, x)
+        out = out.flatten(2)
+        if hip and _bf16_linear_applies(out):
             return BF16Linear.apply(out, self.wo.weight)
         return self.wo(out)
 
 
 # ---------------------------------------------------------------------------
-# Harnesses (AT:521-788)
-def reference(q, k, v, causal, groups):
-    """fp32 attention math, cast to q.dtype (the contract of AT:521-530)."""
-    dim = q.size(-1)
-    seq_len = q.size(1)
-    kf = k.float().repeat_interleave(groups, dim=2).permute(0, 2, 3, 1)   # b h d k
-    vf = v.float().repeat_interleave(groups, dim=2).permute(0, 2, 1, 3)   # b h k d
-    qf = q.float().permute(0, 2, 1, 3)                                    # b h q d
-    scores = torch.matmul(qf, kf.contiguous()) / math.sqrt(dim)
+# Reference math and harnesses (AT:521-788)
+def _attention_fp32(q, k, v, causal, groups, scale=None):
+    """softmax(q k^T * scale [causal]) v in fp32 on BSHD tensors, KV head
+    h // groups for query head h; fp32 BSHD result.  `scale` None divides the
+    scores by sqrt(D) (the form of AT:525), a number multiplies them."""
+    n, dim = q.shape[1], q.shape[-1]
+    expand = lambda t: t.float().repeat_interleave(groups, dim=2).transpose(1, 2)   # B H S D
+    qh, kh, vh = q.float().transpose(1, 2), expand(k), expand(v)
+    s = torch.matmul(qh, kh.transpose(-1, -2).contiguous())
+    s = s / math.sqrt(dim) if scale is None else s * scale
     if causal:
-        keep = torch.ones(seq_len, seq_len, dtype=torch.bool, device=q.device).tril()
-        scores = scores.masked_fill(~keep, float("-inf"))
-    out = torch.matmul(scores.softmax(-1), vf.contiguous())
-    return out.permute(0, 2, 1, 3).to(q.dtype)
+        future = torch.ones(n, n, dtype=torch.bool, device=q.device).triu(1)
+        s = s.masked_fill(future, float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vh.contiguous()).transpose(1, 2)
+
+
+def reference(q, k, v, causal, groups):
+    """The fp32 attention math the kernels answer to, returned in q.dtype
+    (AT:521-530)."""
+    return _attention_fp32(q, k, v, causal, groups).to(q.dtype)
 
 
 def rope_reference(x, theta):
-    """Explicit pairwise rotation of (x_i, x_{i+D/2}) (AT:533-541)."""
-    batch, seq_len, heads, dim = x.shape
+    """RoPE as a complex rotation: the pair (x_i, x_{i+D/2}) is the complex
+    number x_i + j x_{i+D/2}, multiplied by exp(j p theta^(-2i/D)) at position
+    p (AT:533-541) -- an independent form of apply_rope's rotate-half."""
+    n, dim = x.shape[1], x.shape[-1]
     half = dim // 2
-    freqs = 1.0 / (theta ** (2 * torch.arange(half).double() / dim))
-    ang = torch.arange(seq_len).double()[:, None] * freqs[None, :]
-    c = ang.cos().float().view(1, seq_len, 1, half)
-    s = ang.sin().float().view(1, seq_len, 1, half)
-    lo, hi = x[..., :half], x[..., half:]
-    return torch.cat([lo * c - hi * s, lo * s + hi * c], dim=-1)
+    freq = torch.tensor(float(theta), dtype=torch.float64) ** (-2.0 * torch.arange(half, dtype=torch.float64) / dim)
+    turn = torch.polar(torch.ones(n, half, dtype=torch.float64),
+                       torch.arange(n, dtype=torch.float64)[:, None] * freq)
+    z = torch.complex(x[..., :half].double(), x[..., half:].double()) * turn[None, :, None, :]
+    return torch.cat((z.real, z.imag), dim=-1).to(x.dtype)
 
 
-def check_math():
-    """CPU checks of the host-side pieces (AT:544-630), gfx950 tile policy."""
-    passed = True
-
-    def check(label, condition):
-        nonlocal passed
-        passed &= bool(condition)
-        print(f"  {'ok  ' if condition else 'FAIL'}  {label}")
-
-    torch.manual_seed(0)
+def _math_checks(report: Report):
     cfg = AttnConfig(backend="math")
-    print("tilings compiled for gfx950")
+    gen = torch.Generator().manual_seed(0)
+    randn = lambda *shape: torch.randn(*shape, generator=gen)
+
+    report.section("gfx950 tilings")
     try:
-        fwd_space, bwd_space = fwd_configs(), bwd_configs()
+        spaces = {"fwd": fwd_configs(), "bwd": bwd_configs()}
     except _lib.LibraryMissing as exc:
-        print(f"    (library not built: {exc})")
+        report.note(f"library not built ({exc}); tiling checks skipped")
     else:
-        print(f"    forward  {len(fwd_space)}, backward {len(bwd_space)}")
-        check("forward default is compiled", FWD_TILES == fwd_space[0])
-        check("backward default is compiled", BWD_TILES == bwd_space[0])
-        check("every config maps back to its index",
-              all(tile_index("fwd", c) == i for i, c in enumerate(fwd_space))
-              and len({tile_index("bwd", c) for c in bwd_space}) == len(bwd_space))
-        check("waves fit a workgroup", all(c["waves"] * WAVE <= 1024 for c in fwd_space))
+        report.note(f"{len(spaces['fwd'])} forward and {len(spaces['bwd'])} backward tilings")
+        report.expect("defaults are the library's index 0",
+                      spaces["fwd"][0] == FWD_TILES and spaces["bwd"][0] == BWD_TILES)
+        report.expect("every tiling maps back to its own index",
+                      [tile_index("fwd", c) for c in spaces["fwd"]] == list(range(len(spaces["fwd"])))
+                      and len({tile_index("bwd", c) for c in spaces["bwd"]}) == len(spaces["bwd"]))
+        report.expect("every workgroup fits 1024 threads",
+                      max(c["waves"] for c in spaces["fwd"]) * WAVE <= 1024)
 
-    print("\nrope")
-    rope = Rotary(128, 64, 10_000.0)
-    x = torch.randn(2, 64, 3, 128)
-    got, want = apply_rope(x, rope.cos, rope.sin), rope_reference(x, 10_000.0)
-    check(f"matches explicit rotation ({(got - want).abs().max():.1e})",
-          (got - want).abs().max() < 1e-4)
-    check(f"norm preserved ({(got.norm(dim=-1) - x.norm(dim=-1)).abs().max():.1e})",
-          (got.norm(dim=-1) - x.norm(dim=-1)).abs().max() < 1e-4)
-    single = torch.randn(1, 1, 1, 128).expand(1, 64, 1, 128).contiguous()
-    dots = (apply_rope(single, rope.cos, rope.sin)[0, :, 0]
-            * apply_rope(single.clone(), rope.cos, rope.sin)[0, :, 0]).sum(-1)
-    check(f"relative encoding holds ({(dots - dots[0]).abs().max():.1e})",
-          (dots - dots[0]).abs().max() < 1e-3)
+    report.section("RoPE")
+    rope = Rotary(128, 96, 10_000.0)
+    x = randn(2, 96, 3, 128)
+    rotated = apply_rope(x, rope.cos, rope.sin)
+    err = (rotated - rope_reference(x, 10_000.0)).abs().max().item()
+    report.expect("rotate-half equals the complex rotation", err < 1e-4, err)
+    err = (rotated.norm(dim=-1) - x.norm(dim=-1)).abs().max().item()
+    report.expect("rotation keeps each head vector's norm", err < 1e-4, err)
+    # q.k after rotation depends only on the distance between the positions
+    a, b = randn(128), randn(128)
+    ra = apply_rope(a.expand(1, 96, 1, 128).contiguous(), rope.cos, rope.sin)[0, :, 0]
+    rb = apply_rope(b.expand(1, 96, 1, 128).contiguous(), rope.cos, rope.sin)[0, :, 0]
+    spread = max((torch.stack([ra[p] @ rb[p + d] for p in range(0, 96 - d, 7)]).std().item()
+                  for d in (0, 5, 40)))
+    report.expect("scores depend on relative position only", spread < 1e-3, spread)
     rope.set_theta(500_000.0)
-    check("set_theta rebuilds tables", rope.theta == 500_000.0)
+    fresh = Rotary(128, 96, 500_000.0)
+    report.expect("set_theta rebuilds the tables", rope.theta == 500_000.0 and torch.equal(rope.cos, fresh.cos))
 
-    print("\nrmsnorm")
-    y = RMSNorm(8)(torch.randn(3, 8))
-    check(f"unit rms output ({y.pow(2).mean().sqrt():.4f})", abs(y.pow(2).mean().sqrt() - 1) < 0.05)
+    report.section("QK RMSNorm")
+    norm = RMSNorm(16)
+    y = norm(randn(5, 16) * 7)
+    rms = y.square().mean(-1).sqrt()
+    report.expect("unit root-mean-square rows", (rms - 1).abs().max() < 1e-3, (rms - 1).abs().max().item())
+    z = randn(5, 16)
+    drift = (norm(z * 3.5) - norm(z)).abs().max().item()     # up to eps / (2 mean(z^2)) relative
+    report.expect("invariant to scaling its input", drift < 1e-4, drift)
 
-    print("\nmodule")
-    attn = Attention(cfg, Rotary(cfg.head_dim, cfg.max_seq_len, cfg.rope_theta))
-    n_params = sum(p.numel() for p in attn.parameters())
-    check(f"parameters {n_params:,}", n_params == 3_932_416)
-    check("no biases", all(m.bias is None for m in (attn.wq, attn.wk, attn.wv, attn.wo)))
-    x = torch.randn(2, 32, cfg.d_model)
-    y = attn(x, backend="math")
-    check(f"shape {tuple(x.shape)} -> {tuple(y.shape)}", y.shape == x.shape)
-    diff = (y - attn(x, backend="sdpa")).abs().max()
-    check(f"math and sdpa agree ({diff:.1e})", diff < 2e-3)
-    perturbed = x.clone()
-    perturbed[:, -1] += 10.0
-    drift = (attn(perturbed, backend="math")[:, :-1] - y[:, :-1]).abs().max()
-    check(f"causal, no leak from future ({drift:.1e})", drift < 1e-4)
-    x = torch.randn(2, 16, cfg.d_model, requires_grad=True)
-    attn(x, backend="math").sum().backward()
-    check("finite gradients everywhere",
-          torch.isfinite(x.grad).all() and all(torch.isfinite(p.grad).all() for p in attn.parameters()))
+    report.section("sublayer")
+    layer = Attention(cfg, Rotary(cfg.head_dim, cfg.max_seq_len, cfg.rope_theta))
+    count = sum(p.numel() for p in layer.parameters())
+    report.expect("parameter count 3,932,416", count == 3_932_416, count)
+    report.expect("projections carry no bias", all(m.bias is None for m in (layer.wq, layer.wk, layer.wv, layer.wo)))
+    x = randn(2, 40, cfg.d_model)
+    y = layer(x, backend="math")
+    report.expect("output keeps the input's shape", tuple(y.shape) == tuple(x.shape))
+    gap = (y - layer(x, backend="sdpa")).abs().max().item()
+    report.expect("math and sdpa backends agree", gap < 2e-3, gap)
+    later = x.clone()
+    later[:, 30:] = randn(2, 10, cfg.d_model) * 5
+    leak = (layer(later, backend="math")[:, :30] - y[:, :30]).abs().max().item()
+    report.expect("positions never see later positions", leak < 1e-5, leak)
+    x.requires_grad_(True)
+    layer(x, backend="math").square().mean().backward()
+    grads = [x.grad] + [p.grad for p in layer.parameters()]
+    report.expect("gradients reach the input and every parameter, finite",
+                  all(g is not None and bool(torch.isfinite(g).all()) for g in grads))
 
-    print("\nkernel constants")
-    check("(1/dim)**0.5 == 1/sqrt(dim)", abs((1.0 / 128) ** 0.5 - 1 / math.sqrt(128)) < 1e-12)
-    check("LOG2E == log2(e)", abs(LOG2E - math.log2(math.e)) < 1e-15)
-    print("\n" + ("all math checks passed" if passed else "FAILURES ABOVE"))
-    return passed
-
-
-def rel_err(a, b):
-    err = (a.float() - b.float()).abs().max().item()
-    return err, err / max(b.float().abs().max().item(), 1e-12)
+    report.section("constants")
+    report.expect("softmax scale (1/D)^0.5 is 1/sqrt(D)", math.isclose((1.0 / 128) ** 0.5, 1 / math.sqrt(128),
+                                                                        rel_tol=1e-15))
+    report.expect("LOG2E is log2(e)", math.isclose(LOG2E, math.log2(math.e), rel_tol=1e-15))
 
 
-def check_gpu(seq_len=512):
-    """Kernel vs fp32 reference on the GPU (the harness of AT:633-678)."""
-    if not torch.cuda.is_available():
-        print("needs a HIP device")
-        return None
-    print(f"{torch.cuda.get_device_name()}  {torch.cuda.get_device_properties(0).gcnArchName}")
-    heads, kv_heads, dim, groups = 10, 2, 128, 5
+def check_math(quiet=False) -> Report:
+    """CPU checks of the module's host side and math (the reference's
+    check(), AT:544-630): tilings, RoPE, QK-norm, the sublayer, constants."""
+    report = Report("attention math", quiet=quiet)
     torch.manual_seed(0)
-    q = torch.randn(2, seq_len, heads, dim, device="cuda", dtype=DTYPE, requires_grad=True)
-    k = torch.randn(2, seq_len, kv_heads, dim, device="cuda", dtype=DTYPE, requires_grad=True)
-    v = torch.randn(2, seq_len, kv_heads, dim, device="cuda", dtype=DTYPE, requires_grad=True)
-    grad = torch.randn(2, seq_len, heads, dim, device="cuda", dtype=DTYPE)
-    ok = True
-    for causal in (False, True):
-        out = flash_attention(q, k, v, causal, groups)
-        out.backward(grad, retain_graph=True)
-        mine = [t.grad.clone() for t in (q, k, v)]
-        q.grad = k.grad = v.grad = None
-        qf, kf, vf = (t.detach().float().requires_grad_(True) for t in (q, k, v))
-        want = reference(qf, kf, vf, causal, groups)
-        want.backward(grad.float())
-        theirs = [qf.grad, kf.grad, vf.grad]
-        print(f"\ncausal={causal}")
-        for name, a, b in zip(("out", "dQ", "dK", "dV"), [out] + mine, [want] + theirs):
-            err, rel = rel_err(a, b)
-            ok &= rel < 2e-2
-            print(f"  {name:4s} abs {err:.3e}  rel {rel:.3e}  {'ok' if rel < 2e-2 else 'FAIL'}")
-    runs = []
-    for _ in range(2):
-        flash_attention(q, k, v, True, groups).backward(grad, retain_graph=True)
-        runs.append(q.grad.clone())
-        q.grad = None
-    spread = (runs[0].float() - runs[1].float()).abs().max().item()
-    print(f"\nrepeat backward differs by {spread:.3e}"
-          f" ({'deterministic' if spread == 0 else 'NOT deterministic'})")
-    return ok and spread == 0
+    _math_checks(report)
+    return report.finish()
+
+
+def check_gpu(seq_len=512, batch=2, quiet=False) -> Report:
+    """The autograd op against the fp32 reference math on the GPU, causal and
+    full, plus a repeat of the backward (the reference's check_gpu,
+    AT:633-678, whose gate is max|d| / max|ref| < 2e-2; relative L2 is
+    reported beside it).  Inputs ~ N(0,1) from seed 0."""
+    report = Report("attention gpu", quiet=quiet)
+    if not needs_gpu("check_gpu"):
+        return report
+    dev = torch.device("cuda")
+    report.note(f"{torch.cuda.get_device_name(dev)} ({torch.cuda.get_device_properties(dev).gcnArchName})")
+    cfg = AttnConfig()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    leaf = lambda heads: torch.randn(batch, seq_len, heads, cfg.head_dim, device=dev, dtype=DTYPE,
+                                     generator=gen).requires_grad_(True)
+    q, k, v = leaf(cfg.n_heads), leaf(cfg.n_kv_heads), leaf(cfg.n_kv_heads)
+    d_out = torch.randn(q.shape, device=dev, dtype=DTYPE, generator=gen)
+    for causal in (True, False):
+        report.section(f"{'causal' if causal else 'full'} B{batch} S{seq_len}")
+        got = torch.autograd.grad(flash_attention(q, k, v, causal, cfg.groups), (q, k, v), d_out,
+                                  create_graph=False)
+        out = flash_attention(q, k, v, causal, cfg.groups)
+        exact = [t.detach().float().requires_grad_(True) for t in (q, k, v)]
+        want_out = _attention_fp32(*exact, causal, cfg.groups)
+        want = torch.autograd.grad(want_out, exact, d_out.float())
+        for name, a, b in zip(("O", "dQ", "dK", "dV"), (out,) + tuple(got), (want_out,) + tuple(want)):
+            e = compare(a, b)
+            report.expect(f"{name}: max|d|/max|ref| < 2e-2", e["finite"] and e["max_rel"] < 2e-2, e["max_rel"])
+            report.note(f"{name}: max-abs {e['max_abs']:.3e}, rel-L2 {e['rel_l2']:.3e}")
+    report.section("determinism")
+    first, second = (torch.autograd.grad(flash_attention(q, k, v, True, cfg.groups), (q, k, v), d_out)
+                     for _ in range(2))
+    report.expect("two backward passes are bitwise equal", all(torch.equal(a, b) for a, b in zip(first, second)))
+    return report.finish()
 
 
 def attention_flops(batch, seq_len, heads=10, dim=128, causal=True):
@@ -806,100 +825,68 @@ def attention_flops(batch, seq_len, heads=10, dim=128, causal=True):
     return 2 * gemm, 5 * gemm
 
 
-def benchmark(batch=8, seq_len=2048, iters=30):
-    """Times fwd+bwd of SDPA and the HIP kernels with HIP events (AT:681-748).
-    TFLOP/s uses 7*B*H*S^2*D for causal fwd+bwd; the reference's own
-    5*B*H*S^2*D count (AT:690) is printed beside it."""
-    if not torch.cuda.is_available():
-        print("needs a HIP device")
-        return None
-    heads, kv_heads, dim, groups = 10, 2, 128, 5
-    q = torch.randn(batch, seq_len, heads, dim, device="cuda", dtype=DTYPE, requires_grad=True)
-    k = torch.randn(batch, seq_len, kv_heads, dim, device="cuda", dtype=DTYPE, requires_grad=True)
-    v = torch.randn(batch, seq_len, kv_heads, dim, device="cuda", dtype=DTYPE, requires_grad=True)
-    grad = torch.randn(batch, seq_len, heads, dim, device="cuda", dtype=DTYPE)
-    fwd, bwd = attention_flops(batch, seq_len, heads, dim)
-    ref_flops = 2 * 2.0 * batch * heads * seq_len * seq_len * dim * 0.5 * 2.5
-
-    def time_it(fn):
-        for _ in range(10):
-            fn()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(True), torch.cuda.Event(True)
-        start.record()
-        for _ in range(iters):
-            fn()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / iters
-
-    def clear():
-        q.grad = k.grad = v.grad = None
-
-    qh, kh, vh, gh = (t.transpose(1, 2) for t in (q, k, v, grad))
-    results = {}
-
-    def run_sdpa():
-        F.scaled_dot_product_attention(qh, kh, vh, is_causal=True, enable_gqa=True
-                                       ).backward(gh, retain_graph=True)
-        clear()
-
-    try:
-        results["sdpa"] = time_it(run_sdpa)
-    except Exception as exc:  # library path may be missing on a given build
-        print(f"sdpa unavailable: {type(exc).__name__}: {exc}")
-
-    def run_hip():
-        flash_attention(q, k, v, True, groups).backward(grad, retain_graph=True)
-        clear()
-
-    results["hip"] = time_it(run_hip)
-    print()
-    for name, ms in sorted(results.items(), key=lambda kv: kv[1]):
-        print(f"  {name:10s} {ms:8.3f} ms   {(fwd + bwd) / ms * 1e-9:7.1f} TFLOP/s"
-              f"   (reference count {ref_flops / ms * 1e-9:7.1f})")
-    return results
+def benchmark(batch=8, seq_len=2048, iters=30, quiet=False) -> dict:
+    """fwd+bwd of the HIP autograd op and of torch SDPA, HIP-event timed
+    (the reference's benchmark, AT:681-748).  TFLOP/s counts 7*B*H*S^2*D for
+    causal fwd+bwd; the reference's own 5*B*H*S^2*D count (AT:690) is shown
+    beside it.  Returns {name: ms}."""
+    if not needs_gpu("benchmark"):
+        return {}
+    cfg = AttnConfig()
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    leaf = lambda heads: torch.randn(batch, seq_len, heads, cfg.head_dim, device=dev, dtype=DTYPE,
+                                     generator=gen).requires_grad_(True)
+    q, k, v = leaf(cfg.n_heads), leaf(cfg.n_kv_heads), leaf(cfg.n_kv_heads)
+    d_out = torch.randn(q.shape, device=dev, dtype=DTYPE, generator=gen)
+    steps = {
+        "hip": lambda: torch.autograd.grad(flash_attention(q, k, v, True, cfg.groups), (q, k, v), d_out),
+        "sdpa": lambda: torch.autograd.grad(
+            F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                           is_causal=True, enable_gqa=True), (q, k, v), d_out.transpose(1, 2)),
+    }
+    fwd, bwd = attention_flops(batch, seq_len, cfg.n_heads, cfg.head_dim)
+    ms = {}
+    for name, step in steps.items():
+        try:
+            ms[name] = time_cuda(step, warmup=10, iters=iters)
+        except RuntimeError as exc:   # a torch attention backend may be missing from a build
+            print(f"{name}: unavailable ({exc})")
+    if not quiet:
+        for name, t in sorted(ms.items(), key=lambda kv: kv[1]):
+            print(f"  {name:6s} {t:8.3f} ms  {(fwd + bwd) / t * 1e-9:7.1f} TFLOP/s"
+                  f"  (reference count {(fwd + bwd) * 5 / 7 / t * 1e-9:7.1f})")
+    return ms
 
 
 def tune(batch=8, seq_len=2048):
-    """Search the compiled tilings at one shape and record the winners
-    (AT:751-769); ``python -m mimansm1_v1_amd.tune`` does every run shape."""
+    """Time the compiled tilings at one shape and record the winners (the
+    reference's tune(), AT:751-769); ``python -m mimansm1_v1_amd.tune`` does
+    every training shape."""
     try:
-        fwd_space, bwd_space = fwd_configs(), bwd_configs()
+        spaces = {"fwd": fwd_configs(), "bwd": bwd_configs()}
     except _lib.LibraryMissing as exc:
         print(f"library not built: {exc}")
-        return
-    print(f"forward candidates  {len(fwd_space)}")
-    print(f"backward candidates {len(bwd_space)}")
+        return None
+    for kind, space in spaces.items():
+        print(f"{kind}: {len(space)} tilings")
     if not torch.cuda.is_available():
-        for name, space in (("forward", fwd_space), ("backward", bwd_space)):
-            print(f"\n{name}")
-            for c in space:
-                print(f"  {c}")
-        return
+        for kind, space in spaces.items():
+            for config in space:
+                print(f"  {kind}  {config}")
+        return None
     cfg = AttnConfig()
     shape = (batch, cfg.n_heads, seq_len, cfg.head_dim, True, cfg.groups)
-    for kind in ("fwd", "bwd"):
+    winners = {}
+    for kind in spaces:
         config, latency, _ = autotune(kind, shape, verbose=True)
         tuned.record(f"attention_{kind}", shape, config)
         _kernels.pop((kind, shape, AUTOTUNE), None)
-        print(f"\n{kind}: {config}\n     {latency:.3f} ms")
+        winners[kind] = (config, latency)
+        print(f"{kind} winner {latency:.3f} ms: {config}")
+    return winners
 
 
 if __name__ == "__main__":
-    parser = argparse.ArgumentParser()
-    parser.add_argument("--check", action="store_true")
-    parser.add_argument("--gpu", action="store_true")
-    parser.add_argument("--bench", action="store_true")
-    parser.add_argument("--tune", action="store_true")
-    args = parser.parse_args()
-    if not any(vars(args).values()):
-        args.check = True
-    if args.check:
-        check_math()
-    if args.gpu:
-        check_gpu()
-    if args.bench:
-        benchmark()
-    if args.tune:
-        tune()
+    sys.exit(harness_main("mimansm1_v1_amd.attention",
+                          {"check": check_math, "gpu": check_gpu, "bench": benchmark, "tune": tune}))

@@ -395,7 +395,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     float* __restrict__ ws_dk, float* __restrict__ ws_dv,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order,
-    int chunk_tiles, int max_chunks, const DispatchOrder ord, int force_partials) {
+    int chunk_tiles, int max_chunks, const DispatchOrder ord, int force_partials, int ws_rows) {
   static_assert(NSTAGE >= 6, "ring depth: at least 6");
   static_assert(KB == 1 || KB == 2, "32 or 64 keys per wave");
   constexpr int NW = 8 / KB;              // waves per workgroup
@@ -419,7 +419,10 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // interleave, so every workgroup starts at the sequence end and those that
   // run together stream the same rows.  The sums go to partial slot `part`
   // of `nparts`, or straight to dk/dv when nparts == 1 (unless
-  // force_partials: fp32 partials in every case, for the fp32 backward).
+  // force_partials: fp32 partials in every case, for the fp32 backward).  A
+  // workspace slot holds ws_rows key rows per batch element: S for the
+  // per-head tilings, split_keys (the keys of split key tiles, the only ones
+  // with partials) for the grouped ones.
   int b, g, kt, n_qt, u0, n_u, ustep, part, nparts, hbase, HW;
   if constexpr (GROUP) {
     const int j = dispatch_item(ord);
@@ -796,8 +799,8 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
         }
       }
     } else {
-      const long slot = (long)part * B * S * Hkv * HD;
-      float* row = (pwave ? ws_dv : ws_dk) + slot + ((long)(b * S + key) * Hkv + g) * HD;
+      const long slot = (long)part * B * ws_rows * Hkv * HD;
+      float* row = (pwave ? ws_dv : ws_dk) + slot + ((long)(b * ws_rows + key) * Hkv + g) * HD;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
 #pragma unroll
@@ -813,11 +816,12 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
 }
 
 // The dK/dV partial sums to reduce, and where the reduction runs.  Two
-// layouts, both [slot][B][S][Hkv][D] fp32 for dK and for dV:
-//   per-head dK/dV (chunk_tiles == 0): slot = query head of the group; every
-//     element sums its G slots;
-//   grouped dK/dV (chunk_tiles > 0): slot = chunk of the key tile; only keys
-//     [0, split_keys) of each batch are split, and a key of tile kt sums its
+// layouts, fp32, dK's slots then dV's:
+//   per-head dK/dV (chunk_tiles == 0): [G][B][S][Hkv][D], slot = query head
+//     of the group; every element sums its G slots;
+//   grouped dK/dV (chunk_tiles > 0): [C][B][split_keys][Hkv][D], slot = chunk
+//     of the key tile; only keys [0, split_keys) of each batch are split,
+//     and a key of tile kt sums its
 //     dkdv_chunks(G * dkdv_n_qt(S, kt), chunk_tiles, max_chunks) slots (the
 //     other keys were written as bf16 by the dK/dV kernel itself).
 // The dQ kernel folds the reduction in: the last n_red workgroups of its grid
@@ -830,7 +834,7 @@ struct TailReduce {
   __bf16* dv;
   float* dk32;      // non-null: write the sums in fp32 here instead (fp32 backward)
   float* dv32;
-  long n;           // elements of one slot: B*S*Hkv*D
+  long n;           // elements of one slot: B*S*Hkv*D (per-head), B*split_keys*Hkv*D (grouped)
   int G;
   int n_red;        // 0: no reduction in this launch
   int chunk_tiles;  // grouped dK/dV: the plan's chunk length; 0: per-head
@@ -841,14 +845,12 @@ struct TailReduce {
 };
 
 // Elements of the reduction (a multiple of 4).
-__host__ __device__ inline long reduce_len(const TailReduce& red) {
-  return red.chunk_tiles > 0 ? red.n / red.S * red.split_keys : red.n;
-}
+__host__ __device__ inline long reduce_len(const TailReduce& red) { return red.n; }
 
 // Sum the slots of reduction elements i .. i+3 in slot order and round to
 // bf16 once, so the result does not depend on which thread or kernel does it.
 __device__ __forceinline__ void reduce_at(const TailReduce& red, long i) {
-  long e = i;
+  long e = i;          // element of dk / dv; i is the element of a slot
   int slots = red.G;
   if (red.chunk_tiles > 0) {
     const long row = (long)red.Hkv * HD;
@@ -860,11 +862,11 @@ __device__ __forceinline__ void reduce_at(const TailReduce& red, long i) {
     slots = dkdv_chunks(red.G * dkdv_n_qt(red.S, kt, red.causal != 0), red.chunk_tiles, red.max_chunks);
     if (slots <= 1) return;
   }
-  f32x4 sk = *reinterpret_cast<const f32x4*>(red.ws_dk + e);
-  f32x4 sv = *reinterpret_cast<const f32x4*>(red.ws_dv + e);
+  f32x4 sk = *reinterpret_cast<const f32x4*>(red.ws_dk + i);
+  f32x4 sv = *reinterpret_cast<const f32x4*>(red.ws_dv + i);
   for (int j = 1; j < slots; ++j) {
-    sk += *reinterpret_cast<const f32x4*>(red.ws_dk + (long)j * red.n + e);
-    sv += *reinterpret_cast<const f32x4*>(red.ws_dv + (long)j * red.n + e);
+    sk += *reinterpret_cast<const f32x4*>(red.ws_dk + (long)j * red.n + i);
+    sv += *reinterpret_cast<const f32x4*>(red.ws_dv + (long)j * red.n + i);
   }
   if (red.dk32) {
     *reinterpret_cast<f32x4*>(red.dk32 + e) = sk;
@@ -1096,6 +1098,24 @@ size_t bwd_workspace_bytes(int B, int S, int H, int Hkv) {
   return (size_t)2 * G * B * S * Hkv * HD * sizeof(float);
 }
 
+// Where the partial sums of dK/dV tiling `variant` live in a workspace:
+// `slots` slots of `rows` key rows per batch element (`stride` floats each),
+// dK's slots first, then dV's.
+WsSlots ws_slots(int B, int S, int H, int Hkv, bool causal, int variant) {
+  if (dkdv_grouped(variant)) {
+    const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
+    return {(long)B * plan.split_keys * Hkv * HD, plan.split_keys, plan.C};
+  }
+  return {(long)B * S * Hkv * HD, S, H / Hkv};
+}
+
+// Bytes of the partial sums tiling `variant` writes (0 when it writes none).
+size_t bwd_partials_bytes(int B, int S, int H, int Hkv, bool causal, int variant) {
+  if (H / Hkv <= 1) return 0;
+  const WsSlots w = ws_slots(B, S, H, Hkv, causal, variant);
+  return (size_t)2 * w.slots * w.stride * sizeof(float);
+}
+
 // The reduction that follows dK/dV tiling `dkdv_variant` (n_red = 0 when
 // there is nothing to sum).
 TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
@@ -1107,9 +1127,10 @@ TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, 
   red.Hkv = Hkv;
   red.causal = causal ? 1 : 0;
   if (!workspace || G <= 1) return red;
-  red.n = (long)B * S * Hkv * HD;
+  const WsSlots w = ws_slots(B, S, H, Hkv, causal, dkdv_variant);
+  red.n = w.stride;
   red.ws_dk = static_cast<const float*>(workspace);
-  red.ws_dv = red.ws_dk + (long)G * red.n;
+  red.ws_dv = red.ws_dk + (long)w.slots * w.stride;
   red.dk = static_cast<__bf16*>(dk);
   red.dv = static_cast<__bf16*>(dv);
   if (dkdv_grouped(dkdv_variant)) {
@@ -1148,10 +1169,11 @@ static void launch_dkdv_pipe(const __bf16* qp, const __bf16* kp, const __bf16* v
     ord = &dispatch_order(row_block_grid(0, B, S, H, Hkv), false);   // unused: default order
   }
   const dim3 block(512 / KB);
+  const int ws_rows = ws_slots(B, S, H, Hkv, causal, GROUP ? 0 : 1).rows;
 #define MM1_DKDV_PIPE(CS, RG)                                                                      \
   hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, GROUP, RG, KB>), grid, block, 0, stream, qp, kp, vp, \
                      dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale,      \
-                     order, L, C, *ord, force_partials)
+                     order, L, C, *ord, force_partials, ws_rows)
   if (causal) {
     if (ragged) MM1_DKDV_PIPE(true, true);
     else MM1_DKDV_PIPE(true, false);
@@ -1175,9 +1197,9 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
                            float sm_scale, int variant, hipStream_t stream) {
   const int G = H / Hkv;
   const float scale2 = sm_scale * 1.4426950408889634f;
-  const long n_kv = (long)B * S * Hkv * HD;
+  const WsSlots w = ws_slots(B, S, H, Hkv, causal, variant);
   float* ws_dk = static_cast<float*>(workspace);
-  float* ws_dv = ws_dk ? ws_dk + (long)G * n_kv : nullptr;
+  float* ws_dv = ws_dk ? ws_dk + (long)w.slots * w.stride : nullptr;
   auto qp = static_cast<const __bf16*>(q);
   auto kp = static_cast<const __bf16*>(k);
   auto vp = static_cast<const __bf16*>(v);

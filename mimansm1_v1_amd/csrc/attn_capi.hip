@@ -169,6 +169,7 @@ bool layout_matches(const WsLayout& want) {
 
 int from_hip(hipError_t e) { return e == hipSuccess ? MM1_OK : static_cast<int>(e); }
 
+
 }  // namespace
 
 extern "C" {

@@ -106,6 +106,13 @@ __host__ __device__ inline int dkdv_chunks(int len, int L, int C) {
 // x 64 keys).
 __host__ __device__ inline bool dkdv_grouped(int variant) { return variant == 0 || variant == 3; }
 
+// Partial-sum slots of a dK/dV tiling in the backward workspace.
+struct WsSlots {
+  long stride;   // floats per slot
+  int rows;      // key rows per batch element in a slot
+  int slots;     // slots of dK (then as many of dV)
+};
+
 struct DkdvPlan {
   int L;            // target query tiles per chunk
   int C;            // chunks per key tile at most (<= G: the workspace holds G slots)
@@ -117,5 +124,11 @@ struct DkdvPlan {
 // Cached plan for the current device's CU count / for a given CU count.
 const DkdvPlan& dkdv_plan(int B, int S, int H, int Hkv, bool causal);
 const DkdvPlan& dkdv_plan_for(int B, int S, int H, int Hkv, bool causal, int cus);
+
+// Workspace slots of dK/dV tiling `variant` (grouped: the plan's C chunks of
+// its split keys; per-head: G heads of all keys), and their bytes (0 for
+// G == 1, where no partials are written).
+WsSlots ws_slots(int B, int S, int H, int Hkv, bool causal, int variant);
+size_t bwd_partials_bytes(int B, int S, int H, int Hkv, bool causal, int variant);
 
 }  // namespace mm1

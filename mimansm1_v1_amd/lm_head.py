@@ -24,7 +24,7 @@ built library the kernel entry points raise; there is no CPU fallback.
 """
 from __future__ import annotations
 
-import argparse
+import sys
 from dataclasses import dataclass
 
 import torch
@@ -33,6 +33,8 @@ import torch.nn.functional as F
 
 from . import _lib
 from . import tuned
+from .harness import Report, compare, needs_gpu, time_cuda
+from .harness import main as harness_main
 
 DTYPE = torch.bfloat16
 IGNORE_INDEX = -100
@@ -222,49 +224,53 @@ class HeadConfig:
 
 
 class LMHead(nn.Module):
-    """Same structure as LM:279-335: a tied head reads the embedding matrix
-    (no parameters of its own), an untied one owns [d_model, vocab]; the input
-    is scaled by ``logit_scale`` before the kernel.  Kernel backend ``"hip"``
-    (``"tilelang"`` is an alias), or ``"torch"``."""
+    """Output head with the fused loss (LM:279-335).  Tied (the default): the
+    head reads the transpose of the embedding matrix and owns no parameters;
+    untied: its own [d_model, vocab] matrix from N(0, 0.02^2).  The hidden
+    states are multiplied by ``logit_scale`` before the matrix, which scales
+    the logits without touching the kernel.  ``forward(hidden)`` returns the
+    logits; with ``targets`` it returns the mean cross-entropy over the
+    targets that are not IGNORE_INDEX, through the gfx950 kernels (backend
+    ``"hip"``, alias ``"tilelang"``) or torch (``"torch"``)."""
 
     def __init__(self, cfg: HeadConfig, embedding: nn.Embedding = None):
         super().__init__()
         self.cfg = cfg
-        if cfg.tied:
-            assert embedding is not None, "tied head needs the embedding module"
-            self.embedding = [embedding]
-            self.weight = None
-        else:
-            self.embedding = None
-            self.weight = nn.Parameter(torch.empty(cfg.d_model, cfg.vocab))
-            nn.init.normal_(self.weight, std=0.02)
+        if cfg.tied and embedding is None:
+            raise ValueError("a tied head needs the embedding module")
+        # the embedding is held in a list so that it is not registered twice
+        self.embedding = [embedding] if cfg.tied else None
+        self.weight = None if cfg.tied else nn.Parameter(torch.empty(cfg.d_model, cfg.vocab).normal_(0.0, 0.02))
 
     def matrix(self):
-        if self.cfg.tied:
-            return self.embedding[0].weight.t()
-        return self.weight
+        """[d_model, vocab]: the tied embedding's transpose (a view) or own matrix."""
+        return self.embedding[0].weight.t() if self.cfg.tied else self.weight
+
+    def _loss_hip(self, rows, weight, targets):
+        # bf16 kernels: the fp32 stream and the tied matrix's transposed view
+        # become contiguous bf16 here (LM:313-323)
+        return fused_cross_entropy(rows.to(DTYPE).contiguous(), weight.to(DTYPE).contiguous(), targets,
+                                   self.cfg.chunk)
+
+    def _loss_torch(self, rows, weight, targets):
+        # sum over valid rows / their count (at least 1): an all-ignored batch
+        # gives 0, as the fused path does
+        acc = accum_dtype(rows)
+        total = F.cross_entropy(rows.to(acc) @ weight.to(acc), targets, ignore_index=IGNORE_INDEX,
+                                reduction="sum")
+        return total / (targets != IGNORE_INDEX).sum().clamp(min=1)
 
     def forward(self, hidden, targets=None, backend="hip"):
-        shape = hidden.shape
-        flat = hidden.reshape(-1, self.cfg.d_model)
+        rows = hidden.reshape(-1, self.cfg.d_model)
         if self.cfg.logit_scale != 1.0:
-            flat = flat * self.cfg.logit_scale
+            rows = rows * self.cfg.logit_scale
         weight = self.matrix()
         if targets is None:
-            return (flat @ weight).reshape(*shape[:-1], self.cfg.vocab)
-        flat_targets = targets.reshape(-1)
-        if backend in ("hip", "tilelang"):
-            # bf16 kernels: cast the fp32 stream and the (transposed view of
-            # the) tied matrix to contiguous bf16 here, as LM:313-323 does
-            flat = flat.to(DTYPE).contiguous()
-            weight = weight.to(DTYPE).contiguous()
-            return fused_cross_entropy(flat, weight, flat_targets, self.cfg.chunk)
-        if backend == "torch":
-            acc = accum_dtype(flat)
-            valid = (flat_targets != IGNORE_INDEX).sum().clamp(min=1)
-            return F.cross_entropy(flat.to(acc) @ weight.to(acc), flat_targets, ignore_index=IGNORE_INDEX,
-                                   reduction="sum") / valid
-        raise ValueError(f"unknown backend {backend!r}")
+            return (rows @ weight).reshape(*hidden.shape[:-1], self.cfg.vocab)
+        losses = {"hip": self._loss_hip, "tilelang": self._loss_hip, "torch": self._loss_torch}
+        if backend not in losses:
+            raise ValueError(f"unknown backend {backend!r}")
+        return losses[backend](rows, weight, targets.reshape(-1))
 
 
 def lm_head_flops(tokens, cfg=None):
@@ -277,154 +283,131 @@ def lm_head_flops(tokens, cfg=None):
 
 # ---------------------------------------------------------------------------
 # Harnesses (LM:338-590)
-def check_math():
-    """CPU checks of the host-side pieces and the math (LM:338-476)."""
-    passed = True
+def _online_lse(x, tile):
+    """Row log-sum-exp by the running (max, sum) recurrence over column tiles,
+    the recurrence the kernel's partials and their combine carry out."""
+    run_max = torch.full(x.shape[:1], float("-inf"), dtype=x.dtype)
+    run_sum = torch.zeros(x.shape[:1], dtype=x.dtype)
+    for block in x.split(tile, dim=1):
+        new_max = torch.maximum(run_max, block.amax(dim=1))
+        run_sum = run_sum * (run_max - new_max).exp() + (block - new_max[:, None]).exp().sum(dim=1)
+        run_max = new_max
+    return run_max + run_sum.log()
 
-    def check(label, condition):
-        nonlocal passed
-        passed &= bool(condition)
-        print(f"  {'ok  ' if condition else 'FAIL'}  {label}")
 
-    torch.manual_seed(0)
+def check_math(quiet=False) -> Report:
+    """CPU checks (the reference's check(), LM:338-476): memory saved, the
+    online log-sum-exp, the loss and gradient identities the kernels use, the
+    module's host logic."""
+    report = Report("lm head math", quiet=quiet)
     cfg = HeadConfig()
+    gen = torch.Generator().manual_seed(0)
     tokens = 8 * 2048
-    naive, fused = logits_bytes(tokens, cfg.vocab), tokens * 4
-    print(f"logits bf16 {naive / 1e6:.1f} MB; fused lse {fused / 1e6:.4f} MB")
-    check("logits alone exceed 1.5 GB", naive > 1.5e9)
-    check("fused output is under a megabyte", fused < 1e6)
-    check("one-chunk backward d_logits fit a 288 GB card many times over",
-          logits_bytes(tokens, cfg.chunk) < 4e9)
 
-    print("\nonline logsumexp recurrence")
-    x = torch.randn(64, 5000, dtype=torch.float64) * 8
-    m = torch.full((64,), float("-inf"), dtype=torch.float64)
-    s = torch.zeros(64, dtype=torch.float64)
-    for start in range(0, 5000, 128):
-        tile = x[:, start:start + 128]
-        prev = m.clone()
-        m = torch.maximum(m, tile.max(dim=1).values)
-        s = s * torch.exp(prev - m) + torch.exp(tile - m.unsqueeze(1)).sum(1)
-    err = (torch.log(s) + m - torch.logsumexp(x, dim=1)).abs().max().item()
-    check(f"matches torch.logsumexp ({err:.2e})", err < 1e-12)
+    report.section("memory at 8 x 2048 tokens")
+    logits, lse = logits_bytes(tokens, cfg.vocab), tokens * 4
+    report.note(f"bf16 logits {logits / 1e9:.2f} GB, fused forward output {lse / 1e3:.0f} KB")
+    report.expect("the logits the fused forward never stores exceed 1.5 GB", logits > 1.5e9)
+    report.expect("its output is under 1 MB", lse < 1e6)
+    report.expect("the default backward chunk (the whole vocabulary) is under 4 GB of d_logits",
+                  logits_bytes(tokens, cfg.chunk) < 4e9)
 
-    print("\ncross entropy identity")
-    logits = torch.randn(200, 500, dtype=torch.float64)
-    targets = torch.randint(0, 500, (200,))
-    manual = (torch.logsumexp(logits, dim=1) - logits[torch.arange(200), targets]).mean()
-    check("lse - target_logit == cross_entropy", (manual - F.cross_entropy(logits, targets)).abs() < 1e-12)
+    report.section("log-sum-exp")
+    x = torch.randn(48, 6000, generator=gen, dtype=torch.float64) * 10
+    err = (_online_lse(x, 256) - torch.logsumexp(x, dim=1)).abs().max().item()
+    report.expect("running (max, sum) over 256-column tiles equals logsumexp", err < 1e-11, err)
 
-    print("\ngradient identity")
-    logits = torch.randn(64, 200, dtype=torch.float64, requires_grad=True)
-    targets = torch.randint(0, 200, (64,))
-    F.cross_entropy(logits, targets).backward()
-    analytic = (torch.softmax(logits.detach(), dim=1) - F.one_hot(targets, 200).double()) / 64
-    check("d_logits == (softmax - onehot)/N", (logits.grad - analytic).abs().max() < 1e-12)
+    report.section("loss and gradient identities")
+    z = torch.randn(150, 700, generator=gen, dtype=torch.float64, requires_grad=True)
+    t = torch.randint(0, 700, (150,), generator=gen)
+    loss = F.cross_entropy(z, t)
+    by_lse = (torch.logsumexp(z, dim=1) - z.gather(1, t[:, None])[:, 0]).mean()
+    report.expect("cross-entropy = mean(lse - target logit)", (loss - by_lse).abs().item() < 1e-12)
+    (dz,) = torch.autograd.grad(loss, z)
+    closed = (torch.softmax(z.detach(), dim=1) - F.one_hot(t, 700).double()) / 150
+    report.expect("d loss / d logits = (softmax - onehot) / tokens", (dz - closed).abs().max().item() < 1e-12)
 
-    print("\nhost logic")
-    check("gather_target_logits is the target column's dot product",
-          torch.allclose(gather_target_logits(torch.eye(4), torch.arange(12.0).reshape(4, 3),
-                                              torch.tensor([2, 0, 1, 2])),
-                         torch.tensor([2.0, 3.0, 7.0, 11.0])))
+    report.section("host logic")
+    h, w = torch.randn(5, 4, generator=gen), torch.randn(4, 9, generator=gen)
+    t = torch.tensor([8, 0, 3, 3, 5])
+    report.expect("gather_target_logits picks each row's target logit",
+                  torch.allclose(gather_target_logits(h, w, t), (h @ w)[torch.arange(5), t]))
     emb = nn.Embedding(cfg.vocab, cfg.d_model)
     head = LMHead(cfg, emb)
-    check("tied head holds no parameters of its own", sum(p.numel() for p in head.parameters()) == 0)
-    check("shares the embedding matrix", head.matrix().data_ptr() == emb.weight.data_ptr())
-    check("default logit scale 1/sqrt(d_model)", abs(cfg.logit_scale - cfg.d_model ** -0.5) < 1e-15)
-    print("\n" + ("all math checks passed" if passed else "FAILURES ABOVE"))
-    return passed
+    report.expect("a tied head owns no parameters", sum(p.numel() for p in head.parameters()) == 0)
+    report.expect("and reads the embedding's own storage", head.matrix().data_ptr() == emb.weight.data_ptr())
+    report.expect("default logit scale 1/sqrt(d_model)", cfg.logit_scale == cfg.d_model ** -0.5)
+    return report.finish()
 
 
-def check_gpu(tokens=4096):
-    """lse, loss and gradients against the fp32 reference path (LM:479-520)."""
-    if not torch.cuda.is_available():
-        print("needs a HIP device")
-        return None
+def check_gpu(tokens=4096, quiet=False) -> Report:
+    """The fused head against fp32 torch on the GPU (the reference's
+    check_gpu, LM:479-520): the log-sum-exp kernel, the loss, and both
+    gradients (gate max|d| / max|ref| < 3e-2).  hidden ~ N(0, 0.1^2),
+    weight ~ N(0, 0.02^2), uniform targets, seed 0."""
+    report = Report("lm head gpu", quiet=quiet)
+    if not needs_gpu("check_gpu"):
+        return report
     cfg = HeadConfig()
-    torch.manual_seed(0)
-    hidden = (torch.randn(tokens, cfg.d_model, device="cuda", dtype=DTYPE) * 0.1).requires_grad_(True)
-    weight = (torch.randn(cfg.d_model, cfg.vocab, device="cuda", dtype=DTYPE) * 0.02).requires_grad_(True)
-    targets = torch.randint(0, cfg.vocab, (tokens,), device="cuda")
-    lse = get_kernel((tokens, cfg.d_model, cfg.vocab))(hidden, weight)
-    want = torch.logsumexp(hidden.float() @ weight.float(), dim=-1)
-    err = (lse - want).abs().max().item()
-    print(f"lse vs reference: max err {err:.3e}  {'ok' if err < 5e-3 else 'FAIL'}")
-    results = {"lse": err}
-    loss = fused_cross_entropy(hidden, weight, targets)
-    loss.backward()
-    mine = [hidden.grad.clone(), weight.grad.clone()]
-    hidden.grad = weight.grad = None
-    ref = F.cross_entropy(hidden.float() @ weight.float(), targets)
-    ref.backward()
-    theirs = [hidden.grad.clone(), weight.grad.clone()]
-    hidden.grad = weight.grad = None
-    print(f"loss {loss.item():.6f} vs {ref.item():.6f}")
-    results["loss"] = abs(loss.item() - ref.item())
-    for name, a, b in zip(("d_hidden", "d_weight"), mine, theirs):
-        rel = ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp(min=1e-6)).item()
-        results[name] = rel
-        print(f"  {name:9s} rel err {rel:.3e}  {'ok' if rel < 3e-2 else 'FAIL'}")
-    return results
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    hidden = (torch.randn(tokens, cfg.d_model, device=dev, generator=gen) * 0.1).to(DTYPE)
+    weight = (torch.randn(cfg.d_model, cfg.vocab, device=dev, generator=gen) * 0.02).to(DTYPE)
+    targets = torch.randint(0, cfg.vocab, (tokens,), device=dev, generator=gen)
+    logits = hidden.float() @ weight.float()
+
+    report.section(f"log-sum-exp kernel, {tokens} tokens x {cfg.vocab}")
+    err = (get_kernel((tokens, cfg.d_model, cfg.vocab))(hidden, weight) - torch.logsumexp(logits, dim=1)).abs().max()
+    report.expect("lse max-abs < 5e-3", err.item() < 5e-3, err.item())
+
+    report.section("fused_cross_entropy forward + backward")
+    leaves = [hidden.clone().requires_grad_(True), weight.clone().requires_grad_(True)]
+    loss = fused_cross_entropy(*leaves, targets)
+    got = torch.autograd.grad(loss, leaves)
+    exact = [hidden.float().requires_grad_(True), weight.float().requires_grad_(True)]
+    ref = F.cross_entropy(exact[0] @ exact[1], targets)
+    want = torch.autograd.grad(ref, exact)
+    gap = abs(loss.item() - ref.item())
+    report.expect("loss within 1e-3 of fp32", gap < 1e-3, gap)
+    for name, a, b in zip(("d_hidden", "d_weight"), got, want):
+        e = compare(a, b)
+        report.expect(f"{name}: max|d|/max|ref| < 3e-2", e["finite"] and e["max_rel"] < 3e-2, e["max_rel"])
+        report.note(f"{name}: rel-L2 {e['rel_l2']:.3e}")
+    return report.finish()
 
 
-def benchmark(tokens=16384):
-    """Fused vs the naive fp32 logits path, fwd + bwd (LM:523-572)."""
-    if not torch.cuda.is_available():
-        print("needs a HIP device")
-        return None
+def benchmark(tokens=16384, quiet=False) -> dict:
+    """fwd + bwd of the fused head and of fp32 torch logits + cross-entropy
+    (the reference's benchmark, LM:523-572), HIP-event timed.  Returns
+    {name: ms}."""
+    if not needs_gpu("benchmark"):
+        return {}
     cfg = HeadConfig()
-    hidden = (torch.randn(tokens, cfg.d_model, device="cuda", dtype=DTYPE) * 0.1).requires_grad_(True)
-    weight = (torch.randn(cfg.d_model, cfg.vocab, device="cuda", dtype=DTYPE) * 0.02).requires_grad_(True)
-    targets = torch.randint(0, cfg.vocab, (tokens,), device="cuda")
-
-    def time_it(fn, iters=20):
-        for _ in range(5):
-            fn()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(True), torch.cuda.Event(True)
-        start.record()
-        for _ in range(iters):
-            fn()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / iters
-
-    def clear():
-        hidden.grad = weight.grad = None
-
-    def naive():
-        F.cross_entropy(hidden.float() @ weight.float(), targets).backward()
-        clear()
-
-    def fused():
-        fused_cross_entropy(hidden, weight, targets).backward()
-        clear()
-
-    results = {"fused": time_it(fused), "naive": time_it(naive)}
-    for name, ms in sorted(results.items(), key=lambda kv: kv[1]):
-        print(f"  {name:8s} {ms:8.3f} ms")
-    return results
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    hidden = (torch.randn(tokens, cfg.d_model, device=dev, generator=gen) * 0.1).to(DTYPE).requires_grad_(True)
+    weight = (torch.randn(cfg.d_model, cfg.vocab, device=dev, generator=gen) * 0.02).to(DTYPE).requires_grad_(True)
+    targets = torch.randint(0, cfg.vocab, (tokens,), device=dev, generator=gen)
+    steps = {
+        "fused": lambda: torch.autograd.grad(fused_cross_entropy(hidden, weight, targets), (hidden, weight)),
+        "torch fp32": lambda: torch.autograd.grad(F.cross_entropy(hidden.float() @ weight.float(), targets),
+                                                  (hidden, weight)),
+    }
+    ms = {name: time_cuda(step, warmup=5, iters=20) for name, step in steps.items()}
+    if not quiet:
+        fwd, bwd = lm_head_flops(tokens, cfg)
+        for name, t in sorted(ms.items(), key=lambda kv: kv[1]):
+            print(f"  {name:10s} {t:8.3f} ms  {(fwd + bwd) / t * 1e-9:7.1f} TFLOP/s")
+    return ms
 
 
 def tune(tokens=16384):
-    """The gfx950 build has one tiling: list it (LM:575-590)."""
-    print(f"lse candidates {len(lse_configs())}: {lse_configs()}")
+    """The gfx950 build compiles one tiling (the reference autotunes
+    TileLang's space, LM:575-590): list it."""
+    print(f"lse: {len(lse_configs())} tiling(s): {lse_configs()}")
+    return {"lse": lse_configs()}
 
 
 if __name__ == "__main__":
-    parser = argparse.ArgumentParser()
-    parser.add_argument("--check", action="store_true")
-    parser.add_argument("--gpu", action="store_true")
-    parser.add_argument("--bench", action="store_true")
-    parser.add_argument("--tune", action="store_true")
-    args = parser.parse_args()
-    if not any(vars(args).values()):
-        args.check = True
-    if args.check:
-        check_math()
-    if args.gpu:
-        check_gpu()
-    if args.bench:
-        benchmark()
-    if args.tune:
-        tune()
+    sys.exit(harness_main("mimansm1_v1_amd.lm_head",
+                          {"check": check_math, "gpu": check_gpu, "bench": benchmark, "tune": tune}))

@@ -20,8 +20,8 @@ point raises; nothing falls back to another implementation.
 """
 from __future__ import annotations
 
-import argparse
 import math
+import sys
 from dataclasses import dataclass
 
 import torch
@@ -30,6 +30,8 @@ import torch.nn.functional as F
 
 from . import _lib
 from . import tuned
+from .harness import Report, compare, needs_gpu, time_cuda
+from .harness import main as harness_main
 from .wgrad import wgrad
 
 DTYPE = torch.bfloat16
@@ -252,48 +254,53 @@ class FFNConfig:
 
 
 class SwiGLU(nn.Module):
-    """Same parameters, initialisation and backends as SW:323-359; the kernel
-    backend is ``"hip"``, and the reference's name ``"tilelang"`` is an alias."""
+    """The feed-forward block (SW:323-359): raw parameters w_gate, w_up
+    [d_model, ffn] and w_down [ffn, d_model], drawn from N(0, 0.02^2) in that
+    order, w_down's deviation divided by sqrt(2 * 27 layers).  Backends:
+    ``"hip"`` (the gfx950 kernels; the reference's name ``"tilelang"`` is an
+    alias), ``"torch"`` (eager, in the input's dtype) and ``"math"`` (fp32)."""
+
+    _STD = 0.02
 
     def __init__(self, cfg: FFNConfig):
         super().__init__()
         self.cfg = cfg
-        self.w_gate = nn.Parameter(torch.empty(cfg.d_model, cfg.ffn_hidden))
-        self.w_up = nn.Parameter(torch.empty(cfg.d_model, cfg.ffn_hidden))
-        self.w_down = nn.Parameter(torch.empty(cfg.ffn_hidden, cfg.d_model))
-        std = 0.02
-        nn.init.normal_(self.w_gate, std=std)
-        nn.init.normal_(self.w_up, std=std)
-        nn.init.normal_(self.w_down, std=std / math.sqrt(2 * 27))
+        d, f = cfg.d_model, cfg.ffn_hidden
+        for name, shape, std in (("w_gate", (d, f), self._STD), ("w_up", (d, f), self._STD),
+                                 ("w_down", (f, d), self._STD / math.sqrt(2 * 27))):
+            self.register_parameter(name, nn.Parameter(torch.empty(shape).normal_(0.0, std)))
+
+    def _weights(self, dtype=None):
+        ws = (self.w_gate, self.w_up, self.w_down)
+        return ws if dtype is None else tuple(w.to(dtype) for w in ws)
+
+    def _run_hip(self, rows, out_dtype):
+        # the kernels take bf16 operands: the fp32 residual stream and the raw
+        # parameters (which autocast does not reach) are cast here (SW:335-343)
+        return fused_swiglu(rows.to(DTYPE).contiguous(), *self._weights(DTYPE)).to(out_dtype)
+
+    def _run_torch(self, rows, out_dtype):
+        w_gate, w_up, w_down = self._weights()
+        return (F.silu(rows @ w_gate) * (rows @ w_up)) @ w_down
+
+    def _run_math(self, rows, out_dtype):
+        return reference(rows, *self._weights()).to(out_dtype)
 
     def forward(self, x, backend=None):
-        cfg = self.cfg
-        backend = backend or cfg.backend
-        shape = x.shape
-        flat = x.reshape(-1, cfg.d_model)
-        if backend in ("hip", "tilelang"):
-            # bf16 kernels: the fp32 residual stream and raw parameters are cast
-            # here, as the reference does (SW:335-343)
-            out = fused_swiglu(flat.to(DTYPE).contiguous(), self.w_gate.to(DTYPE),
-                               self.w_up.to(DTYPE), self.w_down.to(DTYPE))
-            out = out.to(x.dtype)
-        elif backend == "torch":
-            out = (F.silu(flat @ self.w_gate) * (flat @ self.w_up)) @ self.w_down
-        elif backend == "math":
-            gate = flat.float() @ self.w_gate.float()
-            up = flat.float() @ self.w_up.float()
-            out = ((gate * torch.sigmoid(gate)) * up) @ self.w_down.float()
-            out = out.to(x.dtype)
-        else:
+        backend = backend or self.cfg.backend
+        runs = {"hip": self._run_hip, "tilelang": self._run_hip, "torch": self._run_torch,
+                "math": self._run_math}
+        if backend not in runs:
             raise ValueError(f"unknown backend {backend!r}")
-        return out.reshape(shape)
+        return runs[backend](x.reshape(-1, self.cfg.d_model), x.dtype).reshape(x.shape)
 
 
 def reference(x, w_gate, w_up, w_down):
-    """The fp32 reference (SW:362-365)."""
-    gate = x.float() @ w_gate.float()
-    up = x.float() @ w_up.float()
-    return ((gate * torch.sigmoid(gate)) * up) @ w_down.float()
+    """The fp32 math of the block (SW:362-365): (silu(x Wg) * (x Wu)) Wd with
+    silu(g) = g * sigmoid(g), evaluated in that order."""
+    xf = x.float()
+    g = xf @ w_gate.float()
+    return (g * g.sigmoid() * (xf @ w_up.float())) @ w_down.float()
 
 
 def swiglu_flops(tokens, cfg=None):
@@ -304,160 +311,127 @@ def swiglu_flops(tokens, cfg=None):
 
 # ---------------------------------------------------------------------------
 # Harnesses (SW:368-638)
-def check_math():
-    """CPU checks of the host-side pieces (SW:368-494)."""
-    passed = True
+def check_math(quiet=False) -> Report:
+    """CPU checks (the reference's check(), SW:368-494): what the fusion saves,
+    the gfx950 tiling, the SiLU derivative the gradient kernel uses, the
+    module."""
+    report = Report("swiglu math", quiet=quiet)
+    cfg = FFNConfig()
+    gen = torch.Generator().manual_seed(0)
+    tokens = 8 * 2048
 
-    def check(label, condition):
-        nonlocal passed
-        passed &= bool(condition)
-        print(f"  {'ok  ' if condition else 'FAIL'}  {label}")
+    report.section("intermediate HBM traffic of one forward (8 x 2048 tokens)")
+    per_tensor = tokens * cfg.ffn_hidden * 2
+    # unfused: gate and up written, read by silu(gate) * up, act written, read by down
+    unfused, fused = 6 * per_tensor, 2 * per_tensor
+    report.note(f"[T, F] bf16 tensor {per_tensor / 1e6:.1f} MB: unfused {unfused / 1e6:.0f} MB, fused {fused / 1e6:.0f} MB")
+    report.expect("the fused epilogue cuts it to a third", unfused == 3 * fused)
 
+    report.section("gfx950 tiling")
+    t = GATE_UP_TILES
+    report.expect("defaults are the compiled tilings", gate_up_configs() == [t] and grad_configs() == [GRAD_TILES])
+    report.expect("d_model and ffn are whole tiles", cfg.ffn_hidden % t["block_N"] == 0 and cfg.d_model % t["block_K"] == 0)
+    ring = t["stages"] * t["block_K"] * (t["block_M"] + 2 * t["block_N"]) * 2
+    report.expect("the LDS ring fits 160 KiB", ring <= 160 * 1024, f"{ring // 1024} KiB")
+
+    report.section("SiLU derivative (the gradient kernel's formula)")
+    g = (torch.randn(4096, generator=gen, dtype=torch.float64) * 4).requires_grad_(True)
+    (auto,) = torch.autograd.grad(F.silu(g).sum(), g)
+    sg = torch.sigmoid(g.detach())
+    closed = sg + g.detach() * sg * (1 - sg)
+    err = (auto - closed).abs().max().item()
+    report.expect("d silu(g)/dg = s + g s (1 - s), s = sigmoid(g)", err < 1e-12, err)
+    zero = torch.zeros(1, dtype=torch.float64, requires_grad=True)
+    (at_zero,) = torch.autograd.grad(F.silu(zero).sum(), zero)
+    report.expect("silu(0) = 0 with slope 1/2", F.silu(zero).item() == 0.0 and at_zero.item() == 0.5)
+
+    report.section("module")
     torch.manual_seed(0)
+    block = SwiGLU(cfg)
+    count = sum(p.numel() for p in block.parameters())
+    report.expect("parameter count 3 * d_model * ffn", count == cfg.params, count)
+    x = torch.randn(3, 11, cfg.d_model, generator=gen)
+    y = block(x, backend="torch")
+    report.expect("output keeps the input's shape", tuple(y.shape) == tuple(x.shape))
+    gap = (y - block(x, backend="math")).abs().max().item()
+    report.expect("eager and fp32 backends agree", gap < 1e-4, gap)
+    x.requires_grad_(True)
+    block(x, backend="torch").square().mean().backward()
+    report.expect("gradients reach the input and every weight, finite",
+                  all(t.grad is not None and bool(torch.isfinite(t.grad).all()) for t in (x, *block.parameters())))
+    return report.finish()
+
+
+def check_gpu(tokens=4096, quiet=False) -> Report:
+    """The fused op against the fp32 math on the GPU (the reference's
+    check_gpu, SW:497-556, gate max|d| / max|ref| < 3e-2): the fused
+    activation kernel, then fused_swiglu's output and four gradients.  x ~
+    N(0,1), weights ~ N(0, 0.02^2), seed 0."""
+    report = Report("swiglu gpu", quiet=quiet)
+    if not needs_gpu("check_gpu"):
+        return report
     cfg = FFNConfig()
-    layers, tokens = 27, 8 * 2048
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    draw = lambda *shape, scale=1.0: (torch.randn(*shape, device=dev, generator=gen) * scale).to(DTYPE)
+    x = draw(tokens, cfg.d_model)
+    weights = [draw(cfg.d_model, cfg.ffn_hidden, scale=0.02), draw(cfg.d_model, cfg.ffn_hidden, scale=0.02),
+               draw(cfg.ffn_hidden, cfg.d_model, scale=0.02)]
+    d_out = draw(tokens, cfg.d_model)
 
-    print("hbm traffic, one ffn forward at 8x2048 tokens")
-    unfused = 6 * tokens * cfg.ffn_hidden * 2
-    fused = 2 * tokens * cfg.ffn_hidden * 2
-    print(f"    unfused {unfused / 1e6:7.1f} MB, fused act {fused / 1e6:7.1f} MB")
-    check("fusion removes two thirds of the intermediate traffic", fused * 3 == unfused)
+    report.section(f"gate/up kernel, {tokens} tokens")
+    act = get_kernel("gate_up", tokens, cfg.d_model, cfg.ffn_hidden)(x, weights[0], weights[1])
+    g = x.float() @ weights[0].float()
+    e = compare(act, g * g.sigmoid() * (x.float() @ weights[1].float()))
+    report.expect("act: max|d|/max|ref| < 2e-2", e["finite"] and e["max_rel"] < 2e-2, e["max_rel"])
 
-    print("\ntilings (gfx950)")
-    check("gate_up default is compiled", GATE_UP_TILES in gate_up_configs())
-    check("grad default is compiled", GRAD_TILES in grad_configs())
-    check("ffn and d_model fit the gate/up tile",
-          cfg.ffn_hidden % GATE_UP_TILES["block_N"] == 0 and cfg.d_model % GATE_UP_TILES["block_K"] == 0)
-    lds = GATE_UP_TILES["stages"] * 2 * GATE_UP_TILES["block_K"] * (
-        GATE_UP_TILES["block_M"] + 2 * GATE_UP_TILES["block_N"])
-    check(f"gate/up ring fits LDS ({lds // 1024} KiB of 160)", lds <= 160 * 1024)
-
-    print("\nsilu derivative")
-    z = torch.randn(2000, dtype=torch.float64) * 3
-    z.requires_grad_(True)
-    F.silu(z).sum().backward()
-    sig = torch.sigmoid(z.detach())
-    analytic = sig * (1 + z.detach() * (1 - sig))
-    err = (z.grad - analytic).abs().max().item()
-    check(f"matches sigmoid(z)*(1+z*(1-sigmoid(z))) ({err:.2e})", err < 1e-12)
-    check("silu(0)=0 and dsilu(0)=0.5",
-          abs(F.silu(torch.zeros(1)).item()) < 1e-12 and abs(torch.sigmoid(torch.zeros(1)).item() - 0.5) < 1e-12)
-
-    print("\nmodule")
-    ffn = SwiGLU(cfg)
-    n = sum(p.numel() for p in ffn.parameters())
-    check(f"parameters {n:,} == 3*{cfg.d_model}*{cfg.ffn_hidden}", n == cfg.params)
-    x = torch.randn(2, 16, cfg.d_model)
-    y = ffn(x, backend="torch")
-    check(f"shape {tuple(x.shape)} -> {tuple(y.shape)}", y.shape == x.shape)
-    err = (y - ffn(x, backend="math")).abs().max().item()
-    check(f"torch and fp32 reference agree ({err:.2e})", err < 1e-4)
-    x = torch.randn(2, 8, cfg.d_model, requires_grad=True)
-    ffn(x, backend="torch").sum().backward()
-    check("finite gradients everywhere",
-          torch.isfinite(x.grad).all() and all(torch.isfinite(p.grad).all() for p in ffn.parameters()))
-
-    print("\n" + ("all math checks passed" if passed else "FAILURES ABOVE"))
-    return passed
+    report.section("fused_swiglu forward + backward")
+    leaves = [t.clone().requires_grad_(True) for t in (x, *weights)]
+    out = fused_swiglu(*leaves)
+    got = (out,) + torch.autograd.grad(out, leaves, d_out)
+    exact = [t.detach().float().requires_grad_(True) for t in (x, *weights)]
+    ref_out = reference(*exact)
+    want = (ref_out,) + torch.autograd.grad(ref_out, exact, d_out.float())
+    for name, a, b in zip(("out", "d_x", "d_w_gate", "d_w_up", "d_w_down"), got, want):
+        e = compare(a, b)
+        report.expect(f"{name}: max|d|/max|ref| < 3e-2", e["finite"] and e["max_rel"] < 3e-2, e["max_rel"])
+        report.note(f"{name}: rel-L2 {e['rel_l2']:.3e}")
+    return report.finish()
 
 
-def check_gpu(tokens=4096):
-    """The fused op against the fp32 reference on the GPU (SW:497-556)."""
-    if not torch.cuda.is_available():
-        print("needs a HIP device")
-        return None
+def benchmark(tokens=16384, quiet=False) -> dict:
+    """fwd + bwd of the fused op and of eager torch at `tokens` tokens (the
+    reference's benchmark, SW:559-610), HIP-event timed.  Returns {name: ms}."""
+    if not needs_gpu("benchmark"):
+        return {}
     cfg = FFNConfig()
-    torch.manual_seed(0)
-    dev = "cuda"
-    x = torch.randn(tokens, cfg.d_model, device=dev, dtype=DTYPE, requires_grad=True)
-    wg = (torch.randn(cfg.d_model, cfg.ffn_hidden, device=dev, dtype=DTYPE) * 0.02).requires_grad_(True)
-    wu = (torch.randn(cfg.d_model, cfg.ffn_hidden, device=dev, dtype=DTYPE) * 0.02).requires_grad_(True)
-    wd = (torch.randn(cfg.ffn_hidden, cfg.d_model, device=dev, dtype=DTYPE) * 0.02).requires_grad_(True)
-    grad_out = torch.randn(tokens, cfg.d_model, device=dev, dtype=DTYPE)
-    act = get_kernel("gate_up", tokens, cfg.d_model, cfg.ffn_hidden)(x, wg, wu)
-    want_act = F.silu(x.float() @ wg.float()) * (x.float() @ wu.float())
-    rel = ((act.float() - want_act).abs().max() / want_act.abs().max()).item()
-    print(f"fused activation vs fp32: rel err {rel:.3e}  {'ok' if rel < 2e-2 else 'FAIL'}")
-    results = {"act": rel}
-    out = fused_swiglu(x, wg, wu, wd)
-    out.backward(grad_out, retain_graph=True)
-    mine = [t.grad.clone() for t in (x, wg, wu, wd)]
-    for t in (x, wg, wu, wd):
-        t.grad = None
-    want = reference(x, wg, wu, wd).to(DTYPE)
-    want.backward(grad_out)
-    theirs = [t.grad.clone() for t in (x, wg, wu, wd)]
-    for name, a, b in zip(("out", "d_x", "d_w_gate", "d_w_up", "d_w_down"), [out] + mine, [want] + theirs):
-        rel = ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp(min=1e-6)).item()
-        results[name] = rel
-        print(f"  {name:9s} rel err {rel:.3e}  {'ok' if rel < 3e-2 else 'FAIL'}")
-    return results
-
-
-def benchmark(tokens=16384):
-    """Fused op vs eager torch, fwd + bwd (SW:559-610)."""
-    if not torch.cuda.is_available():
-        print("needs a HIP device")
-        return None
-    cfg = FFNConfig()
-    dev = "cuda"
-    x = torch.randn(tokens, cfg.d_model, device=dev, dtype=DTYPE, requires_grad=True)
-    wg = torch.randn(cfg.d_model, cfg.ffn_hidden, device=dev, dtype=DTYPE, requires_grad=True)
-    wu = torch.randn(cfg.d_model, cfg.ffn_hidden, device=dev, dtype=DTYPE, requires_grad=True)
-    wd = torch.randn(cfg.ffn_hidden, cfg.d_model, device=dev, dtype=DTYPE, requires_grad=True)
-    grad_out = torch.randn(tokens, cfg.d_model, device=dev, dtype=DTYPE)
-    flops = swiglu_flops(tokens, cfg)
-
-    def time_it(fn, iters=30):
-        for _ in range(10):
-            fn()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(True), torch.cuda.Event(True)
-        start.record()
-        for _ in range(iters):
-            fn()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / iters
-
-    def clear():
-        for t in (x, wg, wu, wd):
-            t.grad = None
-
-    def eager():
-        ((F.silu(x @ wg) * (x @ wu)) @ wd).backward(grad_out, retain_graph=True)
-        clear()
-
-    def hip():
-        fused_swiglu(x, wg, wu, wd).backward(grad_out, retain_graph=True)
-        clear()
-
-    results = {"eager": time_it(eager), "hip": time_it(hip)}
-    for name, ms in sorted(results.items(), key=lambda kv: kv[1]):
-        print(f"  {name:10s} {ms:8.3f} ms   {flops / ms * 1e-9:7.1f} TFLOP/s")
-    return results
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    leaf = lambda *shape: torch.randn(*shape, device=dev, dtype=DTYPE, generator=gen).requires_grad_(True)
+    x = leaf(tokens, cfg.d_model)
+    wg, wu, wd = leaf(cfg.d_model, cfg.ffn_hidden), leaf(cfg.d_model, cfg.ffn_hidden), leaf(cfg.ffn_hidden, cfg.d_model)
+    d_out = torch.randn(tokens, cfg.d_model, device=dev, dtype=DTYPE, generator=gen)
+    leaves = (x, wg, wu, wd)
+    steps = {
+        "hip": lambda: torch.autograd.grad(fused_swiglu(*leaves), leaves, d_out),
+        "eager": lambda: torch.autograd.grad((F.silu(x @ wg) * (x @ wu)) @ wd, leaves, d_out),
+    }
+    ms = {name: time_cuda(step, warmup=10, iters=30) for name, step in steps.items()}
+    if not quiet:
+        flops = swiglu_flops(tokens, cfg)
+        for name, t in sorted(ms.items(), key=lambda kv: kv[1]):
+            print(f"  {name:6s} {t:8.3f} ms  {flops / t * 1e-9:7.1f} TFLOP/s")
+    return ms
 
 
 def tune(tokens=16384):
-    """The gfx950 build has one tiling per kernel: list them (SW:613-632)."""
-    print(f"gate_up candidates {len(gate_up_configs())}: {gate_up_configs()}")
-    print(f"grad candidates    {len(grad_configs())}: {grad_configs()}")
+    """The gfx950 build compiles one tiling per kernel (the reference
+    autotunes TileLang's space, SW:613-632): list them."""
+    for name, space in (("gate_up", gate_up_configs()), ("grad", grad_configs())):
+        print(f"{name}: {len(space)} tiling(s): {space}")
+    return {"gate_up": gate_up_configs(), "grad": grad_configs()}
 
 
 if __name__ == "__main__":
-    parser = argparse.ArgumentParser()
-    parser.add_argument("--check", action="store_true")
-    parser.add_argument("--gpu", action="store_true")
-    parser.add_argument("--bench", action="store_true")
-    parser.add_argument("--tune", action="store_true")
-    args = parser.parse_args()
-    if not any(vars(args).values()):
-        args.check = True
-    if args.check:
-        check_math()
-    if args.gpu:
-        check_gpu()
-    if args.bench:
-        benchmark()
-    if args.tune:
-        tune()
+    sys.exit(harness_main("mimansm1_v1_amd.swiglu",
+                          {"check": check_math, "gpu": check_gpu, "bench": benchmark, "tune": tune}))

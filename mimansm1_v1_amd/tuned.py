@@ -94,21 +94,20 @@ def config_of(kernel):
 
 
 def summary(paths=None) -> str:
-    lines = []
+    """What each store holds, one line per record:
+    ``<store>  <device>  <kernel>  <shape>  key=value ...``."""
+    rows = []
     for path in paths or (STORE, TABLE):
         data = _read(path)
-        if not data:
-            lines.append(f"{path}: nothing tuned")
-            continue
-        lines.append(f"{path}")
-        for device, entries in sorted(data.items()):
-            lines.append(f"  {device}  ({len(entries)} kernels)")
-            for key, config in sorted(entries.items()):
-                kernel, shape = key.split(":", 1)
-                terse = " ".join(f"{k}={v}" for k, v in sorted(config.items()))
-                lines.append(f"    {kernel:14s} [{shape}]")
-                lines.append(f"      {terse}")
-    return "\n".join(lines)
+        records = [(device, key, config) for device, entries in sorted(data.items())
+                   for key, config in sorted(entries.items())]
+        if not records:
+            rows.append(f"{path}  (no records)")
+        for device, key, config in records:
+            kernel, _, shape = key.partition(":")
+            fields = " ".join(f"{name}={value}" for name, value in sorted(config.items()))
+            rows.append(f"{path}  {device}  {kernel}  ({shape})  {fields}")
+    return "\n".join(rows)
 
 
 if __name__ == "__main__":

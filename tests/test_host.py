@@ -29,7 +29,27 @@ def test_surface_mirrors_reference_module():
 
 
 def test_check_math_passes():
-    assert A.check_math()
+    """The drop-in modules' CPU harnesses (the reference's check()) hold."""
+    from mimansm1_v1_amd import lm_head, swiglu
+    for module in (A, swiglu, lm_head):
+        report = module.check_math(quiet=True)
+        assert report.ok and len(report.outcomes) >= 8, (module.__name__, report.failures())
+
+
+def test_harness_cli(capsys):
+    """`python -m mimansm1_v1_amd.attention [check|tune|...]`, also with the
+    reference's --flags; an unknown action is an error."""
+    from mimansm1_v1_amd import harness
+    calls = []
+    actions = {"check": lambda: calls.append("check"), "tune": lambda: calls.append("tune")}
+    assert harness.main("m", actions, []) == 0 and calls == ["check"]
+    calls.clear()
+    assert harness.main("m", actions, ["tune", "--check"]) == 0 and calls == ["check", "tune"]
+    failing = harness.Report("x", quiet=True)
+    failing.expect("never", False)
+    assert harness.main("m", {"check": lambda: failing}, []) == 1
+    with pytest.raises(SystemExit):
+        harness.main("m", actions, ["bogus"])
 
 
 def test_attn_config_asserts():
@@ -115,7 +135,10 @@ def test_tuned_store_roundtrip_and_precedence(tmp_path, monkeypatch):
     assert list(data) == ["gfx950-256cu"]
     assert list(data["gfx950-256cu"]) == ["attention_fwd:1,10,64,128,True,5"]
     text = tuned.summary()
-    assert "gfx950-256cu  (1 kernels)" in text and "waves=8" in text
+    line = [ln for ln in text.splitlines() if "attention_fwd" in ln and "store.json" in ln]
+    assert len(line) == 1 and "gfx950-256cu" in line[0] and "(1,10,64,128,True,5)" in line[0]
+    assert "waves=8" in line[0]
+    assert "(no records)" in tuned.summary([tmp_path / "missing.json"])
     assert tuned.config_of(A.FwdKernel(shape, A.FWD_TILES)) == A.FWD_TILES
     assert tuned.device_key() == "no-hip"
 
