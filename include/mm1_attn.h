@@ -40,7 +40,10 @@ extern "C" {
 #define MM1_E_TILES (-7)       /* tiling index out of range (see mm1_attn_tile_count) */
 #define MM1_E_LAYOUT (-8)      /* the workspace holds no dK/dV partial sums of this shape and
                                   dK/dV tiling (see mm1_attn_bwd_dkdv_reduce) */
+#define MM1_E_SCRATCH (-9)     /* shape too large for mm1_attn_bwd_noalloc's static scratch */
 
+/* Bytes of device memory mm1_attn_bwd_noalloc holds per device (see there). */
+#define MM1_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
 
 /* Kernel kinds for the tiling queries below. */
 #define MM1_TILES_FWD 0
@@ -87,6 +90,24 @@ int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
                  void* workspace, size_t workspace_bytes,
                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                  void* stream);
+
+/* mm1_attn_bwd without a workspace argument, for callers that cannot
+ * allocate device memory around the call: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  No counterpart in the
+ * reference.  It calls no allocating routine: the dK/dV partial sums of the
+ * default tilings go to a static device array of MM1_NOALLOC_SCRATCH_BYTES
+ * (128 MiB) that each device the library runs on holds until the process
+ * ends.  mm1_attn_bwd_noalloc_scratch_size() gives the bytes a shape needs
+ * (2 * G * B * split_keys * Hkv * D * 4 at most; about 107 MiB at the
+ * training shapes of 16,384 tokens); a shape needing more returns
+ * MM1_E_SCRATCH.  Every call on one device shares that device's array:
+ * calls that overlap on one device (several streams or host threads) race
+ * and must be serialised by the caller.  Outputs equal mm1_attn_bwd's
+ * (default tilings) bitwise. */
+int mm1_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* dO,
+                         const float* lse2, const float* delta, void* dq, void* dk, void* dv,
+                         int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream);
+size_t mm1_attn_bwd_noalloc_scratch_size(int B, int S, int H, int Hkv, int D, int causal);
 
 /* The stages of the backward, for callers that schedule or time them
  * separately (same arguments and checks as mm1_attn_bwd).  mm1_attn_bwd runs

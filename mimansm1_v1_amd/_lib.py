@@ -31,6 +31,9 @@ SIGNATURES = {
     "mm1_attn_bwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
                                     _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
                                     _c_int, _c_int, _vp]),
+    "mm1_attn_bwd_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_bwd_noalloc_scratch_size": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "mm1_attn_bwd_f32_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "mm1_attn_bwd_f32": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),

@@ -32,6 +32,7 @@ hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void
                          int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
                          int dkdv_variant, hipStream_t stream);
 size_t bwd_f32_workspace_bytes(int B, int S, int H, int Hkv);
+size_t bwd_partials_bytes(int B, int S, int H, int Hkv, bool causal, int variant);
 hipError_t launch_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
                           const float* lse2, const float* delta, float* dq, float* dk, float* dv,
                           void* workspace, int B, int S, int H, int Hkv, bool causal, float sm_scale,
@@ -169,6 +170,36 @@ bool layout_matches(const WsLayout& want) {
 
 int from_hip(hipError_t e) { return e == hipSuccess ? MM1_OK : static_cast<int>(e); }
 
+// ---------------------------------------------------------------------------
+// Scratch of mm1_attn_bwd_noalloc: the dK/dV partial sums of the default
+// backward tilings live in this static device array instead of a workspace
+// the caller allocates.  Every device the library runs on holds its own copy
+// (MM1_NOALLOC_SCRATCH_BYTES) until the process ends.  In host code `scratch`
+// is only a handle: its device address on the current device comes from
+// hipGetSymbolAddress, taken once per device and kept in g_scratch_addr.
+static __device__ __align__(256) char scratch[MM1_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices];
+
+// The current device's address of `scratch` (MM1_OK), or an error code.
+int scratch_addr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return from_hip(e);
+  if (dev < 0 || dev >= kMaxDevices) return MM1_E_SHAPE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return from_hip(e);
+    if (!p) return MM1_E_NULL;
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return MM1_OK;
+}
 
 }  // namespace
 
@@ -379,6 +410,33 @@ int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* 
                 D, causal, sm_scale, dq_tiles, dkdv_tiles, stream);
 }
 
+int mm1_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* dO,
+                         const float* lse2, const float* delta, void* dq, void* dk, void* dv,
+                         int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream) {
+  if (!q || !k || !v || !dO || !lse2 || !delta || !dq || !dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) || !aligned16(dk) ||
+      !aligned16(dv))
+    return MM1_E_ALIGN;
+  const size_t need = mm1::bwd_partials_bytes(B, S, H, Hkv, causal != 0, 0);
+  if (need > MM1_NOALLOC_SCRATCH_BYTES) return MM1_E_SCRATCH;
+  void* ws = nullptr;
+  if (need > 0 && (rc = scratch_addr(&ws)) != MM1_OK) return rc;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = from_hip(mm1::launch_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, ws, B, S, H, Hkv, causal != 0, sm_scale,
+                                     0, st));
+  if (rc) return rc;
+  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, ws, dk, dv, B, S, H, Hkv, causal != 0,
+                                     sm_scale, 0, 0, st));
+}
+
+size_t mm1_attn_bwd_noalloc_scratch_size(int B, int S, int H, int Hkv, int D, int causal) {
+  if (check_shape(B, S, H, Hkv, D) != MM1_OK) return 0;
+  return mm1::bwd_partials_bytes(B, S, H, Hkv, causal != 0, 0);
+}
+
 size_t mm1_attn_bwd_f32_workspace_size(int B, int S, int H, int Hkv, int D) {
   if (check_shape(B, S, H, Hkv, D) != MM1_OK) return 0;
   return mm1::bwd_f32_workspace_bytes(B, S, H, Hkv);
@@ -564,6 +622,9 @@ const char* mm1_attn_strerror(int code) {
     case MM1_E_SCALE: return "mm1_attn: sm_scale must be a positive finite number";
     case MM1_E_ALIGN: return "mm1_attn: tensor pointers must be 16-byte aligned";
     case MM1_E_TILES: return "mm1_attn: tiling index out of range (see mm1_attn_tile_count)";
+    case MM1_E_SCRATCH:
+      return "mm1_attn: the dK/dV partial sums of this shape exceed the static scratch of "
+             "mm1_attn_bwd_noalloc (MM1_NOALLOC_SCRATCH_BYTES); use mm1_attn_bwd with a workspace";
     case MM1_E_LAYOUT:
       return "mm1_attn: the workspace holds no dK/dV partial sums of this shape and dK/dV tiling "
              "(run mm1_attn_bwd_dkdv with the same arguments first)";

@@ -54,7 +54,7 @@ def test_version_matches_header(lib):
 
 def test_error_codes_and_messages(lib):
     codes = dict(re.findall(r"#define (MM1_E_\w+) \((-\d+)\)", HEADER.read_text()))
-    assert len(codes) == 8
+    assert len(codes) == 9
     for name, code in codes.items():
         msg = lib.mm1_attn_strerror(int(code)).decode()
         assert msg.startswith("mm1_attn:") and "unknown" not in msg, name
@@ -138,6 +138,25 @@ def test_reduce_refuses_a_workspace_without_matching_partials(lib):
                                      2, 100, 10, 2, 128, 1, 0.1, 9, None) == -7
     assert lib.mm1_attn_bwd_dkdv_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, need,
                                        2, 100, 10, 2, 128, 1, 0.1, 9, None) == -7
+
+
+def test_noalloc_refuses_shapes_beyond_its_scratch(lib):
+    """mm1_attn_bwd_noalloc checks its arguments and the static scratch's
+    size before any device call: MM1_E_SCRATCH for a shape whose dK/dV partial
+    sums exceed MM1_NOALLOC_SCRATCH_BYTES, the usual codes otherwise."""
+    cap = 128 << 20
+    assert f"(size_t)128 << 20" in HEADER.read_text()
+    need = lib.mm1_attn_bwd_noalloc_scratch_size
+    for B, S in ((8, 2048), (2, 8192), (4, 4096), (1, 16384)):
+        assert 0 < need(B, S, 10, 2, 128, 1) <= cap, (B, S)
+    assert need(2, 8192, 4, 4, 128, 1) == 0          # G = 1: no partials
+    assert need(1, 32768, 10, 2, 128, 1) > cap      # 214 MiB of partials
+    args = (FAKE,) * 9
+    assert lib.mm1_attn_bwd_noalloc(*args, 1, 32768, 10, 2, 128, 1, 0.1, None) == -9
+    assert lib.mm1_attn_bwd_noalloc(None, *args[1:], 2, 64, 10, 2, 128, 1, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_noalloc(*args, 2, 64, 10, 3, 128, 1, 0.1, None) == -2
+    assert lib.mm1_attn_bwd_noalloc(*args, 2, 64, 10, 2, 128, 1, 0.0, None) == -5
+    assert b"static scratch" in lib.mm1_attn_strerror(-9)
 
 
 def test_no_environment_switch_changes_the_tiling(lib, monkeypatch):
