@@ -43,11 +43,14 @@
 #define MM1_DQ_PREFETCH 1
 #endif
 
-// 1: the dK/dV kernel's S / dP products read each Q / dO row fragment one
-// k-step ahead of its product (dK/dV 0.2% faster than 0, a repeatable
-// near-tie: the kernel waits on the LDS queue, not on read latency).
-#ifndef MM1_DKDV_PREFETCH
-#define MM1_DKDV_PREFETCH 1
+// Products by which the dK/dV kernel's LDS operand reads run ahead of their
+// products: Q / dO row fragments of the S / dP products, transposed dO / Q
+// fragments (two reads each) of the dV^T / dK^T accumulations.
+#ifndef MM1_DKDV_PF_ROWS
+#define MM1_DKDV_PF_ROWS 2
+#endif
+#ifndef MM1_DKDV_PF_TR
+#define MM1_DKDV_PF_TR 2
 #endif
 
 namespace mm1 {
@@ -356,6 +359,31 @@ __device__ __forceinline__ void unroll_while(F&& f) {
   }
 }
 
+// Eight products in order: product i takes the A fragment load(i), read PF
+// products ahead of it, and after product i comes between(i).  Scheduling
+// barriers keep that order, so the VALU work handed to between() runs while
+// the products in flight occupy the matrix core (the compiler would
+// otherwise gather it after the last product) and every read stays PF
+// products ahead of its use.
+template <int PF, class Load, class Mma, class Between>
+__device__ __forceinline__ void chain8(Load&& load, Mma&& mma, Between&& between) {
+  bf16x8 fa[PF + 1];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    fa[i] = load(i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i + PF < 8) fa[(i + PF) % (PF + 1)] = load(i + PF);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(i, fa[i % (PF + 1)]);
+    __builtin_amdgcn_sched_barrier(0);
+    between(i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // dK, dV, software-pipelined across the two roles of a pair.
 //
@@ -554,10 +582,11 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     if constexpr (KB == 2) mfma32_acc(a, bb, c);
     else c = mfma32(a, bb, c);
   };
-  // KB = 1 computes S one segment ahead (snext) and keeps dP of two
-  // segments (dpn, dpp), so that a wave's VALU work has products of its own
-  // to run under; KB = 2 has no registers for that and relies on the
-  // accumulation products of the previous tiles instead.
+  // KB = 1 computes S one segment ahead (snext), so that the P wave's
+  // exponentials run between the products of the next S; KB = 2 has no
+  // registers for that and computes S and its exponentials in turn.  The dS
+  // wave computes dS(s-1) between the products of dK^T += Q^T dS(s-2) and
+  // dP(s) last, for the next segment.
   constexpr bool AHEAD = KB == 1;
   bf16x8 pb[KB][2];    // P wave: P(s-1) as the B operand of dV^T
   f32x16 snext[KB];    // P wave: S(s), computed one segment ahead (AHEAD)
@@ -569,33 +598,32 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // S = Q K^T / dP = dO V^T of one tile, per key block (D layout: register r
   // holds query 8*(r/4) + 4*h + (r%4) of the tile, lane l32 holds key
   // kw0 + 32*kb + l32); each row fragment is read once for all key blocks
-  auto product = [&](const char* t, f32x16 (&sacc)[KB]) MM1_INLINE {
+  auto product = [&](const char* t, f32x16 (&sacc)[KB], auto&& between) MM1_INLINE {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) sacc[kb] = zero16();
-#if MM1_DKDV_PREFETCH
-    // the next fragment's read is issued before this step's products; VALU
-    // work (the P wave's exp of the previous tile) may still move in between
-    bf16x8 fa[2];
-    fa[0] = rows_a(t, lb, 0, 0);
+    chain8<MM1_DKDV_PF_ROWS>(
+        [&](int ks) MM1_INLINE { return rows_a(t, lb, 0, ks); },
+        [&](int ks, const bf16x8& fa) MM1_INLINE {
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      if (ks + 1 < 8) fa[(ks + 1) & 1] = rows_a(t, lb, 0, ks + 1);
-      __builtin_amdgcn_sched_barrier(0x406);
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32(fa[ks & 1], breg[kb][ks], sacc[kb]);
-      __builtin_amdgcn_sched_barrier(0x406);
-    }
-#else
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 fa = rows_a(t, lb, 0, ks);
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32(fa, breg[kb][ks], sacc[kb]);
-    }
-#endif
+          for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32(fa, breg[kb][ks], sacc[kb]);
+        },
+        between);
   };
+  // dV^T += dO^T P (P wave) / dK^T += Q^T dS (dS wave) of one tile: product
+  // i = 4*kh + db takes the transposed fragment (db, kh) of tile t and the B
+  // operand bop[kb][kh]
+  auto accumulate_tile = [&](const char* t, const bf16x8 (&bop)[KB][2], auto&& between) MM1_INLINE {
+    chain8<MM1_DKDV_PF_TR>(
+        [&](int i) MM1_INLINE { return tr_a(t, lb, i & 3, i >> 2); },
+        [&](int i, const bf16x8& a) MM1_INLINE {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) accumulate(acc[kb][i & 3], a, bop[kb][i >> 2]);
+        },
+        between);
+  };
+  auto nothing = [](int) MM1_INLINE {};
   if constexpr (AHEAD) {
-    if (pwave) product(smem, snext);
+    if (pwave) product(smem, snext, nothing);
   }
 
   // Segment s.  tn, tc, tp, tp2: ring slots of tiles s+1, s, s-1, s-2.
@@ -615,41 +643,35 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     }
     if constexpr (PW) {
       f32x16 sv[KB];
+      f32x4 lse4[4];
       if constexpr (CUR) {
         const float* lsel = reinterpret_cast<const float*>(tc + 2 * QT);
-        f32x4 lse4[4];
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) lse4[a4] = *reinterpret_cast<const f32x4*>(lsel + 8 * a4 + 4 * h);
+      }
+      // P = exp2(S*scale2 - lse2) of register r of every key block
+      auto exp_at = [&](int r) MM1_INLINE {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          float x = exp2_fast(fmaf(sv[kb][r], scale2, -lse4[r >> 2][r & 3]));
+          pin(x);   // computed here, not sunk towards its first use
+          sv[kb][r] = x;
+        }
+      };
+      if constexpr (CUR) {
         if constexpr (AHEAD) {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) sv[kb] = snext[kb];
-          product(tn, snext);
+          // S(s+1), with the exponentials of S(s) between its products
+          product(tn, snext, [&](int ks) MM1_INLINE {
+            exp_at(2 * ks);
+            exp_at(2 * ks + 1);
+          });
         } else {
-          product(tc, sv);
+          product(tc, sv, nothing);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) exp_at(r);
         }
-        // P = exp2(S*scale2 - lse2)
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              sv[kb][4 * a4 + c] = exp2_fast(fmaf(sv[kb][4 * a4 + c], scale2, -lse4[a4][c]));
-          }
-        }
-      }
-      if constexpr (PREV) {
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-#pragma unroll
-          for (int db = 0; db < 4; ++db) {
-            const bf16x8 a = tr_a(tp + QT, lb, db, kh);
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) accumulate(acc[kb][db], a, pb[kb][kh]);
-          }
-        }
-      }
-      if constexpr (CUR) {
         // causal / past-the-end mask, only in the tiles that need it
         const int p0 = tile_p0(ctl);
         if ((CAUSAL && p0 < kw0 + 32 * KB - 1) || p0 + BQ > S) {
@@ -663,6 +685,28 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
             }
           }
         }
+      }
+      // bf16 P(s), the B operand of the next segment's dV^T product: registers
+      // 2j, 2j+1 of each key block
+      bf16x8 pbn[KB][2];
+      auto pack_at = [&](int j) MM1_INLINE {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) pbn[kb][j >> 2][2 * (j & 3) + e] = (__bf16)sv[kb][2 * j + e];
+          if ((j & 3) == 3) pin(pbn[kb][j >> 2]);
+        }
+      };
+      if constexpr (PREV) {
+        // dV^T += dO(s-1)^T P(s-1), packing P(s) between its products
+        accumulate_tile(tp + QT, pb, [&](int i) MM1_INLINE {
+          if constexpr (CUR) pack_at(i);
+        });
+      } else if constexpr (CUR) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pack_at(j);
+      }
+      if constexpr (CUR) {
         float* mb = mbox + (s & 1) * (KB * MBOX / 4);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -673,59 +717,72 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
             for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c];
             *reinterpret_cast<f32x4*>(mb + kb * (MBOX / 4) + 256 * a4) = v4;
           }
-          pb[kb][0] = pack8(sv[kb], 0);
-          pb[kb][1] = pack8(sv[kb], 8);
-          // keep the conversion in this segment (it would otherwise sink to
-          // its first use, in the next one, where it runs before any product)
-          pin(pb[kb][0]);
-          pin(pb[kb][1]);
+          pb[kb][0] = pbn[kb][0];
+          pb[kb][1] = pbn[kb][1];
         }
       }
     } else {
-      f32x16 dpn[KB];
-      if constexpr (CUR && AHEAD) product(tc + QT, dpn);
-      if constexpr (PREV2) {
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-#pragma unroll
-          for (int db = 0; db < 4; ++db) {
-            const bf16x8 a = tr_a(tp2, lb, db, kh);
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) accumulate(acc[kb][db], a, sbp[kb][kh]);
-          }
-        }
-      }
+      // dS(s-1) = P(s-1) (dP(s-1) - Delta) sm_scale, computed in place of the
+      // mailbox values between the products of dK^T += Q(s-2)^T dS(s-2)
+      f32x16 dsv[KB];
+      f32x4 dl4[4];
       if constexpr (PREV) {
         const float* mb = mbox + ((s - 1) & 1) * (KB * MBOX / 4);
         const float* dll = reinterpret_cast<const float*>(tp + 2 * QT) + BQ;
-        f32x4 dl4[4];
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) dl4[a4] = *reinterpret_cast<const f32x4*>(dll + 8 * a4 + 4 * h);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          f32x16 dsv;
 #pragma unroll
           for (int a4 = 0; a4 < 4; ++a4) {
             const f32x4 p4 = *reinterpret_cast<const f32x4*>(mb + kb * (MBOX / 4) + 256 * a4);
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-              dsv[4 * a4 + c] = p4[c] * (dpp[kb][4 * a4 + c] - dl4[a4][c]) * sm_scale;
+            for (int c = 0; c < 4; ++c) dsv[kb][4 * a4 + c] = p4[c];
           }
-          sbp[kb][0] = pack8(dsv, 0);
-          sbp[kb][1] = pack8(dsv, 8);
-          // keep dS in this segment, under the products (see above)
-          pin(sbp[kb][0]);
-          pin(sbp[kb][1]);
         }
       }
-      if constexpr (CUR) {
-        if constexpr (AHEAD) {
+      auto ds_at = [&](int r) MM1_INLINE {
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) dpp[kb] = dpn[kb];
-        } else {
-          product(tc + QT, dpp);
+        for (int kb = 0; kb < KB; ++kb) {
+          float x = dsv[kb][r] * (dpp[kb][r] - dl4[r >> 2][r & 3]) * sm_scale;
+          pin(x);
+          dsv[kb][r] = x;
+        }
+      };
+      bf16x8 sbn[KB][2];
+      auto dspack_at = [&](int j) MM1_INLINE {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) sbn[kb][j >> 2][2 * (j & 3) + e] = (__bf16)dsv[kb][2 * j + e];
+          if ((j & 3) == 3) pin(sbn[kb][j >> 2]);
+        }
+      };
+      if constexpr (PREV2) {
+        accumulate_tile(tp2, sbp, [&](int i) MM1_INLINE {
+          if constexpr (PREV) {
+            ds_at(2 * i);
+            ds_at(2 * i + 1);
+            dspack_at(i);
+          }
+        });
+      } else if constexpr (PREV) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          ds_at(2 * j);
+          ds_at(2 * j + 1);
+          dspack_at(j);
         }
       }
+      if constexpr (PREV) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          sbp[kb][0] = sbn[kb][0];
+          sbp[kb][1] = sbn[kb][1];
+        }
+      }
+      // dP(s) = dO(s) V^T, used by the next segment
+      if constexpr (CUR) product(tc + QT, dpp, nothing);
     }
     if constexpr (CUR) advance(ch, ctl);
     if constexpr (SYNC) {

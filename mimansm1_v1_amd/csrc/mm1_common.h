@@ -113,6 +113,7 @@ __device__ __forceinline__ void lds_barrier() {
 // Materialise a loaded operand here: the compiler may not sink the load into
 // a loop, where its wait would also drain the LDS DMA copies in flight.
 __device__ __forceinline__ void pin(bf16x8& x) { __asm__ volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(float& x) { __asm__ volatile("" : "+v"(x)); }
 
 __device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 
