@@ -359,31 +359,6 @@ __device__ __forceinline__ void unroll_while(F&& f) {
   }
 }
 
-// Eight products in order: product i takes the A fragment load(i), read PF
-// products ahead of it, and after product i comes between(i).  Scheduling
-// barriers keep that order, so the VALU work handed to between() runs while
-// the products in flight occupy the matrix core (the compiler would
-// otherwise gather it after the last product) and every read stays PF
-// products ahead of its use.
-template <int PF, class Load, class Mma, class Between>
-__device__ __forceinline__ void chain8(Load&& load, Mma&& mma, Between&& between) {
-  bf16x8 fa[PF + 1];
-#pragma unroll
-  for (int i = 0; i < PF; ++i) {
-    fa[i] = load(i);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (i + PF < 8) fa[(i + PF) % (PF + 1)] = load(i + PF);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(i, fa[i % (PF + 1)]);
-    __builtin_amdgcn_sched_barrier(0);
-    between(i);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // dK, dV, software-pipelined across the two roles of a pair.
 //
@@ -428,7 +403,11 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   static_assert(KB == 1 || KB == 2, "32 or 64 keys per wave");
   constexpr int NW = 8 / KB;              // waves per workgroup
   constexpr int NP = NW / 2;              // pairs
-  constexpr int QPW = 8 / NW;             // row quads of a 32-row tile each wave copies
+  // Waves that copy the ring's tiles: the P waves when each has a pair
+  // partner (KB = 1: the dS waves, which carry the longer chain of the
+  // segment, issue no copies and wait for none), else all waves.
+  constexpr int DW = KB == 1 ? NP : NW;
+  constexpr int QPW = 8 / DW;             // row quads of a 32-row tile each copying wave copies
   constexpr int BQ = 32;                  // query positions per tile
   constexpr int QT = BQ * HD * 2;         // one 32 x 128 bf16 operand tile
   constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse2 x 32 | Delta x 32], 1 KiB aligned
@@ -516,7 +495,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
       ++t;
     }
   };
-  // LDS DMA, per wave and tile: row quads w, w + NW, ... of Q and of dO;
+  // LDS DMA, per copying wave and tile: row quads w, w + DW, ... of Q and of dO;
   // wave 0 adds the lse2 | Delta vector.  (quad & 3) == (w & 3) for every quad
   // of the wave, so one per-lane offset serves all of them.
   const uint32_t dma_off = tile_lane_off(qstride, tid);
@@ -524,6 +503,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // Only position tile 0 can be partial, and only when S % 32 != 0
   // (RAGGED); the walks without partial tiles carry no code for them.
   auto issue = [&](int slot, int hh, int t, auto may_be_partial) MM1_INLINE {
+    if (w >= DW) return;
     const int p0 = tile_p0(t);
     const long rows = grp_rows + (long)hh * HD + (long)p0 * qstride;
     const float* vs = vec_src + (long)hh * S;
@@ -531,7 +511,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     if (!decltype(may_be_partial)::value || p0 + BQ <= S) {
 #pragma unroll
       for (int i = 0; i < QPW; ++i) {
-        const int quad = w + NW * i;
+        const int quad = w + DW * i;
         dma16_sbase(dma_off, q + rows + (long)(4 * quad) * qstride, l + quad * 1024);
         dma16_sbase(dma_off, dO + rows + (long)(4 * quad) * qstride, l + QT + quad * 1024);
       }
@@ -540,7 +520,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
       const int L = tid & 63;
 #pragma unroll
       for (int i = 0; i < QPW; ++i) {
-        const int quad = w + NW * i;
+        const int quad = w + DW * i;
         const int row = 4 * quad + (L >> 4);
         const int chunk = (L & 15) ^ swz(row);
         const long src = rows + (long)min(row, S - p0 - 1) * qstride + 8 * chunk;
@@ -601,7 +581,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   auto product = [&](const char* t, f32x16 (&sacc)[KB], auto&& between) MM1_INLINE {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) sacc[kb] = zero16();
-    chain8<MM1_DKDV_PF_ROWS>(
+    mfma_chain<8, MM1_DKDV_PF_ROWS>(
         [&](int ks) MM1_INLINE { return rows_a(t, lb, 0, ks); },
         [&](int ks, const bf16x8& fa) MM1_INLINE {
 #pragma unroll
@@ -613,7 +593,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // i = 4*kh + db takes the transposed fragment (db, kh) of tile t and the B
   // operand bop[kb][kh]
   auto accumulate_tile = [&](const char* t, const bf16x8 (&bop)[KB][2], auto&& between) MM1_INLINE {
-    chain8<MM1_DKDV_PF_TR>(
+    mfma_chain<8, MM1_DKDV_PF_TR>(
         [&](int i) MM1_INLINE { return tr_a(t, lb, i & 3, i >> 2); },
         [&](int i, const bf16x8& a) MM1_INLINE {
 #pragma unroll
@@ -787,12 +767,15 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     if constexpr (CUR) advance(ch, ctl);
     if constexpr (SYNC) {
       // tile s+2 must have landed; the newer prefetches stay in flight
-      // (2 * QPW copies per tile and wave, wave 0 one more)
-      if (s + NSTAGE - 3 < n_u) {
-        if (w == 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"((2 * QPW + 1) * (NSTAGE - 5)) : "memory");
-        else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * QPW * (NSTAGE - 5)) : "memory");
-      } else {
-        wait_dma();
+      // (2 * QPW copies per tile and copying wave, wave 0 one more).  A wave
+      // that copies nothing waits for nothing.
+      if (w < DW) {
+        if (s + NSTAGE - 3 < n_u) {
+          if (w == 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"((2 * QPW + 1) * (NSTAGE - 5)) : "memory");
+          else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * QPW * (NSTAGE - 5)) : "memory");
+        } else {
+          wait_dma();
+        }
       }
       lds_barrier();
     }

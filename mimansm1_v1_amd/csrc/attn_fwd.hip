@@ -136,7 +136,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[jb][r]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = xhalf_max(mx);
       const float m_new = fmaxf(m_run, mx);
       if (__any(!((m_new - m_run) * scale2 <= kRescaleThreshold))) {
         const float alpha = (m_new == -INFINITY) ? 1.f : exp2_fast((m_run - m_new) * scale2);
@@ -181,7 +181,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   }
 
   if (!wave_active) return;
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = xhalf_sum(l_run);
   const float inv = 1.f / l_tot;
   if (rr < R) {
     const long row = ((long)(b * S + qpos) * H + g * G + hq) * HD;
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[jb][r]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = xhalf_max(mx);
     const float m_new = fmaxf(m_run, mx);
     if (__any(!((m_new - m_run) * scale2 <= kRescaleThreshold))) {
       const float alpha = (m_new == -INFINITY) ? 1.f : exp2_fast((m_run - m_new) * scale2);
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   wait_dma();
 
   if (!wave_active) return;
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = xhalf_sum(l_run);
   const float inv = 1.f / l_tot;
   if (rr < R) {
     __bf16* dst = o + ((long)(b * S + qpos) * H + g * G + hq) * HD;

@@ -81,6 +81,43 @@ __device__ __forceinline__ void agpr_fence(f32x16 (&acc)[N]) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// x of this lane combined with x of the lane 32 apart (the other half of a
+// 32x32 product column), as VALU work: v_permlane32_swap exchanges the two
+// halves of a register without an LDS round trip.
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// N products in order: product i takes the A fragment load(i), read PF
+// products ahead of it, and after product i comes between(i).  Scheduling
+// barriers keep that order, so the VALU work handed to between() runs while
+// the products in flight occupy the matrix core (the compiler would
+// otherwise gather it after the last product) and every read stays PF
+// products ahead of its use.
+template <int N, int PF, class Load, class Mma, class Between>
+__device__ __forceinline__ void mfma_chain(Load&& load, Mma&& mma, Between&& between) {
+  bf16x8 fa[PF + 1];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    fa[i] = load(i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (i + PF < N) fa[(i + PF) % (PF + 1)] = load(i + PF);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(i, fa[i % (PF + 1)]);
+    __builtin_amdgcn_sched_barrier(0);
+    between(i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
