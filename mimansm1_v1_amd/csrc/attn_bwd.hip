@@ -366,8 +366,8 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // 128-key tile; a pair of waves owns 32 * KB keys of it, the P wave keeping K
 // and dV^T, the dS wave V and dK^T), but the query tiles are 32 rows and the
 // work on a tile is spread over four segments:
-//   segment s, P wave : S(s+1) = Q(s+1) K^T | P(s) = exp2(S(s) scale2 - lse2) -> mailbox | dV^T += dO(s-1)^T P(s-1)
-//   segment s, dS wave: dP(s) = dO(s) V^T   | dS(s-1) = P(s-1) (dP(s-1) - Delta)          | dK^T += Q(s-2)^T dS(s-2)
+//   segment s, P wave : S(s+1) = Q(s+1) K^T | P(s) = exp2(S(s) scale2 - lse2), P(s) sm_scale -> mailbox | dV^T += dO(s-1)^T P(s-1)
+//   segment s, dS wave: dP(s) = dO(s) V^T   | dS(s-1) = P(s-1) sm_scale (dP(s-1) - Delta)          | dK^T += Q(s-2)^T dS(s-2)
 // Within a segment each wave's VALU work (middle column) depends on no
 // product of the same segment, so it runs under the wave's own products
 // (and, with two waves per SIMD, the other wave's), and the pair meets at one
@@ -694,7 +694,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           for (int a4 = 0; a4 < 4; ++a4) {
             f32x4 v4;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c];
+            for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c] * sm_scale;
             *reinterpret_cast<f32x4*>(mb + kb * (MBOX / 4) + 256 * a4) = v4;
           }
           pb[kb][0] = pbn[kb][0];
@@ -703,7 +703,8 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
       }
     } else {
       // dS(s-1) = P(s-1) (dP(s-1) - Delta) sm_scale, computed in place of the
-      // mailbox values between the products of dK^T += Q(s-2)^T dS(s-2)
+      // mailbox values (P sm_scale: the P wave, which has the shorter chain,
+      // applies the scale) between the products of dK^T += Q(s-2)^T dS(s-2)
       f32x16 dsv[KB];
       f32x4 dl4[4];
       if constexpr (PREV) {
@@ -724,7 +725,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
       auto ds_at = [&](int r) MM1_INLINE {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          float x = dsv[kb][r] * (dpp[kb][r] - dl4[r >> 2][r & 3]) * sm_scale;
+          float x = dsv[kb][r] * (dpp[kb][r] - dl4[r >> 2][r & 3]);
           pin(x);
           dsv[kb][r] = x;
         }
@@ -1018,6 +1019,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     }
   }
 
+  f32x16 negdl;   // the initial accumulator of every dP^T block
+#pragma unroll
+  for (int r = 0; r < 16; ++r) negdl[r] = -dl_i;
   f32x16 dqacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) dqacc[db] = zero16();
@@ -1037,7 +1041,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
       // one 32-key block at a time keeps S^T/dP^T at 32 registers
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
-        f32x16 sv = zero16(), dp = zero16();
+        // dP^T accumulates onto -Delta: the products give dP - Delta directly
+        f32x16 sv = zero16(), dp = negdl;
         // K / V fragments read PF k-steps ahead of their products
         constexpr int PF = MM1_DQ_PREFETCH;
         bf16x8 ka[PF + 1], va[PF + 1];
@@ -1069,7 +1074,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
               const int key = k0 + 32 * jb + 8 * (r >> 2) + 4 * h + (r & 3);
               pr = (CAUSAL ? (key > qp) : (key >= S)) ? 0.f : pr;
             }
-            sv[r] = pr * (dp[r] - dl_i);
+            sv[r] = pr * dp[r];
           }
         };
         if (need_mask) dscore(std::true_type{});
