@@ -953,6 +953,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
   constexpr int BN = TILE_ROWS;
   constexpr int BUF = 2 * TILE_BYTES;   // K, V
   constexpr int DMA_PER_TILE = 2 * (16 / NW);
+  static_assert(NSTAGE * BUF >= NW * 8192, "the epilogue stages 8 KiB per wave in the ring");
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF];
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
@@ -1103,7 +1104,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     }
   }
 
-  if (row_valid) {
+  if constexpr (!F32OUT) {
+    // every slot is free after the last step's barrier: each wave's rows go
+    // out through 8 KiB of it (store_tile_bf16)
+    if (wave_active)
+      store_tile_bf16(dqacc, 1.f, smem + w * 8192, lane, [&](int i) -> __bf16* {
+        const int r = rw0 + i;
+        if (r >= R) return nullptr;
+        const int p = r / G;
+        return static_cast<__bf16*>(dq_out) + ((long)(b * S + p) * H + g * G + (r - p * G)) * HD;
+      });
+  } else if (row_valid) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll

@@ -41,6 +41,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   constexpr int BN = TILE_ROWS;   // keys per iteration
   constexpr int BUF = 2 * TILE_BYTES;
   constexpr int DMA_PER_TILE = 2 * (16 / NW);   // copies one wave issues per K/V tile
+  static_assert(NSTAGE * BUF >= NW * 8192, "the epilogue stages 8 KiB per wave in the ring");
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF];
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
@@ -183,6 +184,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   if (!wave_active) return;
   const float l_tot = xhalf_sum(l_run);
   const float inv = 1.f / l_tot;
+  if constexpr (!F32OUT) {
+    // every slot is free after the last step's barrier: each wave's rows go
+    // out through 8 KiB of it (store_tile_bf16)
+    if (rr < R && h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
+    store_tile_bf16(oacc, inv, smem + w * 8192, lane, [&](int i) -> __bf16* {
+      const int r = rw0 + i;
+      if (r >= R) return nullptr;
+      const int p = r / G;
+      return static_cast<__bf16*>(o_out) + ((long)(b * S + p) * H + g * G + (r - p * G)) * HD;
+    });
+    return;
+  }
   if (rr < R) {
     const long row = ((long)(b * S + qpos) * H + g * G + hq) * HD;
 #pragma unroll
@@ -398,22 +411,28 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   }
   wait_dma();
 
-  if (!wave_active) return;
-  const float l_tot = xhalf_sum(l_run);
-  const float inv = 1.f / l_tot;
-  if (rr < R) {
-    __bf16* dst = o + ((long)(b * S + qpos) * H + g * G + hq) * HD;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        bf16x4 val;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) val[c] = (__bf16)(oacc[db][4 * a4 + c] * inv);
-        *reinterpret_cast<bf16x4*>(dst + 32 * db + 8 * a4 + 4 * h) = val;
-      }
-    }
-    if (h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
+  // The rows go out through LDS (store_tile_bf16): group A's through the K
+  // slots, free since B's last part 1 (before A's last barrier), while B
+  // runs the last part 2; group B's through the V slots after a final
+  // barrier.
+  auto store_rows = [&](char* region) {
+    if (!wave_active) return;
+    const float l_tot = xhalf_sum(l_run);
+    const float inv = 1.f / l_tot;
+    if (rr < R && h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
+    store_tile_bf16(oacc, inv, region + (w & 3) * 8192, lane, [&](int i) -> __bf16* {
+      const int r = rw0 + i;
+      if (r >= R) return nullptr;
+      const int p = r / G;
+      return o + ((long)(b * S + p) * H + g * G + (r - p * G)) * HD;
+    });
+  };
+  if (grp == 0) {
+    store_rows(kslot(0));
+    lds_barrier();
+  } else {
+    lds_barrier();
+    store_rows(vslot(0));
   }
 }
 

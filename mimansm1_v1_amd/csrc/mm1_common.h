@@ -346,6 +346,40 @@ __device__ __forceinline__ void rows_chain2(const char* tile, const LdsBases& lb
   }
 }
 
+// Stores a wave's 32 x 128 fp32 product tile as bf16 rows, each value times
+// `scale` (per lane), through `lds`: 8 KiB owned by the wave.  In registers
+// lane l holds tile row l & 31 and, in acc[db][r], the values
+// 32db + 8(r/4) + 4(l/32) + r%4 of it (the D layout of the products), so a
+// direct store instruction writes 32 separate 16-byte pieces.  Written to LDS
+// and read back, each lane holds 16 bytes of one row and a store instruction
+// covers four whole 256-byte rows.  The 16-byte chunks of LDS row i are
+// permuted by chunk ^ (i & 15), which spreads both the writes (32 rows at
+// one chunk) and the reads (16 chunks of one row) over the banks.  dst(i) is
+// the global address of tile row i, or nullptr for a row outside the tensor.
+template <class Dst>
+__device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4], float scale, char* lds, int lane,
+                                                Dst&& dst) {
+  const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      bf16x4 val;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) val[c] = (__bf16)(acc[db][4 * a4 + c] * scale);
+      const int chunk = (4 * db + a4) ^ (l32 & 15);
+      *reinterpret_cast<bf16x4*>(lds + l32 * 256 + chunk * 16 + 8 * h) = val;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int row = 4 * k + (lane >> 4), ch = lane & 15;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(lds + row * 256 + ((ch ^ (row & 15)) << 4));
+    __bf16* p = dst(row);
+    if (p) *reinterpret_cast<bf16x8*>(p + 8 * ch) = x;
+  }
+}
+
 __device__ __forceinline__ bf16x8 tr_a(const char* tile, const LdsBases& lb, int blk, int ks) {
   bf16x8 out;
 #pragma unroll
