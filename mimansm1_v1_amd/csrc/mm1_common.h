@@ -356,6 +356,14 @@ __device__ __forceinline__ void rows_chain2(const char* tile, const LdsBases& lb
 // permuted by chunk ^ (i & 15), which spreads both the writes (32 rows at
 // one chunk) and the reads (16 chunks of one row) over the banks.  dst(i) is
 // the global address of tile row i, or nullptr for a row outside the tensor.
+// The lanes exchange data through LDS, which the compiler's per-thread view
+// of memory does not see: wave_sync() keeps the writes before the reads.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <class Dst>
 __device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4], float scale, char* lds, int lane,
                                                 Dst&& dst) {
@@ -371,6 +379,7 @@ __device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4], float sc
       *reinterpret_cast<bf16x4*>(lds + l32 * 256 + chunk * 16 + 8 * h) = val;
     }
   }
+  wave_sync();
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int row = 4 * k + (lane >> 4), ch = lane & 15;
