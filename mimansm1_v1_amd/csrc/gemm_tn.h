@@ -90,6 +90,51 @@ struct Problem {
   int n_mblk, n_nblk;
 };
 
+// Stores one bf16 output of a wave's tile, 128 tokens x 32 columns, whose
+// values the lane holds as val(i, q): the bf16x4 of columns 8q + 4(lane/32)
+// .. +3 of token 32i + (lane & 31) (the accumulator layout above).  Stored
+// directly, an instruction writes 32 separate 16-byte pieces; here they go
+// through `lds` (4 KiB owned by the wave) in two rounds of 64 tokens, after
+// which each lane holds 16 bytes of one token's 64-byte row and an
+// instruction writes the rows of 16 tokens.  row(r) is the global address of
+// the first column of token r (0..127) of the tile, or nullptr for a token
+// outside the tensor.  The 16-byte chunks of LDS row r are permuted by
+// chunk ^ ((r >> 2) & 3), which spreads the writes over the banks.
+// wave_sync() orders the lanes' exchange, which the compiler's per-thread
+// view of memory does not see.
+constexpr int STAGE_BYTES = 4096;          // per wave
+
+template <class Val, class Row>
+__device__ __forceinline__ void store_rows64(char* lds, int lane, Val&& val, Row&& row) {
+  const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int r = 32 * ii + l32;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bf16x4 v = val(2 * half + ii, q);
+        *reinterpret_cast<bf16x4*>(lds + r * 64 + ((q ^ ((r >> 2) & 3)) << 4) + 8 * h) = v;
+      }
+    }
+    wave_sync();
+    bf16x8 x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 16 * k + (lane >> 2), c = lane & 3;
+      x[k] = *reinterpret_cast<const bf16x8*>(lds + r * 64 + ((c ^ ((r >> 2) & 3)) << 4));
+    }
+    wave_sync();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 16 * k + (lane >> 2), c = lane & 3;
+      __bf16* p = row(64 * half + r);
+      if (p) *reinterpret_cast<bf16x8*>(p + 8 * c) = x[k];
+    }
+  }
+}
+
 // Launch geometry: one workgroup per CU, a multiple of the 8 XCDs.
 inline int persistent_grid(int cus, int total_tiles) {
   int grid = ((cus > 0 ? cus : 256) + 7) & ~7;

@@ -40,28 +40,27 @@ __device__ __forceinline__ float sigmoidf_(float g) {
 // accumulators (gate_up_swiglu), 2 = act = bf16(bf16(silu(bf16(g))) * bf16(u)),
 // the rounding of F.silu(Gate) * Up on bf16 tensors (FusedSwiGLU.forward).
 // SPLIT: also store Gate and Up (rounded to bf16).
-template <bool SPLIT, int ACT>
-__device__ __forceinline__ void store_quad(const f32x16& g, const f32x16& u, int q, long o,
-                                           __bf16* __restrict__ gate, __bf16* __restrict__ up,
-                                           __bf16* __restrict__ act) {
-  bf16x4 gv, uv, av;
+template <int ACT>
+__device__ __forceinline__ bf16x4 act_quad(const f32x16& g, const f32x16& u, int q) {
+  bf16x4 av;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const float gf = g[4 * q + e], uf = u[4 * q + e];
-    gv[e] = (__bf16)gf;
-    uv[e] = (__bf16)uf;
     if (ACT == 1) {
       av[e] = (__bf16)(gf * sigmoidf_(gf) * uf);
-    } else if (ACT == 2) {
-      const float gb = (float)gv[e];
-      av[e] = (__bf16)(bf16r(gb * sigmoidf_(gb)) * (float)uv[e]);
+    } else {
+      const float gb = bf16r(gf);
+      av[e] = (__bf16)(bf16r(gb * sigmoidf_(gb)) * bf16r(uf));
     }
   }
-  if (SPLIT) {
-    *reinterpret_cast<bf16x4*>(gate + o) = gv;
-    *reinterpret_cast<bf16x4*>(up + o) = uv;
-  }
-  if (ACT != 0) *reinterpret_cast<bf16x4*>(act + o) = av;
+  return av;
+}
+
+__device__ __forceinline__ bf16x4 round_quad(const f32x16& a, int q) {
+  bf16x4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (__bf16)a[4 * q + e];
+  return v;
 }
 
 template <bool SPLIT, int ACT>
@@ -73,19 +72,24 @@ __global__ __launch_bounds__(512, 1) void swiglu_gate_up_kernel(
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w & 1, wn = w >> 1;
   const gemm::Problem p{x, wg, wu, T, d, F, F, n_mblk, n_nblk};
+  // the outputs go out through 4 KiB per wave above the GEMM's ring
+  char* stage = smem + gemm::LDS_BYTES + gemm::STAGE_BYTES * w;
   // Epilogue of a tile: acc[0][i] / acc[1][i] give lane the token
   // m0 + 128wm + 32i + (lane & 31) and, in registers 4q .. 4q+3, the columns
   // n0 + 32wn + 8q + 4(lane/32) + 0..3 of Gate / Up (n0 = 128 nb, wn = 0..3).
   gemm::run<true>(p, smem, [](int, int) {}, [&](int mb, int nb, f32x16 (&acc)[2][4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = mb * gemm::BM + 128 * wm + 32 * i + (lane & 31);
-      if (tok < T) {
-        const long o0 = (long)tok * F + nb * 128 + 32 * wn + 4 * (lane >> 5);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) store_quad<SPLIT, ACT>(acc[0][i], acc[1][i], q, o0 + 8 * q, gate, up, act);
-      }
+    const long tok0 = (long)mb * gemm::BM + 128 * wm;
+    const int col0 = nb * 128 + 32 * wn;
+    auto rows = [&](__bf16* out) {
+      return [=](int r) -> __bf16* { return tok0 + r < T ? out + (tok0 + r) * F + col0 : nullptr; };
+    };
+    if (SPLIT) {
+      gemm::store_rows64(stage, lane, [&](int i, int q) { return round_quad(acc[0][i], q); }, rows(gate));
+      gemm::store_rows64(stage, lane, [&](int i, int q) { return round_quad(acc[1][i], q); }, rows(up));
     }
+    if (ACT != 0)
+      gemm::store_rows64(stage, lane, [&](int i, int q) { return act_quad<ACT>(acc[0][i], acc[1][i], q); },
+                         rows(act));
   });
 }
 
@@ -119,15 +123,16 @@ template <bool SPLIT, int ACT>
 static hipError_t launch_gate_up_t(const __bf16* x, const __bf16* wg, const __bf16* wu, __bf16* gate,
                                    __bf16* up, __bf16* act, int T, int d, int F, hipStream_t stream) {
   auto kern = swiglu_gate_up_kernel<SPLIT, ACT>;
+  const size_t lds = gemm::LDS_BYTES + 8 * gemm::STAGE_BYTES;   // ring + the epilogue's staging
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm::LDS_BYTES);
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   int dev = 0, cus = 0;
   e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   const int n_mblk = (T + gemm::BM - 1) / gemm::BM, n_nblk = F / 128;
-  hipLaunchKernelGGL(kern, dim3(gemm::persistent_grid(cus, n_mblk * n_nblk)), dim3(512), gemm::LDS_BYTES,
+  hipLaunchKernelGGL(kern, dim3(gemm::persistent_grid(cus, n_mblk * n_nblk)), dim3(512), lds,
                      stream, x, wg, wu, gate, up, act, T, d, F, n_mblk, n_nblk);
   return hipGetLastError();
 }
