@@ -135,6 +135,45 @@ __device__ __forceinline__ void store_rows64(char* lds, int lane, Val&& val, Row
   }
 }
 
+// The same for a wave's 128 tokens x 64 columns of the single-matrix layout
+// (two 32-column blocks): val(i, b, q) is the bf16x4 of columns
+// 32b + 8q + 4(lane/32) .. +3 of token 32i + (lane & 31).  Four rounds of 32
+// tokens through `lds` (4 KiB owned by the wave); each lane then holds 16
+// bytes of one token's 128-byte row and an instruction writes the rows of 8
+// tokens.  row(r) is the global address of the first column of token r or
+// nullptr; chunk_ok(c) says whether the 8 columns 8c .. 8c+7 exist.  Chunks
+// of LDS row r are permuted by chunk ^ ((r >> 1) & 7).
+template <class Val, class Row, class ChunkOk>
+__device__ __forceinline__ void store_rows128(char* lds, int lane, Val&& val, Row&& row, ChunkOk&& chunk_ok) {
+  const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bf16x4 v = val(i, b, q);
+        const int chunk = (4 * b + q) ^ ((l32 >> 1) & 7);
+        *reinterpret_cast<bf16x4*>(lds + l32 * 128 + (chunk << 4) + 8 * h) = v;
+      }
+    }
+    wave_sync();
+    bf16x8 x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 8 * k + (lane >> 3), c = lane & 7;
+      x[k] = *reinterpret_cast<const bf16x8*>(lds + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+    }
+    wave_sync();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 8 * k + (lane >> 3), c = lane & 7;
+      __bf16* p = row(32 * i + r);
+      if (p && chunk_ok(c)) *reinterpret_cast<bf16x8*>(p + 8 * c) = x[k];
+    }
+  }
+}
+
 // Launch geometry: one workgroup per CU, a multiple of the 8 XCDs.
 inline int persistent_grid(int cus, int total_tiles) {
   int grid = ((cus > 0 ? cus : 256) + 7) & ~7;

@@ -165,37 +165,45 @@ __global__ __launch_bounds__(512, 1) void lm_dlogits_kernel(
     int T, int d, int V, int v0, int vn, long long ignore_index, int n_mblk, int n_nblk) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv & 1, wn = wv >> 1, hh = lane >> 5;
+  const int wm = wv & 1, wn = wv >> 1;
   const gemm::Problem p{h, w + v0, w + v0, T, d, V, vn, n_mblk, n_nblk};
   const float sc = *scale;
-  gemm::run<false>(p, smem, [](int, int) {}, [&](int mb, int nb, f32x16 (&acc)[2][4]) {
-    const int c0 = nb * 256 + 64 * wn;             // this wave's first column of the chunk
+  // the rows go out through 4 KiB per wave above the GEMM's ring
+  char* stage = smem + gemm::LDS_BYTES + gemm::STAGE_BYTES * wv;
+  // Targets and lse of the tile's tokens, loaded at its first k step (the
+  // loads land during the products, not in the epilogue).
+  long long tv[4];
+  float l2[4];
+  auto pro = [&](int mb, int) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tok = mb * gemm::BM + 128 * wm + 32 * i + (lane & 31);
-      if (tok >= T) continue;
-      const long long tv = targets[tok];
-      const bool valid = tv != ignore_index && tv >= 0 && tv < V;
-      const float coef = valid ? sc : 0.f;
-      const float l2 = lse[tok] * kLog2e;
-      const long long tcol = tv - v0;               // the target's column in this chunk
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int c = c0 + 32 * b + 8 * q + 4 * hh;
-          if (c >= vn) continue;
-          bf16x4 o;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float pr = exp2_fast(acc[b][i][4 * q + e] * kLog2e - l2);
-            if (c + e == tcol) pr -= 1.f;
-            o[e] = (__bf16)(pr * coef);
-          }
-          *reinterpret_cast<bf16x4*>(out + (long)tok * ld + c) = o;
-        }
-      }
+      const int tok = min(mb * gemm::BM + 128 * wm + 32 * i + (lane & 31), T - 1);
+      tv[i] = targets[tok];
+      l2[i] = lse[tok] * kLog2e;
     }
+  };
+  gemm::run<false>(p, smem, pro, [&](int mb, int nb, f32x16 (&acc)[2][4]) {
+    const int c0 = nb * 256 + 64 * wn;             // this wave's first column of the chunk
+    const long tok0 = (long)mb * gemm::BM + 128 * wm;
+    auto val = [&](int i, int b, int q) {
+      const long long t = tv[i];
+      const bool valid = t != ignore_index && t >= 0 && t < V;
+      const float coef = valid ? sc : 0.f;
+      const long long tcol = t - v0;               // the target's column in this chunk
+      const int c = c0 + 32 * b + 8 * q + 4 * (lane >> 5);
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float pr = exp2_fast(acc[b][i][4 * q + e] * kLog2e - l2[i]);
+        if (c + e == tcol) pr -= 1.f;
+        o[e] = (__bf16)(pr * coef);
+      }
+      return o;
+    };
+    gemm::store_rows128(
+        stage, lane, val,
+        [&](int r) -> __bf16* { return tok0 + r < T ? out + (tok0 + r) * ld + c0 : nullptr; },
+        [&](int c) { return c0 + 8 * c < vn; });
   });
 }
 
@@ -243,10 +251,11 @@ hipError_t launch_lm_dlogits(const void* hidden, const void* weight, const long 
   int n_mblk, n_nblk, grid;
   hipError_t e = gemm_geometry(T, vn, n_mblk, n_nblk, grid);
   if (e != hipSuccess) return e;
+  const size_t lds = gemm::LDS_BYTES + 8 * gemm::STAGE_BYTES;   // ring + the epilogue's staging
   e = hipFuncSetAttribute(reinterpret_cast<const void*>(lm_dlogits_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm::LDS_BYTES);
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(lm_dlogits_kernel, dim3(grid), dim3(512), gemm::LDS_BYTES, stream,
+  hipLaunchKernelGGL(lm_dlogits_kernel, dim3(grid), dim3(512), lds, stream,
                      static_cast<const __bf16*>(hidden), static_cast<const __bf16*>(weight), targets, lse, scale,
                      static_cast<__bf16*>(dlogits), ld, T, d, V, v0, vn, ignore_index, n_mblk, n_nblk);
   return hipGetLastError();
