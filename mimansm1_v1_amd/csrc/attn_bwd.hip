@@ -1044,6 +1044,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
       for (int jb = 0; jb < 2; ++jb) {
         // dP^T accumulates onto -Delta: the products give dP - Delta directly
         f32x16 sv = zero16(), dp = negdl;
+        // the wave issuing products goes first; the other wave of the SIMD
+        // fills the gaps with its dS arithmetic
+        wave_prio<1>();
         // K / V fragments read PF k-steps ahead of their products
         constexpr int PF = MM1_DQ_PREFETCH;
         bf16x8 ka[PF + 1], va[PF + 1];
@@ -1078,8 +1081,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
             sv[r] = pr * dp[r];
           }
         };
+        wave_prio<0>();
         if (need_mask) dscore(std::true_type{});
         else dscore(std::false_type{});
+        wave_prio<1>();
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
           const bf16x8 sb = pack8(sv, 8 * kh);

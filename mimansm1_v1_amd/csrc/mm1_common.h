@@ -118,6 +118,16 @@ __device__ __forceinline__ void mfma_chain(Load&& load, Mma&& mma, Between&& bet
   }
 }
 
+// Issue priority of this wave among the waves of its SIMD (0-3, higher
+// first; equal priorities go oldest first).  Scheduling barriers on both
+// sides keep the products where the caller put them relative to it.
+template <int P>
+__device__ __forceinline__ void wave_prio() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(P);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
