@@ -373,7 +373,11 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // (and, with two waves per SIMD, the other wave's), and the pair meets at one
 // barrier per segment, which also publishes the DMA ring.  S(s+1), P(s-1)
 // (bf16) stay in the P wave's registers, dP(s-1) and dS(s-2) (bf16) in the
-// dS wave's.
+// dS wave's.  Each wave starts its segment with the accumulation product
+// (KB = 1: the P wave runs dV^T before S(s+1)), whose tile was published
+// segments earlier: its first operand fragments and the wave's lse2 / Delta
+// vector are read before the previous barrier, so right after a barrier the
+// waves issue products instead of all waiting on the LDS together.
 //
 // KB = 32-key blocks per wave:
 //   KB = 1: 8 waves (4 pairs x 32 keys), two waves per SIMD (a pair shares
@@ -591,26 +595,48 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   };
   // dV^T += dO^T P (P wave) / dK^T += Q^T dS (dS wave) of one tile: product
   // i = 4*kh + db takes the transposed fragment (db, kh) of tile t and the B
-  // operand bop[kb][kh]
-  auto accumulate_tile = [&](const char* t, const bf16x8 (&bop)[KB][2], auto&& between) MM1_INLINE {
-    mfma_chain<8, MM1_DKDV_PF_TR>(
-        [&](int i) MM1_INLINE { return tr_a(t, lb, i & 3, i >> 2); },
+  // operand bop[kb][kh]; its first PFT fragments were read before the
+  // segment's barrier (first)
+  constexpr int PFT = MM1_DKDV_PF_TR;
+  auto tr_frag = [&](const char* t, int i) MM1_INLINE { return tr_a(t, lb, i & 3, i >> 2); };
+  auto accumulate_tile = [&](const bf16x8 (&first)[PFT], const char* t, const bf16x8 (&bop)[KB][2],
+                             auto&& between) MM1_INLINE {
+    mfma_chain_from<8, PFT>(
+        first, [&](int i) MM1_INLINE { return tr_frag(t, i); },
         [&](int i, const bf16x8& a) MM1_INLINE {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) accumulate(acc[kb][i & 3], a, bop[kb][i >> 2]);
         },
         between);
   };
+  // What a wave's next segment starts with, read at the end of this one
+  // from tiles published by earlier barriers, so that after the barrier the
+  // first product waits for no LDS read: the first PFT transposed fragments
+  // of the accumulation product (P wave: dO(s) for dV^T; dS wave: Q(s-1) for
+  // dK^T) and the per-query vector (P wave: lse2 of tile s+1; dS wave:
+  // Delta of tile s).
+  bf16x8 nfa[PFT];
+  f32x4 nvec[4];
+  auto read_first = [&](const char* t) MM1_INLINE {
+#pragma unroll
+    for (int i = 0; i < PFT; ++i) nfa[i] = tr_frag(t, i);
+  };
+  auto read_vec = [&](const float* vsrc) MM1_INLINE {
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) nvec[a4] = *reinterpret_cast<const f32x4*>(vsrc + 8 * a4 + 4 * h);
+  };
   auto nothing = [](int) MM1_INLINE {};
-  if constexpr (AHEAD) {
-    if (pwave) product(smem, snext, nothing);
+  if (pwave) {
+    if constexpr (AHEAD) product(smem, snext, nothing);
+    read_vec(reinterpret_cast<const float*>(smem + 2 * QT));   // lse2 of tile 0
   }
 
   // Segment s.  tn, tc, tp, tp2: ring slots of tiles s+1, s, s-1, s-2.
   // CUR: s < n_u; PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a
   // later segment reads what this one publishes (mailbox, ring).  In the last
   // segment with CUR, S(s+1) reads a slot holding another tile (or nothing
-  // yet) and is discarded: every read stays inside the ring.
+  // yet) and is discarded, as is the lse2 read for segment s+1: every read
+  // stays inside the ring.
   auto segment = [&](const char* tn, const char* tc, const char* tp, const char* tp2, int refill,
                      int s, auto role, auto cur, auto prev, auto prev2, auto sync) MM1_INLINE {
     constexpr bool PW = decltype(role)::value;
@@ -625,9 +651,8 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
       f32x16 sv[KB];
       f32x4 lse4[4];
       if constexpr (CUR) {
-        const float* lsel = reinterpret_cast<const float*>(tc + 2 * QT);
 #pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) lse4[a4] = *reinterpret_cast<const f32x4*>(lsel + 8 * a4 + 4 * h);
+        for (int a4 = 0; a4 < 4; ++a4) lse4[a4] = nvec[a4];
       }
       // P = exp2(S*scale2 - lse2) of register r of every key block
       auto exp_at = [&](int r) MM1_INLINE {
@@ -638,21 +663,8 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           sv[kb][r] = x;
         }
       };
-      if constexpr (CUR) {
-        if constexpr (AHEAD) {
-#pragma unroll
-          for (int kb = 0; kb < KB; ++kb) sv[kb] = snext[kb];
-          // S(s+1), with the exponentials of S(s) between its products
-          product(tn, snext, [&](int ks) MM1_INLINE {
-            exp_at(2 * ks);
-            exp_at(2 * ks + 1);
-          });
-        } else {
-          product(tc, sv, nothing);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) exp_at(r);
-        }
-        // causal / past-the-end mask, only in the tiles that need it
+      // causal / past-the-end mask, only in the tiles that need it
+      auto mask = [&]() MM1_INLINE {
         const int p0 = tile_p0(ctl);
         if ((CAUSAL && p0 < kw0 + 32 * KB - 1) || p0 + BQ > S) {
 #pragma unroll
@@ -665,7 +677,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
             }
           }
         }
-      }
+      };
       // bf16 P(s), the B operand of the next segment's dV^T product: registers
       // 2j, 2j+1 of each key block
       bf16x8 pbn[KB][2];
@@ -677,14 +689,46 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           if ((j & 3) == 3) pin(pbn[kb][j >> 2]);
         }
       };
-      if constexpr (PREV) {
-        // dV^T += dO(s-1)^T P(s-1), packing P(s) between its products
-        accumulate_tile(tp + QT, pb, [&](int i) MM1_INLINE {
-          if constexpr (CUR) pack_at(i);
-        });
-      } else if constexpr (CUR) {
+      if constexpr (AHEAD) {
+        // dV^T += dO(s-1)^T P(s-1) first (its operands were read before the
+        // barrier), with the exponentials of S(s) between its products; then
+        // S(s+1) from the tile the barrier published, with the bf16 pack of
+        // P(s) between its products
+        if constexpr (CUR) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pack_at(j);
+          for (int kb = 0; kb < KB; ++kb) sv[kb] = snext[kb];
+        }
+        if constexpr (PREV) {
+          accumulate_tile(nfa, tp + QT, pb, [&](int i) MM1_INLINE {
+            if constexpr (CUR) {
+              exp_at(2 * i);
+              exp_at(2 * i + 1);
+            }
+          });
+        } else if constexpr (CUR) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) exp_at(r);
+        }
+        if constexpr (CUR) {
+          mask();
+          product(tn, snext, [&](int ks) MM1_INLINE { pack_at(ks); });
+        }
+      } else {
+        if constexpr (CUR) {
+          product(tc, sv, nothing);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) exp_at(r);
+          mask();
+        }
+        if constexpr (PREV) {
+          // dV^T += dO(s-1)^T P(s-1), packing P(s) between its products
+          accumulate_tile(nfa, tp + QT, pb, [&](int i) MM1_INLINE {
+            if constexpr (CUR) pack_at(i);
+          });
+        } else if constexpr (CUR) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pack_at(j);
+        }
       }
       if constexpr (CUR) {
         float* mb = mbox + (s & 1) * (KB * MBOX / 4);
@@ -700,6 +744,8 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           pb[kb][0] = pbn[kb][0];
           pb[kb][1] = pbn[kb][1];
         }
+        read_first(tc + QT);
+        read_vec(reinterpret_cast<const float*>(tn + 2 * QT));
       }
     } else {
       // dS(s-1) = P(s-1) (dP(s-1) - Delta) sm_scale, computed in place of the
@@ -708,10 +754,9 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
       f32x16 dsv[KB];
       f32x4 dl4[4];
       if constexpr (PREV) {
-        const float* mb = mbox + ((s - 1) & 1) * (KB * MBOX / 4);
-        const float* dll = reinterpret_cast<const float*>(tp + 2 * QT) + BQ;
 #pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) dl4[a4] = *reinterpret_cast<const f32x4*>(dll + 8 * a4 + 4 * h);
+        for (int a4 = 0; a4 < 4; ++a4) dl4[a4] = nvec[a4];
+        const float* mb = mbox + ((s - 1) & 1) * (KB * MBOX / 4);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
@@ -740,7 +785,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
         }
       };
       if constexpr (PREV2) {
-        accumulate_tile(tp2, sbp, [&](int i) MM1_INLINE {
+        accumulate_tile(nfa, tp2, sbp, [&](int i) MM1_INLINE {
           if constexpr (PREV) {
             ds_at(2 * i);
             ds_at(2 * i + 1);
@@ -764,6 +809,8 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
       }
       // dP(s) = dO(s) V^T, used by the next segment
       if constexpr (CUR) product(tc + QT, dpp, nothing);
+      if constexpr (PREV) read_first(tp);
+      if constexpr (CUR) read_vec(reinterpret_cast<const float*>(tc + 2 * QT) + BQ);
     }
     if constexpr (CUR) advance(ch, ctl);
     if constexpr (SYNC) {

@@ -118,6 +118,26 @@ __device__ __forceinline__ void mfma_chain(Load&& load, Mma&& mma, Between&& bet
   }
 }
 
+// mfma_chain whose first PF fragments the caller read earlier (before a
+// barrier, say), so the first product waits for no read.
+template <int N, int PF, class Load, class Mma, class Between>
+__device__ __forceinline__ void mfma_chain_from(const bf16x8 (&first)[PF], Load&& load, Mma&& mma,
+                                                Between&& between) {
+  static_assert(PF >= 1 && PF < N, "prefetch depth");
+  bf16x8 fa[PF + 1];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) fa[i] = first[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (i + PF < N) fa[(i + PF) % (PF + 1)] = load(i + PF);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(i, fa[i % (PF + 1)]);
+    __builtin_amdgcn_sched_barrier(0);
+    between(i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Issue priority of this wave among the waves of its SIMD (0-3, higher
 // first; equal priorities go oldest first).  Scheduling barriers on both
 // sides keep the products where the caller put them relative to it.
