@@ -541,8 +541,11 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     advance(ih, itl);
   }
 
-  // This lane's key rows of K (P wave) or V (dS wave) as the B operands,
-  // one per key block.
+  // This lane's key rows of K (P wave) or -V (dS wave) as the B operands,
+  // one per key block.  With -V the dP product accumulates onto Delta and
+  // gives Delta - dP, and the mailbox carries -P sm_scale, so dS = P (dP -
+  // Delta) sm_scale is one multiply; negating a bf16 is exact, so every
+  // value is the one of the unnegated arithmetic up to its sign.
   bf16x8 breg[KB][8];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
@@ -550,6 +553,10 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     const __bf16* src = (pwave ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+    if (!pwave) {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = neg8(breg[kb][ks]);
+    }
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) pin(breg[kb][ks]);
   }
@@ -582,9 +589,11 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // S = Q K^T / dP = dO V^T of one tile, per key block (D layout: register r
   // holds query 8*(r/4) + 4*h + (r%4) of the tile, lane l32 holds key
   // kw0 + 32*kb + l32); each row fragment is read once for all key blocks
-  auto product = [&](const char* t, f32x16 (&sacc)[KB], auto&& between) MM1_INLINE {
+  // (accumulated onto c0)
+  auto product_onto = [&](const char* t, f32x16 (&sacc)[KB], const f32x16& c0,
+                          auto&& between) MM1_INLINE {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) sacc[kb] = zero16();
+    for (int kb = 0; kb < KB; ++kb) sacc[kb] = c0;
     mfma_chain<8, MM1_DKDV_PF_ROWS>(
         [&](int ks) MM1_INLINE { return rows_a(t, lb, 0, ks); },
         [&](int ks, const bf16x8& fa) MM1_INLINE {
@@ -592,6 +601,9 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32(fa, breg[kb][ks], sacc[kb]);
         },
         between);
+  };
+  auto product = [&](const char* t, f32x16 (&sacc)[KB], auto&& between) MM1_INLINE {
+    product_onto(t, sacc, zero16(), between);
   };
   // dV^T += dO^T P (P wave) / dK^T += Q^T dS (dS wave) of one tile: product
   // i = 4*kh + db takes the transposed fragment (db, kh) of tile t and the B
@@ -613,8 +625,10 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // from tiles published by earlier barriers, so that after the barrier the
   // first product waits for no LDS read: the first PFT transposed fragments
   // of the accumulation product (P wave: dO(s) for dV^T; dS wave: Q(s-1) for
-  // dK^T) and the per-query vector (P wave: lse2 of tile s+1; dS wave:
-  // Delta of tile s).
+  // dK^T) and, for the P wave, the lse2 vector of tile s+1 (its
+  // exponentials).  The dS wave reads Delta of tile s just before its dP
+  // product, which starts from it (holding it across the barrier cost more
+  // registers than the read).
   bf16x8 nfa[PFT];
   f32x4 nvec[4];
   auto read_first = [&](const char* t) MM1_INLINE {
@@ -628,8 +642,9 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   auto nothing = [](int) MM1_INLINE {};
   if (pwave) {
     if constexpr (AHEAD) product(smem, snext, nothing);
-    read_vec(reinterpret_cast<const float*>(smem + 2 * QT));   // lse2 of tile 0
+    read_vec(reinterpret_cast<const float*>(smem + 2 * QT));        // lse2 of tile 0
   }
+  const float neg_sm_scale = -sm_scale;
 
   // Segment s.  tn, tc, tp, tp2: ring slots of tiles s+1, s, s-1, s-2.
   // CUR: s < n_u; PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a
@@ -738,7 +753,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           for (int a4 = 0; a4 < 4; ++a4) {
             f32x4 v4;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c] * sm_scale;
+            for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c] * neg_sm_scale;
             *reinterpret_cast<f32x4*>(mb + kb * (MBOX / 4) + 256 * a4) = v4;
           }
           pb[kb][0] = pbn[kb][0];
@@ -748,14 +763,12 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
         read_vec(reinterpret_cast<const float*>(tn + 2 * QT));
       }
     } else {
-      // dS(s-1) = P(s-1) (dP(s-1) - Delta) sm_scale, computed in place of the
-      // mailbox values (P sm_scale: the P wave, which has the shorter chain,
-      // applies the scale) between the products of dK^T += Q(s-2)^T dS(s-2)
+      // dS(s-1) = (-P(s-1) sm_scale) (Delta - dP(s-1)), computed in place of
+      // the mailbox values (-P sm_scale: the P wave, which has the shorter
+      // chain, applies the scale) between the products of
+      // dK^T += Q(s-2)^T dS(s-2)
       f32x16 dsv[KB];
-      f32x4 dl4[4];
       if constexpr (PREV) {
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) dl4[a4] = nvec[a4];
         const float* mb = mbox + ((s - 1) & 1) * (KB * MBOX / 4);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -770,7 +783,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
       auto ds_at = [&](int r) MM1_INLINE {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          float x = dsv[kb][r] * (dpp[kb][r] - dl4[r >> 2][r & 3]);
+          float x = dsv[kb][r] * dpp[kb][r];
           pin(x);
           dsv[kb][r] = x;
         }
@@ -807,10 +820,19 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           sbp[kb][1] = sbn[kb][1];
         }
       }
-      // dP(s) = dO(s) V^T, used by the next segment
-      if constexpr (CUR) product(tc + QT, dpp, nothing);
+      // Delta - dP(s) = Delta + dO(s) (-V)^T, used by the next segment
+      if constexpr (CUR) {
+        f32x16 dlt;   // Delta of tile s in the D layout (register r: query 8*(r/4) + 4*h + r%4)
+        const float* dll = reinterpret_cast<const float*>(tc + 2 * QT) + BQ;
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dll + 8 * a4 + 4 * h);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) dlt[4 * a4 + c] = d4[c];
+        }
+        product_onto(tc + QT, dpp, dlt, nothing);
+      }
       if constexpr (PREV) read_first(tp);
-      if constexpr (CUR) read_vec(reinterpret_cast<const float*>(tc + 2 * QT) + BQ);
     }
     if constexpr (CUR) advance(ch, ctl);
     if constexpr (SYNC) {

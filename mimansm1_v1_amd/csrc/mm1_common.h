@@ -46,6 +46,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 #define MM1_LDS __attribute__((address_space(3)))
 #define MM1_GLOBAL __attribute__((address_space(1)))
@@ -146,6 +147,11 @@ __device__ __forceinline__ void wave_prio() {
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_setprio(P);
   __builtin_amdgcn_sched_barrier(0);
+}
+
+// -x, elementwise (flips the sign bits: exact)
+__device__ __forceinline__ bf16x8 neg8(const bf16x8& x) {
+  return __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, x) ^ 0x80008000u);
 }
 
 __device__ __forceinline__ f32x16 zero16() {
