@@ -80,7 +80,7 @@ def parse(argv=None):
 # Kernel launched by each tiling index of a stage (mm1_attn_tile_desc order).
 KERNEL_NAMES = {"fwd": ("attn_fwd_pp_kernel", "attn_fwd_kernel", "attn_fwd_kernel"),
                 "dkdv": ("attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel", "attn_dkdv_kernel",
-                         "attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel"),
+                         "attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel", "attn_dkdv_quad_kernel"),
                 "dq": ("attn_dq_kernel", "attn_dq_kernel")}
 
 

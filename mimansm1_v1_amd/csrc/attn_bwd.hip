@@ -29,6 +29,9 @@
 //     (128-key tile, query head) and write a partial per head.  The partials
 //     are summed in a fixed order and rounded once (in the dQ launch's tail,
 //     or attn_dkdv_reduce_kernel).
+//   * attn_dkdv_quad_kernel : the grouped walk with the 8 waves as two quads
+//     of single-product waves over 64 keys each (fewer LDS instructions per
+//     product, bitwise the same results).
 //   * attn_dq_kernel      : query-stationary over the packed GQA row space
 //     (as in the forward): K/V tiles in LDS serve all G heads of a group and
 //     dQ is written once in bf16 -- no fp32 scratch and no un-swizzle pass.
@@ -925,6 +928,470 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// dK, dV in quads of single-product waves (the grouped walk of the pipelined
+// kernel: one workgroup per 128-key tile of (b, g), a chunk of the position-
+// major walk over the G heads of the group, 32-query tiles).
+//
+// The 8 waves form two quads of 64 keys.  Each wave of a quad computes one
+// product for both of the quad's 32-key blocks, so every LDS operand fragment
+// of the dK^T / dV^T products feeds two products and every row fragment of S
+// / dP two as well:
+//   S wave : S(s) = Q(s) K^T, P(s) = exp2(S scale2 - lse2), masked -> fp32 mailbox
+//   dP wave: Delta(s) - dP(s) = Delta + dO(s) (-V)^T; between its products
+//            dS(s-1) = (P(s-1) (-sm_scale)) (Delta - dP(s-1)) -> bf16 mailbox
+//   dV wave: dV^T += dO(s-2)^T bf16(P(s-2))
+//   dK wave: dK^T += Q(s-2)^T dS(s-2)
+// A quad issues 88 LDS instructions per 64 products (8 + 16 row reads, 32
+// transposed reads, 16 + 16 fp32 mailbox accesses, 8 bf16 mailbox accesses,
+// 8 vector reads) against 128 for two pairs of the pipelined kernel.  The
+// arithmetic is the pipelined kernel's, operation for operation, so the
+// results are bitwise the same.
+//
+// Waves w and w + 4 share SIMD w % 4: w = 0, 2 are the S waves of quads 0, 1
+// and w = 4, 6 their dV waves (the exponentials run under the dV products);
+// w = 1, 3 the dP waves and w = 5, 7 their dK waves (the dS arithmetic runs
+// under the dK products).  The dV and dK waves copy the ring's tiles.
+//
+// One barrier per segment.  The dV wave reads P(s-1) from the mailbox and
+// the first fragments of its next product (tile s-1) at the end of segment s,
+// before the barrier, and the dK wave the first fragments of its next
+// product: after a barrier only the S and dP waves (the new tile) and the dK
+// wave (the 4 dS reads) wait on the LDS.  Tile x is read in segments x (S,
+// dP, lse2, Delta), x+1 (the dV / dK waves' first fragments) and x+2; segment
+// s refills slot (s+3) % 6, tile s-3's, with tile s+3 and waits for tile s+1
+// before its barrier.
+template <bool CAUSAL, bool RAGGED>
+__global__ __launch_bounds__(512, 1) void attn_dkdv_quad_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
+    float* __restrict__ ws_dk, float* __restrict__ ws_dv,
+    __bf16* __restrict__ dk, __bf16* __restrict__ dv,
+    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale,
+    int chunk_tiles, int max_chunks, const DispatchOrder ord, int force_partials, int ws_rows) {
+  constexpr int NSTAGE = 6;
+  constexpr int BQ = 32;                  // query positions per tile
+  constexpr int QT = BQ * HD * 2;         // one 32 x 128 bf16 operand tile
+  constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse2 x 32 | Delta x 32], 1 KiB aligned
+  constexpr int PBOX = 2 * 2 * 4096;      // P mailbox of a quad: 2 slots x 2 key blocks x 32 x 32 fp32
+  constexpr int DBOX = 2 * 4096;          // dS mailbox of a quad: 2 slots x 2 key blocks x 32 x 32 bf16
+  constexpr int QPW = 2;                  // row quads of a tile each copying wave copies
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + 2 * (PBOX + DBOX)];
+
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
+  const int quad = (w >> 1) & 1;
+  const int role = (w & 1) | ((w >> 1) & 2);   // 0 S, 1 dP, 2 dV, 3 dK
+  const int cw = w - 4;                        // copying wave index (dV, dK waves)
+  const int n_kt = (S + 127) / 128;
+  // the work of this workgroup, as in the grouped pipelined kernel
+  const int j = dispatch_item(ord);
+  if (j < 0) return;
+  const int nbg = B * Hkv;
+  const int bg = j % nbg, rr = j / nbg;
+  const int kt = rr / max_chunks;              // heaviest key tiles first
+  const int c = rr - kt * max_chunks;
+  if (kt >= n_kt) return;
+  const int b = bg / Hkv, g = bg - (bg / Hkv) * Hkv;
+  const int n_qt = dkdv_n_qt(S, kt, CAUSAL);
+  const int len = G * n_qt;
+  const int nparts = dkdv_chunks(len, chunk_tiles, max_chunks);
+  if (c >= nparts) return;                     // an empty item of the default numbering
+  const int ustep = nparts;
+  const int n_u = (len - c + nparts - 1) / nparts;
+  const int part = c;
+  const int kw0 = kt * 128 + 64 * quad;        // this quad's first key
+
+  const int q_begin = CAUSAL ? kt * 128 : 0;
+  const long qstride = (long)H * HD;
+  const long grp_rows = ((long)b * S * H + g * G) * HD;
+  const float* vec_src = (h ? delta : lse2) + ((long)b * H + g * G) * S + l32;
+  auto tile_p0 = [&](int t) MM1_INLINE { return q_begin + (n_qt - 1 - t) * BQ; };
+  auto advance = [&](int& hh, int& t) MM1_INLINE {
+    hh += ustep;
+    if (hh >= G) {
+      hh -= G;
+      ++t;
+    }
+  };
+  const uint32_t dma_off = tile_lane_off(qstride, tid);
+  const uint32_t lds_smem = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  // LDS DMA by the copying waves: row quads cw, cw + 4 of Q and of dO; wave
+  // cw == 0 adds the lse2 | Delta vector.
+  auto issue = [&](int slot, int hh, int t) MM1_INLINE {
+    if (w < 4) return;
+    const int p0 = tile_p0(t);
+    const long rows = grp_rows + (long)hh * HD + (long)p0 * qstride;
+    const float* vs = vec_src + (long)hh * S;
+    const uint32_t l = lds_smem + slot * BUF;
+    if (!RAGGED || p0 + BQ <= S) {
+#pragma unroll
+      for (int i = 0; i < QPW; ++i) {
+        const int rq = cw + 4 * i;
+        dma16_sbase(dma_off, q + rows + (long)(4 * rq) * qstride, l + rq * 1024);
+        dma16_sbase(dma_off, dO + rows + (long)(4 * rq) * qstride, l + QT + rq * 1024);
+      }
+      if (cw == 0) dma4(vs + p0, l + 2 * QT);
+    } else {   // same DMA count per wave as a full tile
+#pragma unroll
+      for (int i = 0; i < QPW; ++i) {
+        const int rq = cw + 4 * i;
+        const int row = 4 * rq + (lane >> 4);
+        const int chunk = (lane & 15) ^ swz(row);
+        const long src = rows + (long)min(row, S - p0 - 1) * qstride + 8 * chunk;
+        dma16(q + src, l + rq * 1024);
+        dma16(dO + src, l + QT + rq * 1024);
+      }
+      if (cw == 0) dma4(vs + min(p0, S - 1 - l32), l + 2 * QT);
+    }
+  };
+  int itl = c / G, ih = c - itl * G;           // issue cursor
+  int ch = ih, ctl = itl;                      // compute cursor (tile s of the walk)
+  for (int it = 0; it < NSTAGE - 3 && it < n_u; ++it) {
+    issue(it, ih, itl);
+    advance(ih, itl);
+  }
+
+  // B operands: this lane's key rows of K (S wave) or -V (dP wave), one per
+  // key block
+  bf16x8 breg[2][8];
+  if (role < 2) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int kk = min(kw0 + 32 * kb + l32, S - 1);
+      const __bf16* src = (role == 0 ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+      if (role == 1) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = neg8(breg[kb][ks]);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) pin(breg[kb][ks]);
+    }
+  }
+  f32x16 acc[2][4];   // dV^T (dV wave) or dK^T (dK wave), per key block
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[kb][db] = zero16();
+  }
+  const LdsBases lb = make_lds_bases(lane);
+  float* const pbox = reinterpret_cast<float*>(smem + NSTAGE * BUF + quad * PBOX) + lane * 4;
+  char* const dbox = smem + NSTAGE * BUF + 2 * PBOX + quad * DBOX + lane * 16;
+  const float neg_sm_scale = -sm_scale;
+  wait_dma();
+  __syncthreads();
+
+  constexpr int PFR = MM1_DKDV_PF_ROWS;
+  constexpr int PFT = MM1_DKDV_PF_TR;
+  // S = Q K^T / Delta - dP = Delta + dO (-V)^T of one tile for both key blocks
+  // (accumulated onto c0); each row fragment feeds both
+  auto product2 = [&](const char* t, f32x16 (&sacc)[2], const f32x16& c0, auto&& between) MM1_INLINE {
+    sacc[0] = c0;
+    sacc[1] = c0;
+    mfma_chain<8, PFR>(
+        [&](int ks) MM1_INLINE { return rows_a(t, lb, 0, ks); },
+        [&](int ks, const bf16x8& fa) MM1_INLINE {
+          sacc[0] = mfma32(fa, breg[0][ks], sacc[0]);
+          sacc[1] = mfma32(fa, breg[1][ks], sacc[1]);
+        },
+        between);
+  };
+  // dV^T += dO^T P / dK^T += Q^T dS of one tile: fragment i = 4*kh + db of
+  // tile t feeds the products of both key blocks with B operands bop[kb][kh];
+  // its first PFT fragments were read before the barrier
+  auto tr_frag = [&](const char* t, int i) MM1_INLINE { return tr_a(t, lb, i & 3, i >> 2); };
+  bf16x8 nfa[PFT];
+  auto read_first = [&](const char* t) MM1_INLINE {
+#pragma unroll
+    for (int i = 0; i < PFT; ++i) nfa[i] = tr_frag(t, i);
+  };
+  auto accumulate2 = [&](const char* t, const bf16x8 (&bop)[2][2]) MM1_INLINE {
+    mfma_chain_from<8, PFT>(
+        nfa, [&](int i) MM1_INLINE { return tr_frag(t, i); },
+        [&](int i, const bf16x8& a) MM1_INLINE {
+          acc[0][i & 3] = mfma32(a, bop[0][i >> 2], acc[0][i & 3]);
+          acc[1][i & 3] = mfma32(a, bop[1][i >> 2], acc[1][i & 3]);
+        },
+        [](int) MM1_INLINE {});
+  };
+  // the per-query vector of tile t (lanes 0-31: lse2, 32-63: Delta) in the
+  // D layout: register r holds query 8*(r/4) + 4*h + r%4
+  auto read_vec16 = [&](const char* t, int off) MM1_INLINE {
+    const float* vsrc = reinterpret_cast<const float*>(t + 2 * QT) + off;
+    f32x16 v16;
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(vsrc + 8 * a4 + 4 * h);
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) v16[4 * a4 + cc] = x[cc];
+    }
+    return v16;
+  };
+  // fp32 mailbox block (slot, kb): [a4][lane] x 4 floats, each 16-byte
+  // access of a wave one contiguous 1 KiB row
+  auto pbox_at = [&](int slot, int kb, int a4) MM1_INLINE { return pbox + slot * 2048 + kb * 1024 + 256 * a4; };
+  auto dbox_at = [&](int slot, int jj) MM1_INLINE { return dbox + slot * 4096 + jj * 1024; };
+
+  bf16x8 pb[2][2];      // dV wave: bf16 P(s-2) of both key blocks (B operands)
+  f32x16 dpp[2];        // dP wave: Delta - dP(s-1)
+  // bf16 pack of registers 2j, 2j+1 of x into y[j >> 2] element pair j & 3
+  auto pack_pair = [&](const f32x16& x, bf16x8 (&y)[2], int jj) MM1_INLINE {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) y[jj >> 2][2 * (jj & 3) + e] = (__bf16)x[2 * jj + e];
+    if ((jj & 3) == 3) pin(y[jj >> 2]);
+  };
+
+  // Segment s.  tc, tp, tp2: ring slots of tiles s, s-1, s-2.  CUR: s < n_u;
+  // PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a later segment
+  // reads what this one publishes.
+  auto segment = [&](const char* tc, const char* tp, const char* tp2, int refill, int s, auto rl,
+                     auto cur, auto prev, auto prev2, auto sync) MM1_INLINE {
+    constexpr int RL = decltype(rl)::value;
+    constexpr bool CUR = decltype(cur)::value, PREV = decltype(prev)::value;
+    constexpr bool PREV2 = decltype(prev2)::value, SYNC = decltype(sync)::value;
+    if (CUR && s + NSTAGE - 3 < n_u) {
+      if constexpr (RL >= 2) issue(refill, ih, itl);
+      advance(ih, itl);
+    }
+    if constexpr (RL == 0) {
+      if constexpr (CUR) {
+        f32x16 sv_[2];
+        // the 8 Q fragments, each feeding both key blocks; key block 0's
+        // products first, then key block 1's with the exponentials of block 0
+        // between them (the dV wave's products on the same SIMD run under the
+        // rest of the exponentials)
+        bf16x8 qf[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) qf[ks] = rows_a(tc, lb, 0, ks);
+        const f32x16 l16 = read_vec16(tc, 0);
+        auto exp_at = [&](int kb, int r) MM1_INLINE {
+          float x = exp2_fast(fmaf(sv_[kb][r], scale2, -l16[r]));
+          pin(x);
+          sv_[kb][r] = x;
+        };
+        f32x16 (&sv)[2] = sv_;
+        sv[0] = zero16();
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          __builtin_amdgcn_sched_barrier(0);
+          sv[0] = mfma32(qf[ks], breg[0][ks], sv[0]);
+        }
+        sv[1] = zero16();
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          __builtin_amdgcn_sched_barrier(0);
+          sv[1] = mfma32(qf[ks], breg[1][ks], sv[1]);
+          __builtin_amdgcn_sched_barrier(0);
+          exp_at(0, 2 * ks);
+          exp_at(0, 2 * ks + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) exp_at(1, r);
+        // causal / past-the-end mask, only in the tiles that need it
+        const int p0 = tile_p0(ctl);
+        if ((CAUSAL && p0 < kw0 + 63) || p0 + BQ > S) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            const int key = kw0 + 32 * kb + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int qpos = p0 + 8 * (r >> 2) + 4 * h + (r & 3);
+              sv[kb][r] = ((CAUSAL && key > qpos) || qpos >= S) ? 0.f : sv[kb][r];
+            }
+          }
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4) {
+            f32x4 v4;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) v4[cc] = sv[kb][4 * a4 + cc];
+            *reinterpret_cast<f32x4*>(pbox_at(s & 1, kb, a4)) = v4;
+          }
+        }
+      }
+    } else if constexpr (RL == 1) {
+      // dS(s-1) from P(s-1) (mailbox) and Delta - dP(s-1), between the
+      // products of Delta - dP(s)
+      f32x16 psv[2];
+      auto read_p = [&]() MM1_INLINE {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4) {
+            const f32x4 p4 = *reinterpret_cast<const f32x4*>(pbox_at((s - 1) & 1, kb, a4));
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) psv[kb][4 * a4 + cc] = p4[cc];
+          }
+        }
+      };
+      bf16x8 sbn[2][2];
+      auto ds_pair = [&](int jj) MM1_INLINE {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int r = 2 * jj + e;
+            float x = psv[kb][r] * neg_sm_scale * dpp[kb][r];
+            pin(x);
+            psv[kb][r] = x;
+          }
+          pack_pair(psv[kb], sbn[kb], jj);
+        }
+      };
+      if constexpr (CUR) {
+        // the mailbox is read after the first product (the reads of the new
+        // tile go first) and dS computed two products late
+        const f32x16 d16 = read_vec16(tc, BQ);
+        f32x16 dpn[2];
+        product2(tc + QT, dpn, d16, [&](int ks) MM1_INLINE {
+          if constexpr (PREV) {
+            if (ks == 0) read_p();
+            if (ks >= 2) ds_pair(ks - 2);
+          }
+        });
+        if constexpr (PREV) {
+          ds_pair(6);
+          ds_pair(7);
+        }
+        dpp[0] = dpn[0];
+        dpp[1] = dpn[1];
+      } else if constexpr (PREV) {
+        read_p();
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) ds_pair(jj);
+      }
+      if constexpr (PREV) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh)
+            *reinterpret_cast<bf16x8*>(dbox_at((s - 1) & 1, 2 * kb + kh)) = sbn[kb][kh];
+        }
+      }
+    } else if constexpr (RL == 2) {
+      if constexpr (PREV2) accumulate2(tp2 + QT, pb);
+      if constexpr (PREV) {
+        // for the next segment: bf16 P(s-1) and the first fragments of dO(s-1)^T
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          f32x16 p16;
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4) {
+            const f32x4 p4 = *reinterpret_cast<const f32x4*>(pbox_at((s - 1) & 1, kb, a4));
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) p16[4 * a4 + cc] = p4[cc];
+          }
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) pack_pair(p16, pb[kb], jj);
+        }
+        read_first(tp + QT);
+      }
+    } else {
+      if constexpr (PREV2) {
+        bf16x8 sbp[2][2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh)
+            sbp[kb][kh] = *reinterpret_cast<const bf16x8*>(dbox_at((s - 2) & 1, 2 * kb + kh));
+        }
+        accumulate2(tp2, sbp);
+      }
+      if constexpr (PREV) read_first(tp);   // Q(s-1)^T for the next segment
+    }
+    if constexpr (CUR) advance(ch, ctl);
+    if constexpr (SYNC) {
+      // tile s+1 must have landed; the newer prefetches stay in flight
+      // (2 * QPW copies per tile and copying wave, wave cw == 0 one more)
+      if (w >= 4) {
+        if (s + NSTAGE - 3 < n_u) {
+          if (cw == 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"((2 * QPW + 1) * 2) : "memory");
+          else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * QPW * 2) : "memory");
+        } else {
+          wait_dma();
+        }
+      }
+      lds_barrier();
+    }
+  };
+
+  using T = std::true_type;
+  using F = std::false_type;
+  auto slot = [&](int cc) MM1_INLINE { return smem + cc * BUF; };
+  auto run = [&](auto rl) MM1_INLINE {
+    const char* s0p = slot(0);
+    if (n_u == 1) {
+      segment(s0p, s0p, s0p, NSTAGE - 3, 0, rl, T{}, F{}, F{}, T{});
+      segment(s0p, s0p, s0p, 0, 1, rl, F{}, T{}, F{}, T{});
+      segment(s0p, s0p, s0p, 0, 2, rl, F{}, F{}, T{}, F{});
+      return;
+    }
+    segment(s0p, s0p, s0p, NSTAGE - 3, 0, rl, T{}, F{}, F{}, T{});
+    segment(slot(1), s0p, s0p, NSTAGE - 2, 1, rl, T{}, T{}, F{}, T{});
+    for (int b0 = 2; b0 < n_u; b0 += NSTAGE) {
+      unroll_while<0, NSTAGE>([&](auto jj) MM1_INLINE {
+        constexpr int C = (2 + decltype(jj)::value) % NSTAGE;
+        const int s = b0 + decltype(jj)::value;
+        if (s >= n_u) return false;
+        segment(slot(C), slot((C + NSTAGE - 1) % NSTAGE), slot((C + NSTAGE - 2) % NSTAGE),
+                (C + 3) % NSTAGE, s, rl, T{}, T{}, T{}, T{});
+        return true;
+      });
+    }
+    const char* tl = slot((n_u - 1) % NSTAGE);
+    const char* tl2 = slot((n_u - 2) % NSTAGE);
+    segment(tl, tl, tl2, 0, n_u, rl, F{}, T{}, T{}, T{});
+    segment(tl, tl, tl, 0, n_u + 1, rl, F{}, F{}, T{}, F{});
+  };
+  switch (role) {
+    case 0: run(std::integral_constant<int, 0>{}); break;
+    case 1: run(std::integral_constant<int, 1>{}); break;
+    case 2: run(std::integral_constant<int, 2>{}); break;
+    default: run(std::integral_constant<int, 3>{}); break;
+  }
+  if (role < 2) return;
+
+  // D layout of dK^T / dV^T: register r of block db holds column
+  // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
+  const bool dvw = role == 2;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int key = kw0 + 32 * kb + l32;
+    if (key >= S) continue;
+    if (nparts == 1 && !force_partials) {
+      __bf16* row = (dvw ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          bf16x4 o4;
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) o4[cc] = (__bf16)acc[kb][db][4 * a4 + cc];
+          *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+        }
+      }
+    } else {
+      const long wslot = (long)part * B * ws_rows * Hkv * HD;
+      float* row = (dvw ? ws_dv : ws_dk) + wslot + ((long)(b * ws_rows + key) * Hkv + g) * HD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          f32x4 o4;
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) o4[cc] = acc[kb][db][4 * a4 + cc];
+          *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+        }
+      }
+    }
+  }
+}
+
 // The dK/dV partial sums to reduce, and where the reduction runs.  Two
 // layouts, fp32, dK's slots then dV's:
 //   per-head dK/dV (chunk_tiles == 0): [G][B][S][Hkv][D], slot = query head
@@ -1314,13 +1781,38 @@ static void launch_dkdv_pipe(const __bf16* qp, const __bf16* kp, const __bf16* v
 #undef MM1_DKDV_PIPE
 }
 
+// The quad kernel (grouped grid and chunk plan of the pipelined kernel).
+static void launch_dkdv_quad(const __bf16* qp, const __bf16* kp, const __bf16* vp, const __bf16* dop,
+                             const float* lse2, const float* delta, float* ws_dk, float* ws_dv,
+                             __bf16* dkp, __bf16* dvp, int B, int S, int H, int Hkv, bool causal,
+                             float scale2, float sm_scale, hipStream_t stream, int force_partials = 0) {
+  const int G = H / Hkv;
+  const bool ragged = S % 32 != 0;
+  const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
+  const dim3 grid(plan.order.n ? plan.order.n : plan.n_items), block(512);
+  const int ws_rows = ws_slots(B, S, H, Hkv, causal, 5).rows;
+#define MM1_DKDV_QUAD(CS, RG)                                                                        \
+  hipLaunchKernelGGL((attn_dkdv_quad_kernel<CS, RG>), grid, block, 0, stream, qp, kp, vp, dop, lse2,   \
+                     delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, plan.L, plan.C, \
+                     plan.order, force_partials, ws_rows)
+  if (causal) {
+    if (ragged) MM1_DKDV_QUAD(true, true);
+    else MM1_DKDV_QUAD(true, false);
+  } else {
+    if (ragged) MM1_DKDV_QUAD(false, true);
+    else MM1_DKDV_QUAD(false, false);
+  }
+#undef MM1_DKDV_QUAD
+}
+
 // variant: 0 = attn_dkdv_pipe_kernel over the whole GQA group per key tile
 //              (chunked by dkdv_plan), 8 waves x 32 keys,
 //          1 = attn_dkdv_pipe_kernel, one workgroup per (key tile, query
 //              head), 8 waves x 32 keys,
 //          2 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries),
 //          3 = as 0 with 4 waves x 64 keys (one wave per SIMD),
-//          4 = as 1 with 4 waves x 64 keys.
+//          4 = as 1 with 4 waves x 64 keys,
+//          5 = attn_dkdv_quad_kernel (grouped, quads of single-product waves).
 hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
                            const float* lse2, const float* delta, void* dk, void* dv,
                            void* workspace, int B, int S, int H, int Hkv, bool causal,
@@ -1352,6 +1844,10 @@ hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const vo
     case 4:
       launch_dkdv_pipe<false, 2>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
                                  scale2, sm_scale, stream);
+      break;
+    case 5:
+      launch_dkdv_quad(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal, scale2,
+                       sm_scale, stream);
       break;
     default: {
       const KeyTileOrder order = key_tile_order(B * H);

@@ -87,6 +87,7 @@ const char* const kDkdvTiles[] = {
     "block_M=128 block_N=64 waves=8 stages=3 schedule=paired",
     "block_M=128 block_N=32 waves=4 stages=7 schedule=group",
     "block_M=128 block_N=32 waves=4 stages=7 schedule=pipelined",
+    "block_M=128 block_N=32 waves=8 stages=6 schedule=quad",
 };
 const char* const kDqTiles[] = {
     "block_M=128 block_N=64 waves=4 stages=2 schedule=ring",

@@ -160,7 +160,7 @@ def _bwd_buffers(lib, q, k, v, H, Hkv, device):
     return o, lse, torch.empty_like(lse), ws, nws
 
 
-@pytest.mark.parametrize("dkdv_tiles", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("dkdv_tiles", [0, 1, 2, 3, 4, 5])
 def test_staged_tiling_calls_and_layout_check(hip_device, dkdv_tiles):
     """The staged calls with an explicit tiling (dK/dV, then the separate sum,
     then dQ; and dK/dV, then dQ with the sum in its tail) give the combined
@@ -198,7 +198,7 @@ def test_staged_tiling_calls_and_layout_check(hip_device, dkdv_tiles):
         for name, x, y in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
             assert torch.equal(x, y), (name, tail)
     # a summing call that disagrees with the layout in the workspace
-    grouped = dkdv_tiles in (0, 3)
+    grouped = dkdv_tiles in (0, 3, 5)
     other = 1 if grouped else 0
     sk, sv = torch.full_like(k, 7.0), torch.full_like(v, 7.0)
     assert lib.mm1_attn_bwd_dkdv_reduce_tiles(p(ws), nws, p(sk), p(sv), B, S, H, Hkv, 128, int(causal),
@@ -215,6 +215,34 @@ def test_staged_tiling_calls_and_layout_check(hip_device, dkdv_tiles):
     torch.cuda.synchronize()
     assert bool((sk == 7.0).all()) and bool((sv == 7.0).all()) and bool((sq == 7.0).all()), \
         "a refused call wrote its outputs"
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,causal", [(2, 300, 10, 2, True), (1, 200, 6, 3, False), (1, 77, 4, 4, True),
+                                              (2, 1111, 10, 2, True), (8, 2048, 10, 2, True)],
+                         ids=["B2S300", "B1S200full", "B1S77mha", "B2S1111", "config2"])
+def test_quad_dkdv_tiling_bitwise_equal_to_pair_tiling(hip_device, B, S, H, Hkv, causal):
+    """The quad dK/dV tiling (5) runs the arithmetic of the pipelined pair
+    tiling (0) operation for operation in the same order, on the same chunk
+    plan: dQ, dK and dV are bitwise equal."""
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    log(f"[case] quad vs pair dK/dV tiling B{B} S{S} H{H} Hkv{Hkv} causal={causal}")
+    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S + H))
+    o, lse, delta, ws, nws = _bwd_buffers(lib, q, k, v, H, Hkv, hip_device)
+    sp = torch.cuda.current_stream(hip_device).cuda_stream
+    p = lambda t: t.data_ptr()
+    args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5)
+    assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), *args, sp) == 0
+    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+    outs = []
+    for dkdv_tiles in (0, 5):
+        r = [torch.empty_like(t) for t in (q, k, v)]
+        assert lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), *(p(t) for t in r),
+                                      p(ws), nws, *args, dkdv_tiles, 1, sp) == 0
+        torch.cuda.synchronize()
+        outs.append(r)
+    for name, x, y in zip(("dq", "dk", "dv"), *outs):
+        assert torch.equal(x, y), name
 
 
 @pytest.mark.parametrize("B,S,H,Hkv", [(8, 2048, 10, 2), (2, 8192, 10, 2), (4, 4096, 10, 2), (3, 2999, 10, 2),
