@@ -478,7 +478,7 @@ def test_grouped_dkdv_plan_errors_and_dispatch_switch(lib, monkeypatch):
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 3, 1, 256, plan) == -2
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 0, plan) == -2
     # the dK/dV tiling index is checked by the dispatch-order query
-    assert lib.mm1_attn_dispatch_order(1, 5, 2, 8192, 10, 2, 1, 256, None, 0) == -7
+    assert lib.mm1_attn_dispatch_order(1, lib.mm1_attn_tile_count(1), 2, 8192, 10, 2, 1, 256, None, 0) == -7
     assert lib.mm1_attn_dispatch_order(1, 1, 2, 8192, 10, 2, 1, 256, None, 0) == 0
     monkeypatch.setenv("MM1_DISPATCH_ORDER", "0")
     assert lib.mm1_attn_dkdv_plan(2, 8192, 10, 2, 1, 256, plan) == 0
