@@ -117,7 +117,7 @@ size_t mm1_attn_bwd_noalloc_scratch_size(int B, int S, int H, int Hkv, int D, in
  *    Otherwise, with the per-head tilings (1, 2, 4) it writes the
  *    per-query-head fp32 partial sums into `workspace`
  *    ([2][G][B][S][Hkv][D], G = H / Hkv) and leaves dk/dv untouched; with the
- *    grouped tilings (0, 3) it writes bf16 dk, dv directly for the key tiles
+ *    grouped tilings (0, 3, 5) it writes bf16 dk, dv directly for the key tiles
  *    one workgroup covers and fp32 partials (one slot per chunk, see
  *    mm1_attn_dkdv_plan) for the others.
  *  - mm1_attn_bwd_dkdv_reduce: sums the partials of each KV head and writes
