@@ -369,8 +369,8 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // 128-key tile; a pair of waves owns 32 * KB keys of it, the P wave keeping K
 // and dV^T, the dS wave V and dK^T), but the query tiles are 32 rows and the
 // work on a tile is spread over four segments:
-//   segment s, P wave : S(s+1) = Q(s+1) K^T | P(s) = exp2(S(s) scale2 - lse2), P(s) sm_scale -> mailbox | dV^T += dO(s-1)^T P(s-1)
-//   segment s, dS wave: dP(s) = dO(s) V^T   | dS(s-1) = P(s-1) sm_scale (dP(s-1) - Delta)          | dK^T += Q(s-2)^T dS(s-2)
+//   segment s, P wave : S(s+1) = Q(s+1) K^T                | P(s) = exp2(S(s) scale2 - lse2), -P(s) sm_scale -> mailbox | dV^T += dO(s-1)^T P(s-1)
+//   segment s, dS wave: Delta - dP(s) = Delta + dO(s) (-V)^T | dS(s-1) = (-P(s-1) sm_scale) (Delta - dP(s-1))          | dK^T += Q(s-2)^T dS(s-2)
 // Within a segment each wave's VALU work (middle column) depends on no
 // product of the same segment, so it runs under the wave's own products
 // (and, with two waves per SIMD, the other wave's), and the pair meets at one
@@ -389,8 +389,10 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 //           per wave.  Every LDS operand fragment (a Q / dO row fragment of S
 //           and dP, a transposed dO / Q fragment of dV^T and dK^T) feeds two
 //           products instead of one, which halves the LDS instructions per
-//           product: the LDS pipe (about one instruction per 4 cycles per
-//           CU) is what bounds KB = 1, at 2 LDS instructions per product.
+//           product (KB = 1 issues 2 per product, near the LDS pipe's rate
+//           of about one instruction per 4 cycles per CU); alone on its
+//           SIMD, a wave has no partner to run its VALU work under, and KB =
+//           2 measures slower.
 //
 // Tile x of the ring lives in slot x % NSTAGE; it is first read in segment
 // x-1 and last in segment x+2, so segment s refills slot (s-3) % NSTAGE with
