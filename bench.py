@@ -188,10 +188,13 @@ class Workload:
 
 
 def time_workload(wl, steps, warmup, repeats=5):
-    """W warm-up steps, then `repeats` timed loops of exactly `steps` steps,
-    each bracketed by a device synchronisation, with HIP events on the launch
-    stream after every stage.  Returns the median loop's ms per step, its
-    per-stage ms, and every loop's ms per step."""
+    """W warm-up steps, then `repeats` rounds of two loops of exactly `steps`
+    steps, each loop bracketed by a device synchronisation: the first times
+    the steps alone (HIP events before and after the loop only), the second
+    records an event on the launch stream after every stage for the per-stage
+    times (about 2.5 us per event, which is why the step itself is timed
+    without them).  Returns the median round's ms per step, that round's
+    per-stage ms, and every round's ms per step."""
     import torch
     for _ in range(warmup):
         wl.step()
@@ -199,16 +202,20 @@ def time_workload(wl, steps, warmup, repeats=5):
     ev = lambda: torch.cuda.Event(enable_timing=True)
     loops = []
     for _ in range(repeats):
-        start = ev()
+        start, end = ev(), ev()
+        torch.cuda.synchronize()
+        start.record(wl.stream)
+        for _ in range(steps):
+            wl.step()
+        end.record(wl.stream)
+        torch.cuda.synchronize()
+        step_ms = start.elapsed_time(end) / steps
         marks = [[ev() for _ in Workload.STAGES] for _ in range(steps)]
         begins = [ev() for _ in range(steps)]
         torch.cuda.synchronize()
-        start.record(wl.stream)
         for i in range(steps):
             begins[i].record(wl.stream)
             wl.step(marks[i])
-        end = ev()
-        end.record(wl.stream)
         torch.cuda.synchronize()
         per_stage = {name: 0.0 for name in Workload.STAGES}
         for i in range(steps):
@@ -216,7 +223,7 @@ def time_workload(wl, steps, warmup, repeats=5):
             for name, mk in zip(Workload.STAGES, marks[i]):
                 per_stage[name] += prev.elapsed_time(mk)
                 prev = mk
-        loops.append((start.elapsed_time(end) / steps, {k: v / steps for k, v in per_stage.items()}))
+        loops.append((step_ms, {k: v / steps for k, v in per_stage.items()}))
     order = sorted(range(repeats), key=lambda i: loops[i][0])
     ms, stages = loops[order[repeats // 2]]
     return ms, stages, [round(x[0], 4) for x in loops]
