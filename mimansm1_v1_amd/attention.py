@@ -281,29 +281,14 @@ def autotune(kind, shape, device=None, verbose=False):
             handle = FwdKernel(shape, config)
             results.append((_median_ms(lambda: handle(q, k, v), device), config))
     else:
-        # Each backward tiling is timed inside the training step it runs in
-        # (forward, Delta, backward), and the step's forward + Delta time is
-        # subtracted: timed back to back on their own, the backward's inputs
-        # stay in the caches between calls, which ranks the tilings
-        # differently from the step.
-        fwd = warm
+        out, lse = warm(q, k, v)
         grad_out = rand(batch, seq_len, heads, dim)
-        delta_k = DeltaKernel(batch, heads, seq_len, dim)
+        delta = DeltaKernel(batch, heads, seq_len, dim)(out, grad_out)
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-
-        def front():
-            o, l = fwd(q, k, v)
-            return o, l, delta_k(o, grad_out)
-
-        base = _median_ms(front, device)
         for config in bwd_configs(dim):
             handle = BwdKernel(shape, config)
-
-            def step():
-                o, l, d = front()
-                handle(q, k, v, grad_out, l, d, dq, dk, dv)
-
-            results.append((max(_median_ms(step, device) - base, 0.0), config))
+            results.append((_median_ms(lambda: handle(q, k, v, grad_out, lse, delta, dq, dk, dv),
+                                       device), config))
     if verbose:
         for ms, config in results:
             print(f"    {ms:8.3f} ms  {' '.join(f'{k}={v}' for k, v in config.items())}")
