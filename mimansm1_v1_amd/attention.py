@@ -118,6 +118,24 @@ def _stream(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+# True: the backward runs its dQ launch on a second stream of the device,
+# beside the dK/dV launch and the dK/dV partial sum on the caller's stream
+# (results bitwise equal to the one-stream call).  Measured in the full
+# fwd+bwd step on gfx950 it gains under 1% at B2 S8192 and loses 5-6% at
+# B8 S2048 and B4 S4096 (the two kernels then compete for CUs rather than
+# filling each other's ragged end), so the default is one stream:
+# mm1_attn_bwd_tiles, dK/dV then dQ with the partial sum in its tail.
+OVERLAP_DQ = False
+_SIDE_STREAMS = {}
+
+
+def _side_stream(device) -> "torch.cuda.Stream":
+    stream = _SIDE_STREAMS.get(device)
+    if stream is None:
+        stream = _SIDE_STREAMS[device] = torch.cuda.Stream(device)   # default priority
+    return stream
+
+
 def _require(t: torch.Tensor, name: str, shape, dtype=DTYPE):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
@@ -196,13 +214,36 @@ class BwdKernel(_Kernel):
         ws_bytes = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, D)
         ws = (torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device)
               if ws_bytes else None)
-        rc = lib.mm1_attn_bwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                    grad_out.data_ptr(), lse.data_ptr(), delta.data_ptr(),
-                                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                    ws.data_ptr() if ws is not None else None, ws_bytes,
-                                    B, S, H, Hkv, D, int(self.causal), self.sm_scale,
-                                    *self.tiles, _stream(q.device))
-        _lib.check(rc, "mm1_attn_bwd_tiles")
+        ws_ptr = ws.data_ptr() if ws is not None else None
+        shape = (B, S, H, Hkv, D, int(self.causal), self.sm_scale)
+        dkdv_tiles, dq_tiles = self.tiles
+        if not OVERLAP_DQ:
+            rc = lib.mm1_attn_bwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                        grad_out.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+                                        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws_ptr, ws_bytes,
+                                        *shape, dkdv_tiles, dq_tiles, _stream(q.device))
+            _lib.check(rc, "mm1_attn_bwd_tiles")
+            return
+        main = torch.cuda.current_stream(q.device)
+        side = _side_stream(q.device)
+        fork = torch.cuda.Event()
+        fork.record(main)
+        side.wait_event(fork)
+        rc = lib.mm1_attn_bwd_dq_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
+                                       lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), *shape, dq_tiles,
+                                       side.cuda_stream)
+        _lib.check(rc, "mm1_attn_bwd_dq_tiles")
+        rc = lib.mm1_attn_bwd_dkdv_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
+                                         lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                         ws_ptr, ws_bytes, *shape, dkdv_tiles, main.cuda_stream)
+        _lib.check(rc, "mm1_attn_bwd_dkdv_tiles")
+        rc = lib.mm1_attn_bwd_dkdv_reduce_tiles(ws_ptr, ws_bytes, dk.data_ptr(), dv.data_ptr(),
+                                                B, S, H, Hkv, D, int(self.causal), dkdv_tiles,
+                                                main.cuda_stream)
+        _lib.check(rc, "mm1_attn_bwd_dkdv_reduce_tiles")
+        join = torch.cuda.Event()
+        join.record(side)
+        main.wait_event(join)
 
 
 class DeltaKernel:
