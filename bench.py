@@ -229,8 +229,10 @@ def time_workload(wl, steps, warmup, repeats=5):
     return ms, stages, [round(x[0], 4) for x in loops]
 
 
-def time_autograd(batch, seq, device, steps, warmup):
-    """The same step through the drop-in autograd op (cross-check)."""
+def time_autograd(batch, seq, device, steps, warmup, repeats=5):
+    """The same step through the drop-in autograd op (cross-check): W warm-up
+    steps, then the median of `repeats` timed loops of `steps` steps, as for
+    the kernels' own step (a single loop reads the clock's ramp as well)."""
     import torch
     import mimansm1_v1_amd as mm
     gen = torch.Generator().manual_seed(0)
@@ -244,14 +246,17 @@ def time_autograd(batch, seq, device, steps, warmup):
 
     for _ in range(warmup):
         run()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(steps):
-        run()
-    t1.record()
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+    loops = []
+    for _ in range(repeats):
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            run()
+        t1.record()
+        torch.cuda.synchronize()
+        loops.append(t0.elapsed_time(t1) / steps)
+    return sorted(loops)[repeats // 2]
 
 
 def _timed(fn, steps, warmup):
@@ -598,7 +603,7 @@ def main(argv=None):
             "loops_ms_per_step": loops,
         }
         if not args.no_autograd:
-            res["ms_per_step_autograd"] = time_autograd(B, S, device, args.steps, args.warmup)
+            res["ms_per_step_autograd"] = time_autograd(B, S, device, args.steps, args.warmup, args.repeats)
         results[cfg] = res
         del wl
         torch.cuda.empty_cache()
