@@ -87,19 +87,22 @@ KERNEL_NAMES = {"fwd": ("attn_fwd_pp_kernel", "attn_fwd_kernel", "attn_fwd_kerne
 def select_tiles(batch, seq, override=None):
     """The tilings the tile record (this machine's store, then the shipped
     gfx950 table) holds for this workload -- what get_kernel's handles launch
-    -- or `override` ("FWD,DKDV,DQ").  Returns {stage: index}; the stage
-    calls pass them explicitly."""
+    -- or `override` ("FWD,DKDV,DQ", one stream).  Returns {stage: index}
+    plus "overlap" (the backward record's dQ side-stream switch, else
+    attention.OVERLAP_DQ); the stage calls pass them explicitly."""
+    from mimansm1_v1_amd import attention as A
     if override:
         f, k, q = (int(x) for x in override.split(","))
-        return {"fwd": f, "dkdv": k, "dq": q}
-    from mimansm1_v1_amd import attention as A
+        return {"fwd": f, "dkdv": k, "dq": q, "overlap": False}
     from mimansm1_v1_amd import tuned
     shape = (batch, HEADS, seq, DIM, True, HEADS // KV_HEADS)
     fwd_cfg = tuned.lookup("attention_fwd", shape)
     bwd_cfg = tuned.lookup("attention_bwd", shape)
     fwd = A.tile_index("fwd", fwd_cfg) if fwd_cfg else None
     bwd = A.tile_index("bwd", bwd_cfg) if bwd_cfg else None
-    return {"fwd": fwd or 0, "dkdv": (bwd or (0, 0))[0], "dq": (bwd or (0, 0))[1]}
+    overlap = bool((bwd_cfg or {}).get("overlap_dq", A.OVERLAP_DQ)) if bwd else A.OVERLAP_DQ
+    return {"fwd": fwd or 0, "dkdv": (bwd or (0, 0))[0], "dq": (bwd or (0, 0))[1],
+            "overlap": overlap}
 
 
 def rope_rotate(x, theta=10_000.0):
@@ -151,11 +154,17 @@ class Workload:
         self.ws = torch.empty(max(self.ws_bytes // 4, 1), dtype=torch.float32, device=device)
         self.scale = DIM ** -0.5
         self.stream = torch.cuda.current_stream(device)
+        self.side = torch.cuda.Stream(device)   # default priority
 
     STAGES = ("fwd", "delta", "dkdv", "dq")
 
     def step(self, marks=None):
-        """One fwd+bwd; if `marks` is given, records an event after each stage."""
+        """One fwd+bwd; if `marks` is given, records an event after each stage.
+        Without `marks`, and when the tile record says so (tiles["overlap"]),
+        the backward runs as BwdKernel then does: dQ on a second stream beside
+        dK/dV, the dK/dV partial sum after dK/dV on the launch stream.  With
+        `marks` the stages run one after the other on the launch stream (dQ
+        with the partial sum in its tail), for the per-kernel times."""
         L, B, S, H, Hkv, D, sp = self.lib, self.B, self.S, self.H, self.Hkv, self.D, self.stream.cuda_stream
         p = lambda t: t.data_ptr()
 
@@ -171,6 +180,23 @@ class Workload:
         chk(L.mm1_attn_delta(p(self.o), p(self.do), p(self.delta), B, S, H, D, sp), "delta")
         if marks is not None:
             marks[1].record(self.stream)
+        if marks is None and t.get("overlap"):
+            import torch
+            fork = torch.cuda.Event()
+            fork.record(self.stream)
+            self.side.wait_event(fork)
+            chk(L.mm1_attn_bwd_dq_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
+                                        p(self.delta), p(self.dq), B, S, H, Hkv, D, 1, self.scale,
+                                        t["dq"], self.side.cuda_stream), "dq")
+            chk(L.mm1_attn_bwd_dkdv_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
+                                          p(self.delta), p(self.dk), p(self.dv), p(self.ws), self.ws_bytes,
+                                          B, S, H, Hkv, D, 1, self.scale, t["dkdv"], sp), "dkdv")
+            chk(L.mm1_attn_bwd_dkdv_reduce_tiles(p(self.ws), self.ws_bytes, p(self.dk), p(self.dv),
+                                                 B, S, H, Hkv, D, 1, t["dkdv"], sp), "dkdv reduce")
+            join = torch.cuda.Event()
+            join.record(self.side)
+            self.stream.wait_event(join)
+            return
         chk(L.mm1_attn_bwd_dkdv_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
                                       p(self.delta), p(self.dk), p(self.dv), p(self.ws), self.ws_bytes,
                                       B, S, H, Hkv, D, 1, self.scale, t["dkdv"], sp), "dkdv")

@@ -90,6 +90,9 @@ def tile_index(kind, config):
     if kind == "fwd":
         space = tile_space("fwd")
         return space.index(config) if config in space else None
+    # a backward record may also say how its two launches share the device
+    if not isinstance(config.pop("overlap_dq", False), bool):
+        return None
     parts = {}
     for sub in ("dkdv", "dq"):
         cut = len(sub) + 1
@@ -120,11 +123,12 @@ def _stream(device) -> int:
 
 # True: the backward runs its dQ launch on a second stream of the device,
 # beside the dK/dV launch and the dK/dV partial sum on the caller's stream
-# (results bitwise equal to the one-stream call).  Measured in the full
-# fwd+bwd step on gfx950 it gains under 1% at B2 S8192 and loses 5-6% at
-# B8 S2048 and B4 S4096 (the two kernels then compete for CUs rather than
-# filling each other's ragged end), so the default is one stream:
-# mm1_attn_bwd_tiles, dK/dV then dQ with the partial sum in its tail.
+# (results bitwise equal to the one-stream call).  A backward tile record's
+# "overlap_dq" entry overrides this default per shape.  Measured in the full
+# fwd+bwd step on gfx950 it gains 0.9% at B2 S8192 (whose dK/dV grid of long
+# causal chunks has the longest tail) and loses 5-6% at B8 S2048 and B4
+# S4096, so the default is one stream: mm1_attn_bwd_tiles, dK/dV then dQ
+# with the partial sum in its tail.
 OVERLAP_DQ = False
 _SIDE_STREAMS = {}
 
@@ -217,7 +221,7 @@ class BwdKernel(_Kernel):
         ws_ptr = ws.data_ptr() if ws is not None else None
         shape = (B, S, H, Hkv, D, int(self.causal), self.sm_scale)
         dkdv_tiles, dq_tiles = self.tiles
-        if not OVERLAP_DQ:
+        if not self.config.get("overlap_dq", OVERLAP_DQ):
             rc = lib.mm1_attn_bwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                         grad_out.data_ptr(), lse.data_ptr(), delta.data_ptr(),
                                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws_ptr, ws_bytes,

@@ -221,24 +221,26 @@ def test_staged_tiling_calls_and_layout_check(hip_device, dkdv_tiles):
                          ids=["B2S1111", "config2", "B1S77mha"])
 def test_backward_dq_overlap_matches_single_stream(hip_device, monkeypatch, B, S, H, Hkv):
     """The backward handle with dQ on a second stream beside dK/dV and the
-    separate partial sum (the OVERLAP_DQ option, off by default) gives the
-    single-stream mm1_attn_bwd_tiles result bitwise."""
+    separate partial sum (a tile record's "overlap_dq", or the OVERLAP_DQ
+    default) gives the single-stream mm1_attn_bwd_tiles result bitwise."""
     from mimansm1_v1_amd import attention as A
     log(f"[case] dQ overlap vs one stream B{B} S{S} H{H} Hkv{Hkv}")
     q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S + 1))
     shape = (B, H, S, 128, True, H // Hkv)
     o, lse = A.FwdKernel(shape, A.FWD_TILES)(q, k, v)
     delta = A.DeltaKernel(B, H, S, 128)(o, do)
-    bwd = A.BwdKernel(shape, A.BWD_TILES)
     outs = []
-    for overlap in (False, True):
-        monkeypatch.setattr(A, "OVERLAP_DQ", overlap)
+    for config, default in ((dict(A.BWD_TILES, overlap_dq=False), True),
+                            (dict(A.BWD_TILES, overlap_dq=True), False),
+                            (dict(A.BWD_TILES), True)):
+        monkeypatch.setattr(A, "OVERLAP_DQ", default)   # the record's entry wins
         grads = [torch.full_like(t, 3.0) for t in (q, k, v)]
-        bwd(q, k, v, do, lse, delta, *grads)
+        A.BwdKernel(shape, config)(q, k, v, do, lse, delta, *grads)
         torch.cuda.synchronize()
         outs.append(grads)
-    for name, x, y in zip(("dq", "dk", "dv"), *outs):
-        assert torch.equal(x, y), name
+    for other in outs[1:]:
+        for name, x, y in zip(("dq", "dk", "dv"), outs[0], other):
+            assert torch.equal(x, y), name
 
 
 @pytest.mark.parametrize("B,S,H,Hkv,causal", [(2, 300, 10, 2, True), (1, 200, 6, 3, False), (1, 77, 4, 4, True),

@@ -194,6 +194,18 @@ def test_shipped_tile_table_names_compiled_tilings():
                 assert A.tile_index(kind, entries[key]) is not None, (key, entries[key])
 
 
+def test_backward_record_overlap_entry():
+    """A backward tile record may carry "overlap_dq" (how its two launches
+    share the device) beside its tilings; anything but a bool there, or an
+    unknown key, names no tiling."""
+    base = dict(A.BWD_TILES)
+    assert A.tile_index("bwd", dict(base, overlap_dq=True)) == A.tile_index("bwd", base) == (0, 0)
+    assert A.tile_index("bwd", dict(base, overlap_dq=False)) == (0, 0)
+    assert A.tile_index("bwd", dict(base, overlap_dq="yes")) is None
+    assert A.tile_index("bwd", dict(base, overlap=True)) is None
+    assert A.tile_index("fwd", dict(A.FWD_TILES, overlap_dq=True)) is None
+
+
 def test_tune_cli_shapes_and_control_flow():
     """stage_shapes follows the stage switch (tune.py:30-46): 8 x 2048 then
     2 x 8192; tune_all skips known entries unless forced, records each
