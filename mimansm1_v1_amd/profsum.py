@@ -7,8 +7,11 @@
         --copy-write DIR/pmc_copy_write/cw_counter_collection.csv \\
         --copy-bytes 1073741824 [--json profiles/traffic_config3.json]
 
-Kernel times come from the ``top_kernels`` view of the ``--kernel-trace
---stats`` database.  FETCH_SIZE / WRITE_SIZE (KiB per dispatch, averaged over a
+Kernel times come from the ``--kernel-trace --stats`` database: calls, mean
+and share from its ``top_kernels`` view, and from the per-dispatch ``kernels``
+view the median and the same figures over the dispatches that ran alone (no
+other dispatch of the trace overlapped them in time; a backward that runs dQ
+on a second stream beside dK/dV gives both kinds).  FETCH_SIZE / WRITE_SIZE (KiB per dispatch, averaged over a
 kernel's dispatches) are scaled by the factors that make the same counters read
 ``--copy-bytes`` for the plain device copy of that many bytes (the largest
 dispatch of the calibration runs).
@@ -41,6 +44,41 @@ def trace_table(db: str):
     con = sqlite3.connect(db)
     rows = con.execute("select name, total_calls, average, percentage from top_kernels").fetchall()
     return [(kernel_key(n), n.split("(")[0].replace("void ", ""), c, avg, pct) for n, c, avg, pct in rows]
+
+
+def _median(xs):
+    xs = sorted(xs)
+    n = len(xs)
+    return None if n == 0 else (xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2]))
+
+
+def dispatch_stats(spans):
+    """spans: (name, start, end) per dispatch, in ns.  Returns {name: (all
+    durations, durations of the dispatches no other dispatch overlapped)} in
+    µs."""
+    order = sorted(range(len(spans)), key=lambda i: spans[i][1])
+    alone = [True] * len(spans)
+    reach, owner = None, None   # latest end among the dispatches started so far, and whose
+    for i in order:
+        _, start, end = spans[i]
+        if reach is not None and start < reach:
+            alone[i] = False
+            alone[owner] = False
+        if reach is None or end > reach:
+            reach, owner = end, i
+    out = defaultdict(lambda: ([], []))
+    for i, (name, start, end) in enumerate(spans):
+        us = (end - start) / 1e3
+        out[name][0].append(us)
+        if alone[i]:
+            out[name][1].append(us)
+    return dict(out)
+
+
+def trace_dispatches(db: str):
+    con = sqlite3.connect(db)
+    spans = con.execute("select name, start, end from kernels").fetchall()
+    return dispatch_stats([(n.split("(")[0].replace("void ", ""), s, e) for n, s, e in spans])
 
 
 def counter_means(path: str):
@@ -79,9 +117,16 @@ def main(argv=None):
     args = ap.parse_args(argv)
 
     if args.trace:
-        print("| kernel | calls | avg µs | share |\n|---|---:|---:|---:|")
+        per = trace_dispatches(args.trace)
+        print("| kernel | calls | avg µs | median µs | share | calls alone | avg alone µs | median alone µs |\n"
+              "|---|---:|---:|---:|---:|---:|---:|---:|")
         for _, full, calls, avg, pct in trace_table(args.trace):
-            print(f"| `{full}` | {calls} | {avg:.1f} | {pct:.1f}% |")
+            every, solo = per.get(full, ([], []))
+            med = _median(every)
+            solo_avg = sum(solo) / len(solo) if solo else None
+            fmt = lambda x: "-" if x is None else f"{x:.1f}"
+            print(f"| `{full}` | {calls} | {avg:.1f} | {fmt(med)} | {pct:.1f}% | {len(solo)} | "
+                  f"{fmt(solo_avg)} | {fmt(_median(solo))} |")
         print()
     if args.fetch and args.write and args.copy_fetch and args.copy_write:
         kib = args.copy_bytes / 1024

@@ -260,6 +260,10 @@ def test_profsum_tables(tmp_path, capsys):
     con = sqlite3.connect(db)
     con.execute("create table top_kernels (name, total_calls, total_duration, average, percentage)")
     con.execute("insert into top_kernels values ('void mm1::attn_fwd_kernel<4, 2, true>(int)', 3, 30.0, 10.0, 100.0)")
+    con.execute("create table kernels (name, start, end)")
+    for start, end in ((0, 8_000), (10_000, 20_000), (30_000, 42_000)):
+        con.execute("insert into kernels values ('void mm1::attn_fwd_kernel<4, 2, true>(int)', ?, ?)",
+                    (start, end))
     con.commit()
     con.close()
     hdr = "Kernel_Name,Counter_Name,Counter_Value\n"
@@ -273,7 +277,7 @@ def test_profsum_tables(tmp_path, capsys):
                   "--copy-fetch", str(tmp_path / "cf.csv"), "--copy-write", str(tmp_path / "cw.csv"),
                   "--copy-bytes", str(1 << 20), "--json", str(out)])
     text = capsys.readouterr().out
-    assert "attn_fwd_kernel<4, 2, true>" in text and "| 3 | 10.0 |" in text
+    assert "attn_fwd_kernel<4, 2, true>" in text and "| 3 | 10.0 | 10.0 | 100.0% | 3 | 10.0 | 10.0 |" in text
     # mean fetch 20 KiB x 2 (copy read 512 KiB for 1 MiB) + 4 KiB writes x 1
     assert json.loads(out.read_text())["fwd"] == (20 * 2 + 4) * 1024
 
@@ -307,3 +311,19 @@ def test_wgrad_chunking_equals_one_product(monkeypatch, t, chunks):
     assert torch.allclose(got, want, atol=1e-4, rtol=1e-5)
     chunked = chunks > 1 and t % chunks == 0 and t >= 64 * chunks
     assert calls == (["bmm"] if chunked else ["mm"])
+
+
+def test_profsum_separates_dispatches_that_ran_alone():
+    """profsum's per-dispatch split: a dispatch counts as alone only when no
+    other dispatch of the trace overlapped it (touching ends do not)."""
+    from mimansm1_v1_amd.profsum import dispatch_stats
+    spans = [("a", 0, 10_000), ("b", 5_000, 15_000),          # overlap each other
+             ("c", 20_000, 30_000), ("c", 30_000, 40_000),    # touch only
+             ("d", 41_000, 100_000), ("e", 42_000, 45_000),   # e inside d
+             ("c", 60_000, 70_000),                           # inside d too
+             ("a", 200_000, 210_000)]
+    st = dispatch_stats(spans)
+    assert st["a"] == ([10.0, 10.0], [10.0])
+    assert st["b"] == ([10.0], [])
+    assert st["c"] == ([10.0, 10.0, 10.0], [10.0, 10.0])
+    assert st["d"] == ([59.0], []) and st["e"] == ([3.0], [])
