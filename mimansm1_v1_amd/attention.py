@@ -125,10 +125,11 @@ def _stream(device) -> int:
 # beside the dK/dV launch and the dK/dV partial sum on the caller's stream
 # (results bitwise equal to the one-stream call).  A backward tile record's
 # "overlap_dq" entry overrides this default per shape.  Measured in the full
-# fwd+bwd step on gfx950 it gains 0.9% at B2 S8192 (whose dK/dV grid of long
-# causal chunks has the longest tail) and loses 5-6% at B8 S2048 and B4
-# S4096, so the default is one stream: mm1_attn_bwd_tiles, dK/dV then dQ
-# with the partial sum in its tail.
+# fwd+bwd step on gfx950 it gains 0.6-0.9% with the 256-row dQ tiling (one
+# workgroup per CU) at B2 S8192 and B4 S4096 and loses 4-7% with the
+# 128-row one (two per CU), so the default is one stream (mm1_attn_bwd_tiles:
+# dK/dV, then dQ with the partial sum in its tail) and the shipped records
+# switch it on where it was measured faster.
 OVERLAP_DQ = False
 _SIDE_STREAMS = {}
 
