@@ -839,3 +839,24 @@ def test_bf16_linear_projection(hip_device, shape):
     log(f"    dX rel_l2 {e_dx:.2e} (autograd {e_dx_ag:.2e}); dW rel_l2 {e_dw:.2e} (autograd {e_dw_ag:.2e})")
     assert outs["fn"][1].dtype == x.dtype and outs["fn"][2].dtype == w.dtype
     assert e_dx < 5e-3 and e_dw < 1e-4 and e_dw <= e_dw_ag + 1e-6
+
+
+@pytest.mark.parametrize("S", [1111, 2048])
+def test_bench_overlapped_step_matches_staged_step(hip_device, S):
+    """bench.py's timed step with dQ beside dK/dV on a second stream (what a
+    tile record with overlap_dq runs) writes the same O, lse2, dQ, dK and dV,
+    bitwise, as its per-stage step on one stream."""
+    import bench
+    from mimansm1_v1_amd import _lib
+    log(f"[case] bench step overlapped vs staged B1 S{S}")
+    wl = bench.Workload(_lib.load(), 1, S, hip_device, {"fwd": 0, "dkdv": 0, "dq": 1, "overlap": True})
+    outs = []
+    for staged in (False, True):
+        for t in (wl.o, wl.lse, wl.dq, wl.dk, wl.dv):
+            t.fill_(7.0)
+        marks = [torch.cuda.Event() for _ in bench.Workload.STAGES] if staged else None
+        wl.step(marks)
+        torch.cuda.synchronize()
+        outs.append([t.clone() for t in (wl.o, wl.lse, wl.dq, wl.dk, wl.dv)])
+    for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), *outs):
+        assert torch.equal(x, y), name
