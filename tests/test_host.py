@@ -327,3 +327,21 @@ def test_profsum_separates_dispatches_that_ran_alone():
     assert st["b"] == ([10.0], [])
     assert st["c"] == ([10.0, 10.0, 10.0], [10.0, 10.0])
     assert st["d"] == ([59.0], []) and st["e"] == ([3.0], [])
+
+
+def test_bench_select_tiles_follows_the_record(monkeypatch):
+    """bench.py launches what the tile record names, including the dQ
+    side-stream switch; an explicit --tiles override runs on one stream."""
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    import bench
+    records = {"attention_fwd": dict(A.FWD_TILES),
+               "attention_bwd": dict(A.BWD_TILES, dq_block_M=256, dq_waves=8, dq_stages=3,
+                                     overlap_dq=True)}
+    monkeypatch.setattr(tuned, "lookup", lambda name, shape: records.get(name))
+    assert bench.select_tiles(2, 8192) == {"fwd": 0, "dkdv": 0, "dq": 1, "overlap": True}
+    records["attention_bwd"].pop("overlap_dq")
+    monkeypatch.setattr(A, "OVERLAP_DQ", True)
+    assert bench.select_tiles(2, 8192)["overlap"] is True       # the module default
+    monkeypatch.setattr(A, "OVERLAP_DQ", False)
+    assert bench.select_tiles(2, 8192)["overlap"] is False
+    assert bench.select_tiles(2, 8192, "1,5,0") == {"fwd": 1, "dkdv": 5, "dq": 0, "overlap": False}
