@@ -580,8 +580,8 @@ def main(argv=None):
     args = parse(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box in this setup has one MI355X, so "
-              f"--gpus {args.gpus} is not supported (the attention shards per (batch, KV head) "
-              f"with no exchange; see DESIGN.md).", file=sys.stderr)
+              f"--gpus {args.gpus} is not supported (the attention would shard per (batch, KV "
+              f"head), each GPU computing its share with no exchange).", file=sys.stderr)
         return 2
     sys.path.insert(0, str(ROOT))
     import torch

@@ -1,8 +1,8 @@
 """Formats the parity records a GPU test run leaves (MM1_PARITY_LOG, one JSON
 object per checked output, written by tests/parity.py) as a markdown table.
 
-    MM1_PARITY_LOG=gpurun_out/parity.jsonl python -m pytest tests -m gpu ...
-    python tests/parity_table.py gpurun_out/parity.jsonl [--cases config,golden,ragged]
+    MM1_PARITY_LOG=/tmp/parity.jsonl python -m pytest tests -m gpu ...
+    python tests/parity_table.py /tmp/parity.jsonl [--cases config,golden,ragged]
 """
 from __future__ import annotations
 
