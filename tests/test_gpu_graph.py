@@ -80,6 +80,28 @@ def test_attention_step_graph_replays(hip_device, B, S, tiles):
     _replay_and_compare(step, [o, lse, delta, dq, dk, dv])
 
 
+@pytest.mark.parametrize("S", [777, 2048])
+def test_overlapped_backward_graph_replays(hip_device, S):
+    """The backward handle with a tile record that puts dQ on a second stream
+    (fork from the caller's stream by an event, join back by another) captures
+    as one graph: every replay equals the eager call bitwise."""
+    from mimansm1_v1_amd import attention as A
+    H, Hkv, D = 10, 2, 128
+    log(f"[case] overlapped backward graph B=1 S={S}")
+    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(1, S, H, Hkv, D, seed=S + 3))
+    shape = (1, H, S, D, True, H // Hkv)
+    o, lse = A.FwdKernel(shape, A.FWD_TILES)(q, k, v)
+    delta = A.DeltaKernel(1, H, S, D)(o, do)
+    config = dict(A.BWD_TILES, dq_block_M=256, dq_waves=8, dq_stages=3, overlap_dq=True)
+    bwd = A.BwdKernel(shape, config)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+    def step(_sp):   # the handle launches on torch's current stream (and its side stream)
+        bwd(q, k, v, do, lse, delta, dq, dk, dv)
+
+    _replay_and_compare(step, [dq, dk, dv])
+
+
 def test_swiglu_and_head_graph_replays(hip_device):
     from mimansm1_v1_amd import _lib
     from mimansm1_v1_amd import swiglu as SG
