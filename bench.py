@@ -6,18 +6,21 @@
 A step is one forward + backward of the attention op over one batch of the
 BASELINE.json workload (default config 3: batch 2, seq 8192, 10 query heads,
 2 KV heads, head_dim 128, causal, bf16, synthetic N(0,1) inputs resident in
-HBM).  The step runs exactly the kernels ``FlashAttention`` runs -- forward,
-Delta, dK/dV, dQ with the dK/dV group sum in its tail -- through the library's C ABI, with HIP
-events between them on the launch stream so every kernel's average duration
-is measured live over the timed region.
+HBM).  The step runs exactly the kernels ``FlashAttention`` runs -- the
+forward (K/V conversion, attention), the backward's prep (Delta, fp16 dO),
+dK/dV, dQ with the dK/dV group sum in its tail -- through the library's C
+ABI, and a second loop records HIP events between the stages on the launch
+stream so every stage's average duration is measured live.
 
 Printed: one JSON line.  ``value`` is algorithmic TFLOP/s of the whole step
 (7 * B * H * S^2 * D for causal fwd+bwd: fwd 2 GEMMs + bwd 5 GEMMs of
 2*S^2*D/2 each per head), from the median of --repeats timed loops of
 --steps steps; ``roofline`` is the dominant kernel's algorithmic TFLOP/s
-against the bf16 dense MFMA peak; ``cpu_baseline`` is the fp32 reference math
-(oracle, torch autograd) timed on this host's cores on the same workload (or
-one batch element of it when host RAM is short).
+against the bf16 dense MFMA peak (the fp16 products of the kernels run at the
+same rate); ``cpu_baseline`` is the fp32 reference math (oracle, torch
+autograd) timed on this host's cores on the same workload (or one batch
+element of it when host RAM is short), and each extra config carries its own;
+``gpu_clock`` is the shader clock sampled while the timed loops ran.
 """
 from __future__ import annotations
 
@@ -79,8 +82,7 @@ def parse(argv=None):
 
 # Kernel launched by each tiling index of a stage (mm1_attn_tile_desc order).
 KERNEL_NAMES = {"fwd": ("attn_fwd_pp_kernel", "attn_fwd_kernel", "attn_fwd_kernel"),
-                "dkdv": ("attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel", "attn_dkdv_kernel",
-                         "attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel", "attn_dkdv_quad_kernel"),
+                "dkdv": ("attn_dkdv_pipe_kernel", "attn_dkdv_pipe_kernel"),
                 "dq": ("attn_dq_kernel", "attn_dq_kernel")}
 
 
@@ -146,17 +148,18 @@ class Workload:
         self.q, self.k, self.v, self.do = dev(q), dev(k), dev(v), dev(do)
         self.o = torch.empty_like(self.q)
         self.lse = torch.empty(batch, HEADS, seq, dtype=torch.float32, device=device)
-        self.delta = torch.empty_like(self.lse)
         self.dq = torch.empty_like(self.q)
         self.dk = torch.empty_like(self.k)
         self.dv = torch.empty_like(self.v)
+        self.st_bytes = lib.mm1_attn_fwd_state_size(batch, seq, HEADS, KV_HEADS, DIM)
+        self.state = torch.empty(self.st_bytes, dtype=torch.uint8, device=device)
         self.ws_bytes = lib.mm1_attn_bwd_workspace_size(batch, seq, HEADS, KV_HEADS, DIM)
-        self.ws = torch.empty(max(self.ws_bytes // 4, 1), dtype=torch.float32, device=device)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
         self.scale = DIM ** -0.5
         self.stream = torch.cuda.current_stream(device)
         self.side = torch.cuda.Stream(device)   # default priority
 
-    STAGES = ("fwd", "delta", "dkdv", "dq")
+    STAGES = ("fwd", "prep", "dkdv", "dq")
 
     def step(self, marks=None):
         """One fwd+bwd; if `marks` is given, records an event after each stage.
@@ -164,7 +167,7 @@ class Workload:
         the backward runs as BwdKernel then does: dQ on a second stream beside
         dK/dV, the dK/dV partial sum after dK/dV on the launch stream.  With
         `marks` the stages run one after the other on the launch stream (dQ
-        with the partial sum in its tail), for the per-kernel times."""
+        with the partial sum in its tail), for the per-stage times."""
         L, B, S, H, Hkv, D, sp = self.lib, self.B, self.S, self.H, self.Hkv, self.D, self.stream.cuda_stream
         p = lambda t: t.data_ptr()
 
@@ -173,11 +176,14 @@ class Workload:
                 raise RuntimeError(f"{name}: {L.mm1_attn_strerror(rc).decode()}")
 
         t = self.tiles
-        chk(L.mm1_attn_fwd_tiles(p(self.q), p(self.k), p(self.v), p(self.o), p(self.lse),
-                                 B, S, H, Hkv, D, 1, self.scale, t["fwd"], sp), "fwd")
+        st = (p(self.state), self.st_bytes)
+        ws = (p(self.ws), self.ws_bytes)
+        shape = (B, S, H, Hkv, D, 1, self.scale)
+        chk(L.mm1_attn_fwd_tiles(p(self.q), p(self.k), p(self.v), p(self.o), p(self.lse), *st, *shape,
+                                 t["fwd"], sp), "fwd")
         if marks is not None:
             marks[0].record(self.stream)
-        chk(L.mm1_attn_delta(p(self.o), p(self.do), p(self.delta), B, S, H, D, sp), "delta")
+        chk(L.mm1_attn_bwd_prep(p(self.o), p(self.do), *st, *ws, B, S, H, Hkv, D, self.scale, sp), "prep")
         if marks is not None:
             marks[1].record(self.stream)
         if marks is None and t.get("overlap"):
@@ -185,30 +191,24 @@ class Workload:
             fork = torch.cuda.Event()
             fork.record(self.stream)
             self.side.wait_event(fork)
-            chk(L.mm1_attn_bwd_dq_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
-                                        p(self.delta), p(self.dq), B, S, H, Hkv, D, 1, self.scale,
-                                        t["dq"], self.side.cuda_stream), "dq")
-            chk(L.mm1_attn_bwd_dkdv_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
-                                          p(self.delta), p(self.dk), p(self.dv), p(self.ws), self.ws_bytes,
-                                          B, S, H, Hkv, D, 1, self.scale, t["dkdv"], sp), "dkdv")
-            chk(L.mm1_attn_bwd_dkdv_reduce_tiles(p(self.ws), self.ws_bytes, p(self.dk), p(self.dv),
-                                                 B, S, H, Hkv, D, 1, t["dkdv"], sp), "dkdv reduce")
+            chk(L.mm1_attn_bwd_dq_tiles(p(self.lse), *st, p(self.dq), *ws, *shape, t["dq"],
+                                        self.side.cuda_stream), "dq")
+            chk(L.mm1_attn_bwd_dkdv_tiles(p(self.lse), *st, p(self.dk), p(self.dv), *ws, *shape, t["dkdv"], sp),
+                "dkdv")
+            chk(L.mm1_attn_bwd_dkdv_reduce_tiles(*ws, p(self.dk), p(self.dv), B, S, H, Hkv, D, 1, t["dkdv"], sp),
+                "dkdv reduce")
             join = torch.cuda.Event()
             join.record(self.side)
             self.stream.wait_event(join)
             return
-        chk(L.mm1_attn_bwd_dkdv_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
-                                      p(self.delta), p(self.dk), p(self.dv), p(self.ws), self.ws_bytes,
-                                      B, S, H, Hkv, D, 1, self.scale, t["dkdv"], sp), "dkdv")
+        chk(L.mm1_attn_bwd_dkdv_tiles(p(self.lse), *st, p(self.dk), p(self.dv), *ws, *shape, t["dkdv"], sp),
+            "dkdv")
         if marks is not None:
             marks[2].record(self.stream)
         # dQ, with the dK/dV group sum folded into the same launch (what
-        # mm1_attn_bwd runs after mm1_attn_bwd_dkdv)
-        chk(L.mm1_attn_bwd_dq_reduce_tiles(p(self.q), p(self.k), p(self.v), p(self.do), p(self.lse),
-                                           p(self.delta), p(self.dq), p(self.dk), p(self.dv),
-                                           p(self.ws), self.ws_bytes, B, S, H, Hkv, D, 1, self.scale,
-                                           t["dkdv"], t["dq"], sp),
-            "dq")
+        # mm1_attn_bwd runs after the dK/dV stage)
+        chk(L.mm1_attn_bwd_dq_reduce_tiles(p(self.lse), *st, p(self.dq), p(self.dk), p(self.dv), *ws, *shape,
+                                           t["dkdv"], t["dq"], sp), "dq")
         if marks is not None:
             marks[3].record(self.stream)
 

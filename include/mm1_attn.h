@@ -4,17 +4,37 @@
  * (CODE/mimans/model/attention_tilelang.py).  Plain C: bf16 tensors are passed
  * as `void*`, fp32 tensors as `float*`, the HIP stream as `void*`
  * (a hipStream_t; NULL = the default stream).  The caller owns every buffer;
- * the library allocates no device memory, never synchronises and is safe to
- * call from several host threads.  Its only state is host-side: a cache of
- * per-shape workgroup dispatch tables (mm1_attn_dispatch_order) and, per
- * backward workspace, the layout of the dK/dV partial sums the last
- * mm1_attn_bwd_dkdv* call on it wrote (checked by the calls that sum them).
+ * the library allocates no device memory (apart from the static scratch of
+ * mm1_attn_bwd_noalloc, below), never synchronises and is safe to call from
+ * several host threads.  Its only host state is a cache of per-shape
+ * workgroup dispatch tables (mm1_attn_dispatch_order) and, per backward
+ * workspace address, the layout of the dK/dV partial sums the last
+ * mm1_attn_bwd_dkdv_tiles call on it wrote (checked by the calls that sum
+ * them).
  *
  * Layouts (all contiguous, last dimension stride 1):
  *   q, o, dO, dq : [B, S, H,   D] bf16
  *   k, v, dk, dv : [B, S, Hkv, D] bf16
  *   lse2, delta  : [B, H, S]      fp32
  * Requirements: B >= 1, S >= 1, H % Hkv == 0, D == 128, sm_scale > 0.
+ *
+ * Operand precision.  The products run on the matrix cores with fp16
+ * operands and fp32 accumulation.  The library converts q, k, v (and dO,
+ * after scaling it by a power of two chosen from max|dO| and max|V|) to fp16
+ * copies, which is exact for bf16 values of magnitude in [2^-17, 65504];
+ * q, k and v must lie within fp16's range (|x| <= 65504; smaller values lose
+ * at most 2^-25 absolutely).  The softmax weights P and the score gradients
+ * dS are rounded to fp16 (11 significant bits) before their products; the
+ * reference rounds them to bf16 (8 bits, attention_tilelang.py:178-180,
+ * :306-314).
+ *
+ * The forward state.  The forward leaves in a caller-owned buffer
+ * (mm1_attn_fwd_state_size bytes) what the backward reads: the fp16 copies
+ * of q, k, v, the residual O - bf16(O) of its fp32 output rounded to bf16
+ * (so the backward's Delta = rowsum(O dO) sees 16 significant bits of O),
+ * and max|V|.  A caller keeps it with (o, lse2) until the backward, as the
+ * reference's FlashAttention.forward saves (q, k, v, out, lse)
+ * (attention_tilelang.py:365).
  *
  * Return value: 0 on success, a negative MM1_E_* code for an argument error,
  * or a positive hipError_t from the launch.  mm1_attn_strerror() names both.
@@ -28,22 +48,22 @@
 extern "C" {
 #endif
 
-#define MM1_ATTN_VERSION 3
+#define MM1_ATTN_VERSION 4
 
 #define MM1_OK 0
 #define MM1_E_NULL (-1)        /* a required pointer is NULL */
 #define MM1_E_SHAPE (-2)       /* B, S, H or Hkv out of range, or H % Hkv != 0 */
 #define MM1_E_HEAD_DIM (-3)    /* head_dim other than 128 */
-#define MM1_E_WORKSPACE (-4)   /* workspace smaller than mm1_attn_bwd_workspace_size() */
+#define MM1_E_WORKSPACE (-4)   /* state or workspace smaller than its *_size() */
 #define MM1_E_SCALE (-5)       /* sm_scale not a positive finite number */
 #define MM1_E_ALIGN (-6)       /* a tensor pointer is not 16-byte aligned */
 #define MM1_E_TILES (-7)       /* tiling index out of range (see mm1_attn_tile_count) */
 #define MM1_E_LAYOUT (-8)      /* the workspace holds no dK/dV partial sums of this shape and
-                                  dK/dV tiling (see mm1_attn_bwd_dkdv_reduce) */
+                                  dK/dV tiling (see mm1_attn_bwd_dkdv_reduce_tiles) */
 #define MM1_E_SCRATCH (-9)     /* shape too large for mm1_attn_bwd_noalloc's static scratch */
 
 /* Bytes of device memory mm1_attn_bwd_noalloc holds per device (see there). */
-#define MM1_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+#define MM1_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
 
 /* Kernel kinds for the tiling queries below. */
 #define MM1_TILES_FWD 0
@@ -53,141 +73,161 @@ extern "C" {
 /* Library version (MM1_ATTN_VERSION of the build). */
 int mm1_attn_version(void);
 
+/* Bytes of the forward state of a shape (0 for a bad shape).  No
+ * counterpart in the reference, whose backward reads the bf16 q, k, v and
+ * out it saved (attention_tilelang.py:365, :370). */
+size_t mm1_attn_fwd_state_size(int B, int S, int H, int Hkv, int D);
+
 /* Forward: o = softmax(q k^T * sm_scale [+ causal mask]) v, per query head h
  * reading KV head h / (H / Hkv); lse2[b,h,i] = log2(e) * logsumexp_j(s_ij).
+ * Also writes the forward state (state_bytes >= mm1_attn_fwd_state_size).
  * Replaces get_kernel("fwd", B, H, S, D, causal, groups)(q, k, v) -> (O, lse),
  * the TileLang kernel flash_fwd (attention_tilelang.py:110-190, called :364). */
 int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
-                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                 void* stream);
+                 void* state, size_t state_bytes,
+                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream);
 
 /* The forward with fp32 o [B, S, H, D]: the values mm1_attn_fwd rounds to
- * bf16 (its 4-wave tiling; lse2 as mm1_attn_fwd).  No counterpart in the
- * reference, whose forward writes bf16 O (attention_tilelang.py:182-185): for
- * callers that check O where one bf16 half-ulp of |O| is already more than
- * their tolerance. */
+ * bf16, from the same kernel of tiling `tiles` (-1 = the default); the
+ * state as mm1_attn_fwd's.  No counterpart in the reference, whose forward
+ * writes bf16 O (attention_tilelang.py:182-185): for callers that check O
+ * where one bf16 half-ulp of |O| is already more than their tolerance. */
 int mm1_attn_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2,
-                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream);
+                     void* state, size_t state_bytes,
+                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, int tiles,
+                     void* stream);
 
-/* Backward preprocess: delta[b,h,i] = sum_d o[b,i,h,d] * dO[b,i,h,d] (fp32).
- * Replaces flash_delta(B, H, S, D)(O, dO) -> Delta
- * (attention_tilelang.py:192-217, called :380). */
+/* A forward state without the forward: the fp16 copies of q, k, v and
+ * max|V| (the O residual is not written; the backward then needs the
+ * caller's delta, mm1_attn_bwd_prep_delta).  For a caller of the reference's
+ * bwd kernel handle, which takes (q, k, v, dO, lse, Delta) directly
+ * (attention_tilelang.py:386-388). */
+int mm1_attn_prep(const void* q, const void* k, const void* v, void* state, size_t state_bytes,
+                  int B, int S, int H, int Hkv, int D, void* stream);
+
+/* Backward preprocess of the reference: delta[b,h,i] = sum_d o[b,i,h,d] *
+ * dO[b,i,h,d] (fp32) from the bf16 o.  Replaces flash_delta(B, H, S, D)(O,
+ * dO) -> Delta (attention_tilelang.py:192-217, called :380).  The backward
+ * below computes its own Delta from the forward state (o plus its residual);
+ * this call is the reference's operator for callers that want it. */
 int mm1_attn_delta(const void* o, const void* dO, float* delta,
                    int B, int S, int H, int D, void* stream);
 
-/* Bytes of fp32 scratch mm1_attn_bwd needs for the dK/dV partial sums
- * (0 when H == Hkv): G = H / Hkv slots of [B, S, Hkv, D] for dK and for dV.  No counterpart in the reference, whose backward takes
- * caller-zeroed fp32 dQ/dK/dV accumulators instead (attention_tilelang.py:381-383). */
+/* Bytes of the backward workspace of a shape (0 for a bad shape): fp16 dO,
+ * the scaled Delta, the dO scale and the dK/dV partial sums (2 * G fp32
+ * slots of [B, S, Hkv, D] when G = H / Hkv > 1).  No counterpart in the
+ * reference, whose backward takes caller-zeroed fp32 dQ/dK/dV accumulators
+ * instead (attention_tilelang.py:381-383). */
 size_t mm1_attn_bwd_workspace_size(int B, int S, int H, int Hkv, int D);
 
-/* Backward: given delta from mm1_attn_delta, writes bf16 dq, dk, dv directly.
- * Replaces get_kernel("bwd", ...)(q, k, v, dO, lse, Delta, dQ, dK, dV) followed
- * by flash_unswizzle and the dk/dv casts (attention_tilelang.py:242-323, :385-389).
- * Deterministic: no atomics; bitwise identical across repeated calls. */
-int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
-                 const float* lse2, const float* delta,
+/* Backward: bf16 dq, dk, dv from (o, dO, lse2) and the forward state:
+ * Delta from o and the state's residual, dO to fp16, dK/dV, then dQ with the
+ * dK/dV group sum in the same launch.  Replaces flash_delta + get_kernel(
+ * "bwd", ...)(q, k, v, dO, lse, Delta, dQ, dK, dV) + flash_unswizzle + the
+ * dk/dv casts (attention_tilelang.py:380-389, :242-323).  Deterministic: no
+ * atomics; bitwise identical across repeated calls. */
+int mm1_attn_bwd(const void* o, const void* dO, const float* lse2,
+                 const void* state, size_t state_bytes,
                  void* dq, void* dk, void* dv,
                  void* workspace, size_t workspace_bytes,
-                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                 void* stream);
+                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream);
 
 /* mm1_attn_bwd without a workspace argument, for callers that cannot
  * allocate device memory around the call: code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc.  No counterpart in the
- * reference.  It calls no allocating routine: the dK/dV partial sums of the
- * default tilings go to a static device array of MM1_NOALLOC_SCRATCH_BYTES
- * (128 MiB) that each device the library runs on holds until the process
- * ends.  mm1_attn_bwd_noalloc_scratch_size() gives the bytes a shape needs
- * (2 * G * B * split_keys * Hkv * D * 4 at most; about 107 MiB at the
- * training shapes of 16,384 tokens); a shape needing more returns
- * MM1_E_SCRATCH.  Every call on one device shares that device's array:
- * calls that overlap on one device (several streams or host threads) race
- * and must be serialised by the caller.  Outputs equal mm1_attn_bwd's
+ * reference.  It calls no allocating routine: the backward workspace of the
+ * default tilings goes to a static device array of
+ * MM1_NOALLOC_SCRATCH_BYTES (256 MiB) that each device the library runs on
+ * holds from the library's load until the process ends (a device-side
+ * static of the code object, not a hipMalloc).
+ * mm1_attn_bwd_noalloc_scratch_size() gives the bytes a shape needs (about
+ * 150 MiB at the training shapes of 16,384 tokens); a shape needing more
+ * returns MM1_E_SCRATCH.  Every call on one device shares that device's
+ * array: calls that overlap on one device (several streams or host threads)
+ * race and must be serialised by the caller.  Outputs equal mm1_attn_bwd's
  * (default tilings) bitwise. */
-int mm1_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* dO,
-                         const float* lse2, const float* delta, void* dq, void* dk, void* dv,
+int mm1_attn_bwd_noalloc(const void* o, const void* dO, const float* lse2,
+                         const void* state, size_t state_bytes, void* dq, void* dk, void* dv,
                          int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream);
 size_t mm1_attn_bwd_noalloc_scratch_size(int B, int S, int H, int Hkv, int D, int causal);
 
 /* The stages of the backward, for callers that schedule or time them
- * separately (same arguments and checks as mm1_attn_bwd).  mm1_attn_bwd runs
- * mm1_attn_bwd_dkdv then mm1_attn_bwd_dq_reduce; mm1_attn_bwd_dkdv_reduce
- * followed by mm1_attn_bwd_dq is the same result in two launches.
- *  - mm1_attn_bwd_dkdv: dK/dV.  With H == Hkv it writes bf16 dk, dv directly.
- *    Otherwise, with the per-head tilings (1, 2, 4) it writes the
- *    per-query-head fp32 partial sums into `workspace`
- *    ([2][G][B][S][Hkv][D], G = H / Hkv) and leaves dk/dv untouched; with the
- *    grouped tilings (0, 3, 5) it writes bf16 dk, dv directly for the key tiles
- *    one workgroup covers and fp32 partials (one slot per chunk, see
- *    mm1_attn_dkdv_plan) for the others.
- *  - mm1_attn_bwd_dkdv_reduce: sums the partials of each KV head and writes
- *    bf16 dk, dv (no-op when H == Hkv).  The layout it reads is the one the
- *    default dK/dV tiling writes; mm1_attn_bwd_dkdv_reduce_tiles names the
- *    tiling.  The partials must come from a mm1_attn_bwd_dkdv* call on the
- *    same workspace with the same shape, `causal` and dK/dV tiling: the
- *    library records, per workspace address, the layout that call wrote, and
- *    the summing calls return MM1_E_LAYOUT (launching nothing) when the
- *    record is missing or differs.  The same holds for
- *    mm1_attn_bwd_dq_reduce*.
- *  - mm1_attn_bwd_dq: bf16 dq.
- *  - mm1_attn_bwd_dq_reduce: bf16 dq, and the group sum of
- *    mm1_attn_bwd_dkdv_reduce done by the tail of the same launch (must run
- *    after mm1_attn_bwd_dkdv on the same stream).
- * Together they replace flash_bwd + flash_unswizzle + casts
- * (attention_tilelang.py:242-323, :385-389); no counterpart as separate calls. */
-int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
-                      const float* lse2, const float* delta, void* dk, void* dv,
+ * separately (same checks as mm1_attn_bwd).  mm1_attn_bwd runs
+ * mm1_attn_bwd_prep, mm1_attn_bwd_dkdv_tiles, mm1_attn_bwd_dq_reduce_tiles;
+ * mm1_attn_bwd_dq_tiles and mm1_attn_bwd_dkdv_reduce_tiles split the last
+ * one into two launches (same results).
+ *  - mm1_attn_bwd_prep: Delta from o and the state, fp16 dO and its scale,
+ *    into `workspace`.  mm1_attn_bwd_prep_delta takes the caller's delta
+ *    instead of o (a state from mm1_attn_prep has no O residual).  The
+ *    calls below read what a prep call wrote into the same workspace; the
+ *    library cannot check that one did.
+ *  - mm1_attn_bwd_dkdv_tiles: dK/dV.  With H == Hkv it writes bf16 dk, dv
+ *    directly.  Otherwise, with the per-head tiling (1) it writes the
+ *    per-query-head fp32 partial sums into `workspace` and leaves dk/dv
+ *    untouched; with the grouped tiling (0) it writes bf16 dk, dv directly
+ *    for the key tiles one workgroup covers and fp32 partials (one slot per
+ *    chunk, see mm1_attn_dkdv_plan) for the others.
+ *  - mm1_attn_bwd_dkdv_reduce_tiles: sums the partials of each KV head and
+ *    writes bf16 dk, dv (no-op when H == Hkv).  It must name the dK/dV
+ *    tiling of the mm1_attn_bwd_dkdv_tiles call that filled the workspace,
+ *    with the same shape and `causal`: the library records, per workspace
+ *    address, the layout that call wrote, and the summing calls return
+ *    MM1_E_LAYOUT (launching nothing) when the record is missing or
+ *    differs.  The record is keyed by address only: a workspace freed and
+ *    reallocated at the same address (as a caching allocator does) with no
+ *    dK/dV call since passes the check, and the sum then reads whatever the
+ *    memory holds.  The same holds for mm1_attn_bwd_dq_reduce_tiles.
+ *  - mm1_attn_bwd_dq_tiles: bf16 dq.
+ *  - mm1_attn_bwd_dq_reduce_tiles: bf16 dq, and the group sum of
+ *    mm1_attn_bwd_dkdv_reduce_tiles done by the tail of the same launch (must
+ *    run after mm1_attn_bwd_dkdv_tiles on the same stream).
+ * Tiling arguments index mm1_attn_tile_desc (-1 = the default).  Together
+ * they replace flash_delta + flash_bwd + flash_unswizzle + casts
+ * (attention_tilelang.py:192-323, :380-389); no counterpart as separate
+ * calls. */
+int mm1_attn_bwd_prep(const void* o, const void* dO, const void* state, size_t state_bytes,
                       void* workspace, size_t workspace_bytes,
-                      int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                      void* stream);
-int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
-                             int B, int S, int H, int Hkv, int D, int causal, void* stream);
-int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
-                    const float* lse2, const float* delta, void* dq,
-                    int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                    void* stream);
-int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const void* dO,
-                           const float* lse2, const float* delta, void* dq, void* dk, void* dv,
-                           const void* workspace, size_t workspace_bytes,
-                           int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                           void* stream);
-
-/* The stages with an explicit tiling (indices of mm1_attn_tile_desc, -1 =
- * the default): what a tuned kernel handle that stages the backward calls.
- * A summing call must name the dK/dV tiling of the mm1_attn_bwd_dkdv_tiles
- * call that filled the workspace (else MM1_E_LAYOUT). */
-int mm1_attn_bwd_dkdv_tiles(const void* q, const void* k, const void* v, const void* dO,
-                            const float* lse2, const float* delta, void* dk, void* dv,
+                      int B, int S, int H, int Hkv, int D, float sm_scale, void* stream);
+int mm1_attn_bwd_prep_delta(const void* dO, const float* delta, const void* state, size_t state_bytes,
+                            void* workspace, size_t workspace_bytes,
+                            int B, int S, int H, int Hkv, int D, float sm_scale, void* stream);
+int mm1_attn_bwd_dkdv_tiles(const float* lse2, const void* state, size_t state_bytes, void* dk, void* dv,
                             void* workspace, size_t workspace_bytes,
                             int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                             int dkdv_tiles, void* stream);
-int mm1_attn_bwd_dkdv_reduce_tiles(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
+int mm1_attn_bwd_dkdv_reduce_tiles(void* workspace, size_t workspace_bytes, void* dk, void* dv,
                                    int B, int S, int H, int Hkv, int D, int causal, int dkdv_tiles,
                                    void* stream);
-int mm1_attn_bwd_dq_tiles(const void* q, const void* k, const void* v, const void* dO,
-                          const float* lse2, const float* delta, void* dq,
+int mm1_attn_bwd_dq_tiles(const float* lse2, const void* state, size_t state_bytes, void* dq,
+                          void* workspace, size_t workspace_bytes,
                           int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                           int dq_tiles, void* stream);
-int mm1_attn_bwd_dq_reduce_tiles(const void* q, const void* k, const void* v, const void* dO,
-                                 const float* lse2, const float* delta, void* dq, void* dk, void* dv,
-                                 const void* workspace, size_t workspace_bytes,
+int mm1_attn_bwd_dq_reduce_tiles(const float* lse2, const void* state, size_t state_bytes,
+                                 void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
                                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                                  int dkdv_tiles, int dq_tiles, void* stream);
 
+/* mm1_attn_bwd with an explicit tiling: what a tuned kernel handle
+ * launches (-1 = the default of mm1_attn_bwd; MM1_E_TILES for an index out
+ * of range). */
+int mm1_attn_bwd_tiles(const void* o, const void* dO, const float* lse2,
+                       const void* state, size_t state_bytes,
+                       void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
+                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                       int dkdv_tiles, int dq_tiles, void* stream);
+
 /* The backward with fp32 gradients: dq, dk, dv as fp32 [B,S,H,D] /
- * [B,S,Hkv,D], the values mm1_attn_bwd rounds to bf16 (up to the fp32
- * summation order of the dK/dV tiling: this call sums per-head fp32 partials
- * in head order).  Needs mm1_attn_bwd_f32_workspace_size() bytes of scratch
- * (2 * G slots of [B,S,Hkv,D] fp32, also for G == 1).  Replaces the fp32
- * dQ / dK / dV buffers that get_kernel("bwd", ...) fills
- * (attention_tilelang.py:258-260, :381-387) before flash_unswizzle and the
- * casts: a caller that wants the unrounded gradients (a parity check, an
- * fp32 master-gradient path) uses it. */
-size_t mm1_attn_bwd_f32_workspace_size(int B, int S, int H, int Hkv, int D);
-int mm1_attn_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
-                     const float* lse2, const float* delta, float* dq, float* dk, float* dv,
-                     void* workspace, size_t workspace_bytes,
-                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream);
+ * [B,S,Hkv,D], the values mm1_attn_bwd_tiles with the same tilings rounds to
+ * bf16 (same kernels, same summation order).  Replaces the fp32 dQ / dK / dV
+ * buffers that get_kernel("bwd", ...) fills (attention_tilelang.py:258-260,
+ * :381-387) before flash_unswizzle and the casts: a caller that wants the
+ * unrounded gradients (a parity check, an fp32 master-gradient path) uses
+ * it. */
+int mm1_attn_bwd_f32_tiles(const void* o, const void* dO, const float* lse2,
+                           const void* state, size_t state_bytes,
+                           float* dq, float* dk, float* dv, void* workspace, size_t workspace_bytes,
+                           int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                           int dkdv_tiles, int dq_tiles, void* stream);
 
 /* Tilings compiled into the library.  The reference autotunes each TileLang
  * kernel over a space of (block_M, block_N, threads, num_stages)
@@ -204,19 +244,12 @@ int mm1_attn_bwd_f32(const void* q, const void* k, const void* v, const void* dO
 int mm1_attn_tile_count(int kind);
 const char* mm1_attn_tile_desc(int kind, int index);
 
-/* mm1_attn_fwd and mm1_attn_bwd with an explicit tiling: `tiles`,
- * `dkdv_tiles`, `dq_tiles` index the tilings above (-1 = the default of the
- * calls without them); MM1_E_TILES for an index out of range.  What a tuned
- * kernel handle (get_kernel with a remembered config) launches. */
+/* mm1_attn_fwd with an explicit tiling (-1 = the default; MM1_E_TILES for an
+ * index out of range): what a tuned kernel handle launches. */
 int mm1_attn_fwd_tiles(const void* q, const void* k, const void* v, void* o, float* lse2,
+                       void* state, size_t state_bytes,
                        int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                        int tiles, void* stream);
-int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* dO,
-                       const float* lse2, const float* delta,
-                       void* dq, void* dk, void* dv,
-                       void* workspace, size_t workspace_bytes,
-                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                       int dkdv_tiles, int dq_tiles, void* stream);
 
 /* Workgroup dispatch order of a causal grid (diagnostic; no counterpart in
  * the reference, whose TileLang grids run in launch order).  The causal
@@ -231,7 +264,7 @@ int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* 
  * `tiles` builds for a device with `cus` compute units: entry b is the work
  * item of launch slot b in the default numbering (0xFFFF for a slot without
  * one).  Writes min(n, cap) entries and returns n, the launch's grid size; 0
- * when the launch uses the default order (the per-head dK/dV tilings,
+ * when the launch uses the default order (the per-head dK/dV tiling,
  * causal == 0 for the forward / dQ, a tiling with two workgroups per CU,
  * more items than the table holds, no modelled gain, or MM1_DISPATCH_ORDER=0
  * in the environment, read per call); a negative MM1_E_* code for bad

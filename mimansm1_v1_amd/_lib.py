@@ -14,50 +14,36 @@ from pathlib import Path
 
 # Every symbol include/mm1_attn.h declares, with its ctypes signature.
 _c_int, _c_float, _c_size, _vp = ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+SHAPE = [_c_int] * 5                       # B, S, H, Hkv, D
+SHAPE_CS = SHAPE + [_c_int, _c_float]       # ..., causal, sm_scale
 SIGNATURES = {
     "mm1_attn_version": (_c_int, []),
-    "mm1_attn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp,
-                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
-    "mm1_attn_fwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
-                                    _c_int, _c_int, _c_float, _c_int, _vp]),
-    "mm1_attn_fwd_f32": (_c_int, [_vp, _vp, _vp, _vp, _vp,
-                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_fwd_state_size": (_c_size, SHAPE),
+    "mm1_attn_fwd": (_c_int, [_vp] * 5 + [_vp, _c_size] + SHAPE_CS + [_vp]),
+    "mm1_attn_fwd_tiles": (_c_int, [_vp] * 5 + [_vp, _c_size] + SHAPE_CS + [_c_int, _vp]),
+    "mm1_attn_fwd_f32": (_c_int, [_vp] * 5 + [_vp, _c_size] + SHAPE_CS + [_c_int, _vp]),
+    "mm1_attn_prep": (_c_int, [_vp] * 3 + [_vp, _c_size] + SHAPE + [_vp]),
     "mm1_attn_tile_count": (_c_int, [_c_int]),
     "mm1_attn_tile_desc": (ctypes.c_char_p, [_c_int, _c_int]),
     "mm1_attn_delta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
-    "mm1_attn_bwd_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
-    "mm1_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
-                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
-    "mm1_attn_bwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
-                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
-                                    _c_int, _c_int, _vp]),
-    "mm1_attn_bwd_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
-    "mm1_attn_bwd_noalloc_scratch_size": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
-    "mm1_attn_bwd_f32_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
-    "mm1_attn_bwd_f32": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
-                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "mm1_attn_bwd_workspace_size": (_c_size, SHAPE),
+    "mm1_attn_bwd_prep": (_c_int, [_vp, _vp, _vp, _c_size, _vp, _c_size] + SHAPE + [_c_float, _vp]),
+    "mm1_attn_bwd_prep_delta": (_c_int, [_vp, _vp, _vp, _c_size, _vp, _c_size] + SHAPE + [_c_float, _vp]),
+    "mm1_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _vp, _vp, _vp, _c_size] + SHAPE_CS + [_vp]),
+    "mm1_attn_bwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _vp, _vp, _vp, _c_size] + SHAPE_CS
+                           + [_c_int, _c_int, _vp]),
+    "mm1_attn_bwd_f32_tiles": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _vp, _vp, _vp, _c_size] + SHAPE_CS
+                               + [_c_int, _c_int, _vp]),
+    "mm1_attn_bwd_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _vp, _vp] + SHAPE_CS + [_vp]),
+    "mm1_attn_bwd_noalloc_scratch_size": (_c_size, SHAPE + [_c_int]),
+    "mm1_attn_bwd_dkdv_tiles": (_c_int, [_vp, _vp, _c_size, _vp, _vp, _vp, _c_size] + SHAPE_CS + [_c_int, _vp]),
+    "mm1_attn_bwd_dkdv_reduce_tiles": (_c_int, [_vp, _c_size, _vp, _vp] + SHAPE + [_c_int, _c_int, _vp]),
+    "mm1_attn_bwd_dq_tiles": (_c_int, [_vp, _vp, _c_size, _vp, _vp, _c_size] + SHAPE_CS + [_c_int, _vp]),
+    "mm1_attn_bwd_dq_reduce_tiles": (_c_int, [_vp, _vp, _c_size, _vp, _vp, _vp, _vp, _c_size] + SHAPE_CS
+                                     + [_c_int, _c_int, _vp]),
     "mm1_attn_dispatch_order": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                          _c_int, _vp, _c_int]),
-    "mm1_attn_bwd_dkdv": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
-                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
-    "mm1_attn_bwd_dkdv_reduce": (_c_int, [_vp, _c_size, _vp, _vp,
-                                          _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "mm1_attn_dkdv_plan": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
-    "mm1_attn_bwd_dq": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                                 _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
-    "mm1_attn_bwd_dq_reduce": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
-                                        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
-    "mm1_attn_bwd_dkdv_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
-                                         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
-                                         _c_int, _vp]),
-    "mm1_attn_bwd_dkdv_reduce_tiles": (_c_int, [_vp, _c_size, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
-                                                _c_int, _c_int, _c_int, _vp]),
-    "mm1_attn_bwd_dq_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                                       _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _vp]),
-    "mm1_attn_bwd_dq_reduce_tiles": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size,
-                                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
-                                              _c_int, _c_int, _vp]),
     "mm1_qknorm_rope_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "mm1_qknorm_rope_bwd_workspace_size": (_c_size, []),

@@ -178,22 +178,34 @@ class _Kernel:
         return f"<{type(self).__name__} shape={self.shape} config={self.config}>"
 
 
+def _state(lib, B, S, H, Hkv, D, device):
+    """A forward state buffer (mm1_attn_fwd_state_size bytes, uint8)."""
+    return torch.empty(lib.mm1_attn_fwd_state_size(B, S, H, Hkv, D), dtype=torch.uint8, device=device)
+
+
 class FwdKernel(_Kernel):
-    """(q, k, v) -> (O, lse2); replaces flash_fwd (AT:110-190)."""
+    """(q, k, v) -> (O, lse2); replaces flash_fwd (AT:110-190).  ``run``
+    also returns the forward state the backward reads (the fp16 operand
+    copies and the O residual, include/mm1_attn.h)."""
     kind = "fwd"
 
-    def __call__(self, q, k, v):
+    def run(self, q, k, v):
         B, H, S, D, Hkv = self.batch, self.heads, self.seq_len, self.dim, self.kv_heads
         _require(q, "q", (B, S, H, D))
         _require(k, "k", (B, S, Hkv, D))
         _require(v, "v", (B, S, Hkv, D))
+        lib = _lib.load()
         out = torch.empty_like(q)
         lse = torch.empty(B, H, S, dtype=torch.float32, device=q.device)
-        rc = _lib.load().mm1_attn_fwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                            out.data_ptr(), lse.data_ptr(), B, S, H, Hkv, D,
-                                            int(self.causal), self.sm_scale, self.tiles,
-                                            _stream(q.device))
+        state = _state(lib, B, S, H, Hkv, D, q.device)
+        rc = lib.mm1_attn_fwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                    state.data_ptr(), state.numel(), B, S, H, Hkv, D, int(self.causal),
+                                    self.sm_scale, self.tiles, _stream(q.device))
         _lib.check(rc, "mm1_attn_fwd_tiles")
+        return out, lse, state
+
+    def __call__(self, q, k, v):
+        out, lse, _ = self.run(q, k, v)
         return out, lse
 
 
@@ -201,8 +213,17 @@ class BwdKernel(_Kernel):
     """(q, k, v, dO, lse, Delta, dQ, dK, dV) -> None, writing bf16 dQ/dK/dV in
     place.  Replaces flash_bwd (AT:242-323) + flash_unswizzle (AT:224-240) +
     the dk/dv casts (AT:389): the reference's buffers are fp32 accumulators,
-    these are the final bf16 gradients."""
+    these are the final bf16 gradients.  Called this way it converts q, k, v
+    itself (mm1_attn_prep) and uses the caller's Delta; ``run_saved`` is the
+    backward of FlashAttention, from the forward's output and state (its
+    Delta comes from 16 significant bits of O)."""
     kind = "bwd"
+
+    def _check_grads(self, dq, dk, dv):
+        B, H, S, D, Hkv = self.batch, self.heads, self.seq_len, self.dim, self.kv_heads
+        _require(dq, "dq", (B, S, H, D))
+        _require(dk, "dk", (B, S, Hkv, D))
+        _require(dv, "dv", (B, S, Hkv, D))
 
     def __call__(self, q, k, v, grad_out, lse, delta, dq, dk, dv):
         B, H, S, D, Hkv = self.batch, self.heads, self.seq_len, self.dim, self.kv_heads
@@ -212,43 +233,72 @@ class BwdKernel(_Kernel):
         _require(grad_out, "grad_out", (B, S, H, D))
         _require(lse, "lse", (B, H, S), torch.float32)
         _require(delta, "delta", (B, H, S), torch.float32)
-        _require(dq, "dq", (B, S, H, D))
-        _require(dk, "dk", (B, S, Hkv, D))
-        _require(dv, "dv", (B, S, Hkv, D))
+        self._check_grads(dq, dk, dv)
         lib = _lib.load()
-        ws_bytes = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, D)
-        ws = (torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device)
-              if ws_bytes else None)
-        ws_ptr = ws.data_ptr() if ws is not None else None
+        state = _state(lib, B, S, H, Hkv, D, q.device)
+        rc = lib.mm1_attn_prep(q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr(), state.numel(),
+                               B, S, H, Hkv, D, _stream(q.device))
+        _lib.check(rc, "mm1_attn_prep")
+        ws = self._workspace(lib, q.device)
+        rc = lib.mm1_attn_bwd_prep_delta(grad_out.data_ptr(), delta.data_ptr(), state.data_ptr(), state.numel(),
+                                         ws.data_ptr(), ws.numel(), B, S, H, Hkv, D, self.sm_scale,
+                                         _stream(q.device))
+        _lib.check(rc, "mm1_attn_bwd_prep_delta")
+        self._stages(lib, lse, state, ws, dq, dk, dv)
+
+    def run_saved(self, out, grad_out, lse, state, dq, dk, dv):
+        """dQ, dK, dV from the forward's (out, lse, state) and dO."""
+        B, H, S, D, Hkv = self.batch, self.heads, self.seq_len, self.dim, self.kv_heads
+        _require(out, "out", (B, S, H, D))
+        _require(grad_out, "grad_out", (B, S, H, D))
+        _require(lse, "lse", (B, H, S), torch.float32)
+        self._check_grads(dq, dk, dv)
+        lib = _lib.load()
+        ws = self._workspace(lib, out.device)
+        rc = lib.mm1_attn_bwd_prep(out.data_ptr(), grad_out.data_ptr(), state.data_ptr(), state.numel(),
+                                   ws.data_ptr(), ws.numel(), B, S, H, Hkv, D, self.sm_scale,
+                                   _stream(out.device))
+        _lib.check(rc, "mm1_attn_bwd_prep")
+        self._stages(lib, lse, state, ws, dq, dk, dv)
+
+    def _workspace(self, lib, device):
+        B, H, S, D, Hkv = self.batch, self.heads, self.seq_len, self.dim, self.kv_heads
+        return torch.empty(lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, D), dtype=torch.uint8, device=device)
+
+    def _stages(self, lib, lse, state, ws, dq, dk, dv):
+        B, H, S, D, Hkv = self.batch, self.heads, self.seq_len, self.dim, self.kv_heads
         shape = (B, S, H, Hkv, D, int(self.causal), self.sm_scale)
         dkdv_tiles, dq_tiles = self.tiles
+        st, wsp = (state.data_ptr(), state.numel()), (ws.data_ptr(), ws.numel())
         if not self.config.get("overlap_dq", OVERLAP_DQ):
-            rc = lib.mm1_attn_bwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                        grad_out.data_ptr(), lse.data_ptr(), delta.data_ptr(),
-                                        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws_ptr, ws_bytes,
-                                        *shape, dkdv_tiles, dq_tiles, _stream(q.device))
-            _lib.check(rc, "mm1_attn_bwd_tiles")
+            rc = lib.mm1_attn_bwd_dkdv_tiles(lse.data_ptr(), *st, dk.data_ptr(), dv.data_ptr(), *wsp, *shape,
+                                             dkdv_tiles, _stream(dq.device))
+            _lib.check(rc, "mm1_attn_bwd_dkdv_tiles")
+            rc = lib.mm1_attn_bwd_dq_reduce_tiles(lse.data_ptr(), *st, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                                  *wsp, *shape, dkdv_tiles, dq_tiles, _stream(dq.device))
+            _lib.check(rc, "mm1_attn_bwd_dq_reduce_tiles")
             return
-        main = torch.cuda.current_stream(q.device)
-        side = _side_stream(q.device)
+        main = torch.cuda.current_stream(dq.device)
+        side = _side_stream(dq.device)
         fork = torch.cuda.Event()
         fork.record(main)
         side.wait_event(fork)
-        rc = lib.mm1_attn_bwd_dq_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
-                                       lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), *shape, dq_tiles,
-                                       side.cuda_stream)
-        _lib.check(rc, "mm1_attn_bwd_dq_tiles")
-        rc = lib.mm1_attn_bwd_dkdv_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
-                                         lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                         ws_ptr, ws_bytes, *shape, dkdv_tiles, main.cuda_stream)
-        _lib.check(rc, "mm1_attn_bwd_dkdv_tiles")
-        rc = lib.mm1_attn_bwd_dkdv_reduce_tiles(ws_ptr, ws_bytes, dk.data_ptr(), dv.data_ptr(),
-                                                B, S, H, Hkv, D, int(self.causal), dkdv_tiles,
-                                                main.cuda_stream)
-        _lib.check(rc, "mm1_attn_bwd_dkdv_reduce_tiles")
-        join = torch.cuda.Event()
-        join.record(side)
-        main.wait_event(join)
+        try:
+            rc = lib.mm1_attn_bwd_dq_tiles(lse.data_ptr(), *st, dq.data_ptr(), *wsp, *shape, dq_tiles,
+                                           side.cuda_stream)
+            _lib.check(rc, "mm1_attn_bwd_dq_tiles")
+            rc = lib.mm1_attn_bwd_dkdv_tiles(lse.data_ptr(), *st, dk.data_ptr(), dv.data_ptr(), *wsp, *shape,
+                                             dkdv_tiles, main.cuda_stream)
+            _lib.check(rc, "mm1_attn_bwd_dkdv_tiles")
+            rc = lib.mm1_attn_bwd_dkdv_reduce_tiles(*wsp, dk.data_ptr(), dv.data_ptr(), B, S, H, Hkv, D,
+                                                    int(self.causal), dkdv_tiles, main.cuda_stream)
+            _lib.check(rc, "mm1_attn_bwd_dkdv_reduce_tiles")
+        finally:
+            # the caller's stream waits for the side stream even when a launch
+            # was refused, so no buffer is reused under a running dQ kernel
+            join = torch.cuda.Event()
+            join.record(side)
+            main.wait_event(join)
 
 
 class DeltaKernel:
@@ -327,13 +377,12 @@ def autotune(kind, shape, device=None, verbose=False):
             handle = FwdKernel(shape, config)
             results.append((_median_ms(lambda: handle(q, k, v), device), config))
     else:
-        out, lse = warm(q, k, v)
+        out, lse, state = warm.run(q, k, v)
         grad_out = rand(batch, seq_len, heads, dim)
-        delta = DeltaKernel(batch, heads, seq_len, dim)(out, grad_out)
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         for config in bwd_configs(dim):
             handle = BwdKernel(shape, config)
-            results.append((_median_ms(lambda: handle(q, k, v, grad_out, lse, delta, dq, dk, dv),
+            results.append((_median_ms(lambda: handle.run_saved(out, grad_out, lse, state, dq, dk, dv),
                                        device), config))
     if verbose:
         for ms, config in results:
@@ -390,26 +439,27 @@ class FlashAttention(torch.autograd.Function):
         if k.shape[-2] * groups != heads:
             raise ValueError(f"groups={groups} does not match heads={heads}, "
                              f"kv_heads={k.shape[-2]}")
-        out, lse = get_kernel("fwd", batch, heads, seq_len, dim, causal, groups)(q, k, v)
-        ctx.save_for_backward(q, k, v, out, lse)
+        out, lse, state = get_kernel("fwd", batch, heads, seq_len, dim, causal, groups).run(q, k, v)
+        # the backward reads the fp16 copies of q, k, v in `state`, not q, k, v
+        ctx.save_for_backward(out, lse, state)
         ctx.causal, ctx.groups = causal, groups
+        ctx.kv_shape, ctx.kv_dtype = k.shape, k.dtype
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        q, k, v, out, lse = ctx.saved_tensors
-        batch, seq_len, heads, dim = q.shape
-        kv_heads = v.shape[-2]
+        out, lse, state = ctx.saved_tensors
+        batch, seq_len, heads, dim = out.shape
+        kv_heads = ctx.kv_shape[-2]
         groups = heads // kv_heads
         grad_out = grad_out if grad_out.is_contiguous() else grad_out.contiguous()
-        if grad_out.dtype != q.dtype:
-            grad_out = grad_out.to(q.dtype)
-        delta = flash_delta(batch, heads, seq_len, dim)(out, grad_out)
-        dq = torch.empty_like(q)
-        dk = torch.empty_like(k)
-        dv = torch.empty_like(v)
-        get_kernel("bwd", batch, heads, seq_len, dim, ctx.causal, groups)(
-            q, k, v, grad_out, lse, delta, dq, dk, dv)
+        if grad_out.dtype != out.dtype:
+            grad_out = grad_out.to(out.dtype)
+        dq = torch.empty_like(out)
+        dk = torch.empty(ctx.kv_shape, dtype=ctx.kv_dtype, device=out.device)
+        dv = torch.empty(ctx.kv_shape, dtype=ctx.kv_dtype, device=out.device)
+        get_kernel("bwd", batch, heads, seq_len, dim, ctx.causal, groups).run_saved(
+            out, grad_out, lse, state, dq, dk, dv)
         return dq, dk, dv, None, None
 
 

@@ -35,13 +35,8 @@ DEVICE_FLAGS = [
 ]
 
 
-# Per-source extra flags.  attn_bwd.hip holds kernels with one wave per SIMD
-# whose long-lived accumulators sit in AGPRs (inline-asm MFMAs); the
-# compiler's own MFMAs there must stay in the VGPR form, where the VALU reads
-# their results without copies.
-EXTRA_FLAGS = {
-    "attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
-}
+# Per-source extra flags (none at present).
+EXTRA_FLAGS: dict = {}
 
 
 def hipcc() -> str:

@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "dispatch_order.h"
+#include "attn_layout.h"
 #include "mm1_common.h"
 
 // k-steps by which the dQ kernel's K / V row reads run ahead of their
@@ -99,20 +100,152 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV: one workgroup per (128-key tile, query head), 8 waves in 4 pairs.
-// Pair i owns keys kt*128 + 32i .. +31 and splits the work by role:
-//   P wave  (wave i):     S = Q K^T, P = exp2(S*scale2 - lse2), dV^T += dO^T P;
-//                         keeps K (B operand) and the dV^T accumulators;
-//   dS wave (wave i + 4): dP = dO V^T, dS = P (dP - Delta), dK^T += Q^T dS;
-//                         keeps V and the dK^T accumulators.
-// P goes from the P wave to the dS wave through a two-slot fp32 LDS mailbox,
-// one barrier per 32-query block.  Both waves of a pair sit on one SIMD, so
-// one wave's softmax VALU work overlaps the other's MFMAs, and each needs
-// about half the registers of a wave doing both (two waves per SIMD fit).
-// Query tiles (Q, dO row-major; lse2, Delta) arrive by LDS DMA in a two-stage
-// ring; the transposed operands of dV^T and dK^T are read with the LDS
-// transpose read.
-// Work item of a dK/dV workgroup: key tile kt = item / (B*H) of query head
+// Backward preprocess of the state-based backward (mm1_attn_bwd_prep).
+//
+// dO is used by the products as do16 = fp16(2^E dO), with E from max|dO| and
+// max|V| (do_scale_exp).  E = 0 whenever that is safe, so the common case
+// converts dO in the same pass that computes Delta and finds max|dO|; a
+// second launch (attn_do16_kernel) reconverts dO with 2^E only when E != 0.
+//
+// attn_delta16_kernel:
+//   Delta_i = sum_d O_id dO_id in fp32, O from the bf16 output and its
+//   residual byte (lo8_decode: 15 significant bits of the forward's fp32 O);
+//   with o == nullptr the caller's Delta is copied (mm1_attn_bwd_prep_delta).
+//   do16 = fp16(dO) (E = 0), and max|dO| of the workgroup's rows in
+//   part_max[blockIdx.x].  16 lanes per (b, s, h) row, grid-stride over pairs
+//   of rows.
+__global__ __launch_bounds__(256) void attn_delta16_kernel(
+    const __bf16* __restrict__ o, const uint8_t* __restrict__ o_lo, const __bf16* __restrict__ dO,
+    const float* __restrict__ delta_in, float* __restrict__ delta, _Float16* __restrict__ do16,
+    float* __restrict__ part_max, int B, int S, int H) {
+  const long nrows = (long)B * S * H;
+  const int c = threadIdx.x & 15;
+  float mx = 0.f;
+  for (long row0 = (((long)blockIdx.x * 256 + threadIdx.x) >> 4) * 2; row0 < nrows;
+       row0 += (long)gridDim.x * 32) {
+    const long row1 = min(row0 + 1, nrows - 1);
+    const bf16x8 d0 = *reinterpret_cast<const bf16x8*>(dO + row0 * HD + 8 * c);
+    const bf16x8 d1 = *reinterpret_cast<const bf16x8*>(dO + row1 * HD + 8 * c);
+    f16x8 h0, h1;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float f0 = (float)d0[t], f1 = (float)d1[t];
+      mx = fmaxf(mx, fmaxf(fabsf(f0), fabsf(f1)));
+      h0[t] = (_Float16)f0;
+      h1[t] = (_Float16)f1;
+    }
+    *reinterpret_cast<f16x8*>(do16 + row0 * HD + 8 * c) = h0;
+    if (row0 + 1 < nrows) *reinterpret_cast<f16x8*>(do16 + row1 * HD + 8 * c) = h1;
+    float acc0 = 0.f, acc1 = 0.f;
+    if (o) {
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(o + row0 * HD + 8 * c);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(o + row1 * HD + 8 * c);
+      const uint2 b0 = *reinterpret_cast<const uint2*>(o_lo + row0 * HD + 8 * c);
+      const uint2 b1 = *reinterpret_cast<const uint2*>(o_lo + row1 * HD + 8 * c);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t ob0 = (a0[t >> 1] >> (16 * (t & 1))) & 0xffffu;
+        const uint32_t ob1 = (a1[t >> 1] >> (16 * (t & 1))) & 0xffffu;
+        const uint32_t q0 = ((t < 4 ? b0.x : b0.y) >> (8 * (t & 3))) & 0xffu;
+        const uint32_t q1 = ((t < 4 ? b1.x : b1.y) >> (8 * (t & 3))) & 0xffu;
+        acc0 = fmaf(lo8_decode(ob0, q0), (float)d0[t], acc0);
+        acc1 = fmaf(lo8_decode(ob1, q1), (float)d1[t], acc1);
+      }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) {
+        acc0 += __shfl_xor(acc0, m);
+        acc1 += __shfl_xor(acc1, m);
+      }
+    }
+    if (c == 0) {
+      auto put = [&](long row, float v) {
+        const int hh = (int)(row % H);
+        const long bs = row / H;
+        const int sp = (int)(bs % S);
+        const int bb = (int)(bs / S);
+        const long i = ((long)bb * H + hh) * S + sp;
+        delta[i] = o ? v : delta_in[i];
+      };
+      put(row0, acc0);
+      if (row0 + 1 < nrows) put(row0 + 1, acc1);
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  __shared__ float wmax[4];
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) part_max[blockIdx.x] = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+}
+
+// The power of two 2^E that dO is scaled by before its fp16 rounding, from
+// mdo = max|dO| and mv = max|V|.  dS = P (dP - Delta) sm_scale, with
+// |dP_ij| <= D mdo mv and |Delta_i| <= max_j |dP_ij|, is bounded by
+// bound = 2 D sm_scale mdo mv; the fp16 values must stay below 2^15.
+//   * E = 0 when 2^-8 <= mdo <= 2^8 and bound < 2^15: dO's largest values
+//     keep 11 significant bits, and values below fp16's normal range (2^-14,
+//     at most 2^-6 of the largest) lose at most 2^-25 absolutely;
+//   * otherwise E = -ilogb(mdo) (2^E mdo in [1, 2)), lowered until 2^E
+//     bound < 2^15.
+// mdo == 0 (or a non-finite maximum, which the results then carry): E = 0.
+__device__ __forceinline__ int do_scale_exp(float mdo, float mv, float sm_scale) {
+  if (!(mdo > 0.f) || !isfinite(mdo) || !isfinite(mv)) return 0;
+  const float bound = 2.f * HD * sm_scale * mdo * mv;
+  const bool bound_ok = !(bound >= 32768.f);
+  if (mdo >= 0x1p-8f && mdo <= 0x1p8f && bound_ok) return 0;
+  int e = -ilogbf(mdo);
+  if (bound > 0.f && isfinite(bound)) e = min(e, 14 - ilogbf(bound));
+  return max(-120, min(120, e));
+}
+
+// E from the partial maxima; scale[0] = 2^-E, scale[1] = 2^E (the kernels
+// that consume the scaled values multiply their dQ / dK / dV by scale[0]:
+// exact, a power of two).  With E != 0 it reconverts dO -> fp16(2^E dO) and
+// scales Delta by 2^E in place; with E == 0 (attn_delta16_kernel's
+// conversion stands) every workgroup leaves after reading the maxima.  Each
+// workgroup reduces the n_dmax + n_vmax partial maxima itself (a few KiB,
+// L2-resident), so no other launch sits between the maxima and the
+// conversion.
+__global__ __launch_bounds__(256) void attn_do16_kernel(
+    const __bf16* __restrict__ dO, _Float16* __restrict__ do16, float* __restrict__ delta,
+    const float* __restrict__ dmax, int n_dmax, const float* __restrict__ vmax, int n_vmax,
+    float* __restrict__ scale, float sm_scale, long n_do, long n_delta) {
+  float md = 0.f, mv = 0.f;
+  for (int i = threadIdx.x; i < n_dmax; i += 256) md = fmaxf(md, dmax[i]);
+  for (int i = threadIdx.x; i < n_vmax; i += 256) mv = fmaxf(mv, vmax[i]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    md = fmaxf(md, __shfl_xor(md, m));
+    mv = fmaxf(mv, __shfl_xor(mv, m));
+  }
+  __shared__ float wm[2][4];
+  if ((threadIdx.x & 63) == 0) {
+    wm[0][threadIdx.x >> 6] = md;
+    wm[1][threadIdx.x >> 6] = mv;
+  }
+  __syncthreads();
+  md = fmaxf(fmaxf(wm[0][0], wm[0][1]), fmaxf(wm[0][2], wm[0][3]));
+  mv = fmaxf(fmaxf(wm[1][0], wm[1][1]), fmaxf(wm[1][2], wm[1][3]));
+  const int e = do_scale_exp(md, mv, sm_scale);
+  const float up = ldexpf(1.f, e);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    scale[0] = ldexpf(1.f, -e);
+    scale[1] = up;
+  }
+  if (e == 0) return;
+  const long stride = (long)gridDim.x * 256;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n_do / 8; i += stride) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(dO + 8 * i);
+    f16x8 r;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r[t] = (_Float16)((float)x[t] * up);
+    *reinterpret_cast<f16x8*>(do16 + 8 * i) = r;
+  }
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n_delta; i += stride) delta[i] *= up;
+}
+
+// ---------------------------------------------------------------------------
+// Work item of a per-head dK/dV workgroup: key tile kt = item / (B*H) of query head
 // bh = item % (B*H), or -1 for a launch slot without one.  Slot b runs on XCD
 // b % 8.  The slots are dealt so that each XCD owns whole query heads, and
 // the workgroups it runs at one time share the Q/dO tiles they stream.  Each
@@ -140,220 +273,6 @@ __device__ __forceinline__ int key_tile_item(int slot, int nbh, int n_kt, KeyTil
   return kt < n_kt ? kt * nbh + part / o.q : -1;
 }
 
-template <bool CAUSAL>
-__global__ __launch_bounds__(512, 1) void attn_dkdv_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
-    float* __restrict__ ws_dk, float* __restrict__ ws_dv,
-    __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order) {
-  constexpr int BQ = TILE_ROWS;                      // query positions per tile
-  constexpr int BUF = 2 * TILE_BYTES + 2 * BQ * 4;   // Q, dO, lse2, delta
-  constexpr int MBOX = 32 * 32 * 4;                  // one 32 x 32 fp32 P block
-  constexpr int NSTAGE = 3;
-  // LDS DMA instructions one wave issues per query tile: two row quads of Q
-  // and two of dO (waves 0 and 1 add one vector copy each and so wait for
-  // one copy more than needed, which is safe).
-  constexpr int kDmaPerTile = 2 * (16 / 8);
-  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + 4 * 2 * MBOX];
-  char* mbox_base = smem + NSTAGE * BUF;
-
-  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
-  const int pair = w & 3;
-  const bool pwave = w < 4;
-  const int nbh = B * H;
-  const int item = key_tile_item(blockIdx.x, nbh, (S + 127) / 128, order);
-  if (item < 0) return;
-  const int kt = item / nbh;              // heaviest key tiles first
-  const int bh = item % nbh;
-  const int b = bh / H, hq = bh % H;
-  const int g = hq / G, hh = hq % G;
-  const int kw0 = kt * 128 + 32 * pair;   // this pair's first key
-  const int key = kw0 + l32;
-
-  const int q_begin = CAUSAL ? kt * 128 : 0;
-  const int n_qt = (S - q_begin + BQ - 1) / BQ;
-  const long qstride = (long)H * HD;
-  const __bf16* qbase = q + ((long)b * S * H + hq) * HD;
-  const __bf16* dobase = dO + ((long)b * S * H + hq) * HD;
-  const float* lse_row = lse2 + ((long)b * H + hq) * S;
-  const float* dl_row = delta + ((long)b * H + hq) * S;
-
-  // Query tiles are walked from the sequence end down to q_begin, so the
-  // workgroups of one head that start together read the same tiles together.
-  auto tile_p0 = [&](int it) { return q_begin + (n_qt - 1 - it) * BQ; };
-  const uint32_t dma_off = tile_lane_off(qstride, tid);
-  auto issue_tile = [&](char* buf, int p0) {
-    tile_dma<8>(buf, qbase + (long)p0 * qstride, qstride, S - p0, dma_off, tid);
-    tile_dma<8>(buf + TILE_BYTES, dobase + (long)p0 * qstride, qstride, S - p0, dma_off, tid);
-    if (w == 0) vec64_dma(buf + 2 * TILE_BYTES, lse_row + p0, S - p0, lane);
-    if (w == 1) vec64_dma(buf + 2 * TILE_BYTES + BQ * 4, dl_row + p0, S - p0, lane);
-  };
-  issue_tile(smem, tile_p0(0));
-  if (n_qt > 1) issue_tile(smem + BUF, tile_p0(1));
-
-  // This lane's key row of K (P wave) or V (dS wave) as the B operand.
-  bf16x8 breg[8];
-  {
-    const int kk = min(key, S - 1);
-    const __bf16* src = (pwave ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) breg[ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) pin(breg[ks]);
-  }
-
-  f32x16 acc[4];   // dV^T (P wave) or dK^T (dS wave)
-#pragma unroll
-  for (int db = 0; db < 4; ++db) acc[db] = zero16();
-  const LdsBases lb = make_lds_bases(lane);
-  wait_dma();
-  __syncthreads();
-
-  // One query tile; the loop below runs it NSTAGE times per trip so the ring
-  // slot (and every LDS offset) is a compile-time constant.
-  auto step = [&](auto slot, int it, auto role) {
-    constexpr int P = decltype(slot)::value;
-    constexpr bool PW = decltype(role)::value;   // P wave (else dS wave)
-    const char* ql = smem + P * BUF;
-    const char* dol = ql + TILE_BYTES;
-    const float* lsel = reinterpret_cast<const float*>(ql + 2 * TILE_BYTES);
-    const float* dll = lsel + BQ;
-    const int p0 = tile_p0(it);
-    if (it + 2 < n_qt) issue_tile(smem + ((P + 2) % NSTAGE) * BUF, tile_p0(it + 2));
-    // pairs whose keys all lie after this tile skip it (causal); the
-    // barriers are still taken by every wave
-    const bool active = !CAUSAL || p0 + BQ - 1 >= kw0;
-    const bool need_mask = (CAUSAL && p0 < kw0 + 31) || (p0 + BQ > S);
-
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      // D layout: register r holds query 32*qb + 8*(r/4) + 4*h + (r%4) of the tile.
-      // mailbox layout [register group a4][lane] x 4 floats: each 16-byte access
-      // of a wave is one contiguous 1 KiB row (no bank conflicts)
-      float* mbox = reinterpret_cast<float*>(mbox_base + (pair * 2 + qb) * MBOX) + lane * 4;
-      f32x16 sv;
-      if (active) {
-        const char* arows = PW ? ql : dol;
-        // lse2 (P wave) rows of this block, read ahead of the products
-        f32x4 lse4[4];
-        if constexpr (PW) {
-#pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4)
-            lse4[a4] = *reinterpret_cast<const f32x4*>(lsel + 32 * qb + 8 * a4 + 4 * h);
-        }
-        sv = zero16();
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) sv = mfma32(rows_a(arows, lb, qb, ks), breg[ks], sv);
-        if constexpr (PW) {
-          // P = exp2(S*scale2 - lse2); masked (causal or past the end) only in
-          // the tiles that need it, as separate straight-line code
-          auto softmax = [&](auto masked) {
-#pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-              const int i0 = 32 * qb + 8 * a4 + 4 * h;
-#pragma unroll
-              for (int c = 0; c < 4; ++c) {
-                const int r = 4 * a4 + c;
-                float pr = exp2_fast(fmaf(sv[r], scale2, -lse4[a4][c]));
-                if constexpr (decltype(masked)::value) {
-                  const int qpos = p0 + i0 + c;
-                  pr = ((CAUSAL && key > qpos) || qpos >= S) ? 0.f : pr;
-                }
-                sv[r] = pr;
-              }
-            }
-          };
-          if (need_mask) softmax(std::true_type{});
-          else softmax(std::false_type{});
-#pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-            f32x4 v4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) v4[c] = sv[4 * a4 + c];
-            *reinterpret_cast<f32x4*>(mbox + 256 * a4) = v4;
-          }
-        }
-      }
-      lds_barrier();   // P of this block is in the mailbox
-      if (active) {
-        if constexpr (PW) {
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh) {
-            const bf16x8 pb = pack8(sv, 8 * kh);
-#pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db] = mfma32(tr_a(dol, lb, db, 2 * qb + kh), pb, acc[db]);
-          }
-        } else {
-          f32x16 dsv;
-#pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-            const int i0 = 32 * qb + 8 * a4 + 4 * h;
-            const f32x4 dl4 = *reinterpret_cast<const f32x4*>(dll + i0);
-            const f32x4 p4 = *reinterpret_cast<const f32x4*>(mbox + 256 * a4);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) dsv[4 * a4 + c] = p4[c] * (sv[4 * a4 + c] - dl4[c]) * sm_scale;
-          }
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh) {
-            const bf16x8 sb = pack8(dsv, 8 * kh);
-#pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db] = mfma32(tr_a(ql, lb, db, 2 * qb + kh), sb, acc[db]);
-          }
-        }
-      }
-    }
-    // the next tile must have landed; the one after it stays in flight
-    if (it + 2 < n_qt) {
-      __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");
-    } else {
-      wait_dma();
-    }
-    lds_barrier();
-  };
-  // each role runs its own specialised copy of the loop (same barriers)
-  auto run = [&](auto role) {
-    for (int it = 0; it < n_qt; it += NSTAGE) {
-      step(std::integral_constant<int, 0>{}, it, role);
-      if (it + 1 < n_qt) step(std::integral_constant<int, 1>{}, it + 1, role);
-      if (it + 2 < n_qt) step(std::integral_constant<int, 2>{}, it + 2, role);
-    }
-  };
-  if (pwave) run(std::true_type{});
-  else run(std::false_type{});
-
-  if (key >= S) return;
-  // D layout of dK^T / dV^T: register r of block db holds column
-  // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
-  if (G == 1) {
-    __bf16* row = (pwave ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        bf16x4 o4;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o4[c] = (__bf16)acc[db][4 * a4 + c];
-        *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
-      }
-    }
-  } else {
-    const long slot = (long)hh * B * S * Hkv * HD;
-    float* row = (pwave ? ws_dv : ws_dk) + slot + ((long)(b * S + key) * Hkv + g) * HD;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        f32x4 o4;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o4[c] = acc[db][4 * a4 + c];
-        *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
-      }
-    }
-  }
-}
-
 // Calls f(integral_constant<J>) for J = 0 .. N-1 while it returns true.
 template <int J, int N, class F>
 __device__ __forceinline__ void unroll_while(F&& f) {
@@ -365,34 +284,31 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // ---------------------------------------------------------------------------
 // dK, dV, software-pipelined across the two roles of a pair.
 //
-// Same decomposition and roles as attn_dkdv_kernel (one workgroup per
-// 128-key tile; a pair of waves owns 32 * KB keys of it, the P wave keeping K
-// and dV^T, the dS wave V and dK^T), but the query tiles are 32 rows and the
-// work on a tile is spread over four segments:
+// One workgroup per 128-key tile, 8 waves in 4 pairs, one pair per SIMD; a
+// pair owns 32 keys of the tile and splits the work by role: the P wave
+// keeps K (B operand) and the dV^T accumulators, the dS wave V and dK^T.  P
+// goes from the P wave to the dS wave through a two-slot fp32 LDS mailbox.
+// The query tiles are 32 rows (Q, dO row-major; the transposed operands of
+// dV^T and dK^T come from the LDS transpose read), and the work on a tile is
+// spread over four segments:
 //   segment s, P wave : S(s+1) = Q(s+1) K^T                | P(s) = exp2(S(s) scale2 - lse2), -P(s) sm_scale -> mailbox | dV^T += dO(s-1)^T P(s-1)
 //   segment s, dS wave: Delta - dP(s) = Delta + dO(s) (-V)^T | dS(s-1) = (-P(s-1) sm_scale) (Delta - dP(s-1))          | dK^T += Q(s-2)^T dS(s-2)
 // Within a segment each wave's VALU work (middle column) depends on no
 // product of the same segment, so it runs under the wave's own products
 // (and, with two waves per SIMD, the other wave's), and the pair meets at one
 // barrier per segment, which also publishes the DMA ring.  S(s+1), P(s-1)
-// (bf16) stay in the P wave's registers, dP(s-1) and dS(s-2) (bf16) in the
+// (fp16) stay in the P wave's registers, dP(s-1) and dS(s-2) (fp16) in the
 // dS wave's.  Each wave starts its segment with the accumulation product
-// (KB = 1: the P wave runs dV^T before S(s+1)), whose tile was published
-// segments earlier: its first operand fragments and the wave's lse2 / Delta
-// vector are read before the previous barrier, so right after a barrier the
-// waves issue products instead of all waiting on the LDS together.
+// (the P wave runs dV^T before S(s+1)), whose tile was published segments
+// earlier: its first operand fragments and the wave's lse2 / Delta vector
+// are read before the previous barrier, so right after a barrier the waves
+// issue products instead of all waiting on the LDS together.
 //
-// KB = 32-key blocks per wave:
-//   KB = 1: 8 waves (4 pairs x 32 keys), two waves per SIMD (a pair shares
-//           one SIMD), 256 registers per wave;
-//   KB = 2: 4 waves (2 pairs x 64 keys), one wave per SIMD, 512 registers
-//           per wave.  Every LDS operand fragment (a Q / dO row fragment of S
-//           and dP, a transposed dO / Q fragment of dV^T and dK^T) feeds two
-//           products instead of one, which halves the LDS instructions per
-//           product (KB = 1 issues 2 per product, near the LDS pipe's rate
-//           of about one instruction per 4 cycles per CU); alone on its
-//           SIMD, a wave has no partner to run its VALU work under, and KB =
-//           2 measures slower.
+// Operands: the fp16 copies q16, k16, v16 of the forward state and do16 =
+// fp16(2^E dO) with Delta scaled alike (attn_do16_kernel), so dP, dS and
+// the accumulators carry the factor 2^E; the epilogue multiplies dK and dV
+// by scale[0] = 2^-E.  F32OUT: dk / dv (and the partials) are fp32, the
+// values the bf16 path rounds.
 //
 // Tile x of the ring lives in slot x % NSTAGE; it is first read in segment
 // x-1 and last in segment x+2, so segment s refills slot (s-3) % NSTAGE with
@@ -400,25 +316,24 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // segments of lead).  Tiles whose queries all precede a pair's keys (causal)
 // are computed with the mask (P = 0): the pair would otherwise only wait at
 // the barrier.
-template <int NSTAGE, bool CAUSAL, bool GROUP, bool RAGGED, int KB>
-__global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
-    float* __restrict__ ws_dk, float* __restrict__ ws_dv,
-    __bf16* __restrict__ dk, __bf16* __restrict__ dv,
+template <int NSTAGE, bool CAUSAL, bool GROUP, bool RAGGED, bool F32OUT>
+__global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
+    const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
+    const _Float16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
+    const float* __restrict__ scale, float* __restrict__ ws_dk, float* __restrict__ ws_dv,
+    void* __restrict__ dk, void* __restrict__ dv,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order,
-    int chunk_tiles, int max_chunks, const DispatchOrder ord, int force_partials, int ws_rows) {
+    int chunk_tiles, int max_chunks, const DispatchOrder ord, int ws_rows) {
   static_assert(NSTAGE >= 6, "ring depth: at least 6");
-  static_assert(KB == 1 || KB == 2, "32 or 64 keys per wave");
-  constexpr int NW = 8 / KB;              // waves per workgroup
+  constexpr int KB = 1;                   // 32-key blocks per wave
+  constexpr int NW = 8;                   // waves per workgroup
   constexpr int NP = NW / 2;              // pairs
-  // Waves that copy the ring's tiles: the P waves when each has a pair
-  // partner (KB = 1: the dS waves, which carry the longer chain of the
-  // segment, issue no copies and wait for none), else all waves.
-  constexpr int DW = KB == 1 ? NP : NW;
+  // Waves that copy the ring's tiles: the P waves (the dS waves, which carry
+  // the longer chain of the segment, issue no copies and wait for none).
+  constexpr int DW = NP;
   constexpr int QPW = 8 / DW;             // row quads of a 32-row tile each copying wave copies
   constexpr int BQ = 32;                  // query positions per tile
-  constexpr int QT = BQ * HD * 2;         // one 32 x 128 bf16 operand tile
+  constexpr int QT = BQ * HD * 2;         // one 32 x 128 fp16 operand tile
   constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse2 x 32 | Delta x 32], 1 KiB aligned
   constexpr int MBOX = 32 * 32 * 4;       // one 32 x 32 fp32 P block
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + NP * 2 * KB * MBOX];
@@ -434,11 +349,10 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // head hbase + u % HW of the group).  The chunks of a split key tile
   // interleave, so every workgroup starts at the sequence end and those that
   // run together stream the same rows.  The sums go to partial slot `part`
-  // of `nparts`, or straight to dk/dv when nparts == 1 (unless
-  // force_partials: fp32 partials in every case, for the fp32 backward).  A
-  // workspace slot holds ws_rows key rows per batch element: S for the
-  // per-head tilings, split_keys (the keys of split key tiles, the only ones
-  // with partials) for the grouped ones.
+  // of `nparts`, or straight to dk/dv when nparts == 1.  A workspace slot
+  // holds ws_rows key rows per batch element: S for the per-head tilings,
+  // split_keys (the keys of split key tiles, the only ones with partials)
+  // for the grouped ones.
   int b, g, kt, n_qt, u0, n_u, ustep, part, nparts, hbase, HW;
   if constexpr (GROUP) {
     const int j = dispatch_item(ord);
@@ -549,15 +463,15 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // This lane's key rows of K (P wave) or -V (dS wave) as the B operands,
   // one per key block.  With -V the dP product accumulates onto Delta and
   // gives Delta - dP, and the mailbox carries -P sm_scale, so dS = P (dP -
-  // Delta) sm_scale is one multiply; negating a bf16 is exact, so every
+  // Delta) sm_scale is one multiply; negating an fp16 is exact, so every
   // value is the one of the unnegated arithmetic up to its sign.
-  bf16x8 breg[KB][8];
+  f16x8 breg[KB][8];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int kk = min(kw0 + 32 * kb + l32, S - 1);
-    const __bf16* src = (pwave ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
+    const _Float16* src = (pwave ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = *reinterpret_cast<const f16x8*>(src + 16 * ks);
     if (!pwave) {
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = neg8(breg[kb][ks]);
@@ -572,22 +486,15 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
 #pragma unroll
     for (int db = 0; db < 4; ++db) acc[kb][db] = zero16();
   }
-  // KB = 2: the 128 accumulator registers live in AGPRs (mfma32_acc), the
-  // rest of the wave's state in the 256 VGPRs
-  auto accumulate = [&](f32x16& c, const bf16x8& a, const bf16x8& bb) MM1_INLINE {
-    if constexpr (KB == 2) mfma32_acc(a, bb, c);
-    else c = mfma32(a, bb, c);
-  };
-  // KB = 1 computes S one segment ahead (snext), so that the P wave's
-  // exponentials run between the products of the next S; KB = 2 has no
-  // registers for that and computes S and its exponentials in turn.  The dS
-  // wave computes dS(s-1) between the products of dK^T += Q^T dS(s-2) and
-  // dP(s) last, for the next segment.
-  constexpr bool AHEAD = KB == 1;
-  bf16x8 pb[KB][2];    // P wave: P(s-1) as the B operand of dV^T
-  f32x16 snext[KB];    // P wave: S(s), computed one segment ahead (AHEAD)
+  auto accumulate = [&](f32x16& c, const f16x8& a, const f16x8& bb) MM1_INLINE { c = mfma32h(a, bb, c); };
+  // The P wave computes S one segment ahead (snext), so that its
+  // exponentials run between the products of the next S.  The dS wave
+  // computes dS(s-1) between the products of dK^T += Q^T dS(s-2) and dP(s)
+  // last, for the next segment.
+  f16x8 pb[KB][2];     // P wave: P(s-1) as the B operand of dV^T
+  f32x16 snext[KB];    // P wave: S(s), computed one segment ahead
   f32x16 dpp[KB];      // dS wave: dP(s-1)
-  bf16x8 sbp[KB][2];   // dS wave: dS(s-2) as the B operand of dK^T
+  f16x8 sbp[KB][2];    // dS wave: dS(s-2) as the B operand of dK^T
   const LdsBases lb = make_lds_bases(lane);
   wait_dma();
   __syncthreads();
@@ -601,9 +508,9 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
     for (int kb = 0; kb < KB; ++kb) sacc[kb] = c0;
     mfma_chain<8, MM1_DKDV_PF_ROWS>(
         [&](int ks) MM1_INLINE { return rows_a(t, lb, 0, ks); },
-        [&](int ks, const bf16x8& fa) MM1_INLINE {
+        [&](int ks, const f16x8& fa) MM1_INLINE {
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32(fa, breg[kb][ks], sacc[kb]);
+          for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32h(fa, breg[kb][ks], sacc[kb]);
         },
         between);
   };
@@ -616,11 +523,11 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // segment's barrier (first)
   constexpr int PFT = MM1_DKDV_PF_TR;
   auto tr_frag = [&](const char* t, int i) MM1_INLINE { return tr_a(t, lb, i & 3, i >> 2); };
-  auto accumulate_tile = [&](const bf16x8 (&first)[PFT], const char* t, const bf16x8 (&bop)[KB][2],
+  auto accumulate_tile = [&](const f16x8 (&first)[PFT], const char* t, const f16x8 (&bop)[KB][2],
                              auto&& between) MM1_INLINE {
     mfma_chain_from<8, PFT>(
         first, [&](int i) MM1_INLINE { return tr_frag(t, i); },
-        [&](int i, const bf16x8& a) MM1_INLINE {
+        [&](int i, const f16x8& a) MM1_INLINE {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) accumulate(acc[kb][i & 3], a, bop[kb][i >> 2]);
         },
@@ -634,7 +541,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   // exponentials).  The dS wave reads Delta of tile s just before its dP
   // product, which starts from it (holding it across the barrier cost more
   // registers than the read).
-  bf16x8 nfa[PFT];
+  f16x8 nfa[PFT];
   f32x4 nvec[4];
   auto read_first = [&](const char* t) MM1_INLINE {
 #pragma unroll
@@ -646,7 +553,7 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   };
   auto nothing = [](int) MM1_INLINE {};
   if (pwave) {
-    if constexpr (AHEAD) product(smem, snext, nothing);
+    product(smem, snext, nothing);
     read_vec(reinterpret_cast<const float*>(smem + 2 * QT));        // lse2 of tile 0
   }
   const float neg_sm_scale = -sm_scale;
@@ -698,57 +605,39 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           }
         }
       };
-      // bf16 P(s), the B operand of the next segment's dV^T product: registers
+      // fp16 P(s), the B operand of the next segment's dV^T product: registers
       // 2j, 2j+1 of each key block
-      bf16x8 pbn[KB][2];
+      f16x8 pbn[KB][2];
       auto pack_at = [&](int j) MM1_INLINE {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-          for (int e = 0; e < 2; ++e) pbn[kb][j >> 2][2 * (j & 3) + e] = (__bf16)sv[kb][2 * j + e];
+          for (int e = 0; e < 2; ++e) pbn[kb][j >> 2][2 * (j & 3) + e] = (_Float16)sv[kb][2 * j + e];
           if ((j & 3) == 3) pin(pbn[kb][j >> 2]);
         }
       };
-      if constexpr (AHEAD) {
-        // dV^T += dO(s-1)^T P(s-1) first (its operands were read before the
-        // barrier), with the exponentials of S(s) between its products; then
-        // S(s+1) from the tile the barrier published, with the bf16 pack of
-        // P(s) between its products
-        if constexpr (CUR) {
+      // dV^T += dO(s-1)^T P(s-1) first (its operands were read before the
+      // barrier), with the exponentials of S(s) between its products; then
+      // S(s+1) from the tile the barrier published, with the fp16 pack of
+      // P(s) between its products
+      if constexpr (CUR) {
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) sv[kb] = snext[kb];
-        }
-        if constexpr (PREV) {
-          accumulate_tile(nfa, tp + QT, pb, [&](int i) MM1_INLINE {
-            if constexpr (CUR) {
-              exp_at(2 * i);
-              exp_at(2 * i + 1);
-            }
-          });
-        } else if constexpr (CUR) {
+        for (int kb = 0; kb < KB; ++kb) sv[kb] = snext[kb];
+      }
+      if constexpr (PREV) {
+        accumulate_tile(nfa, tp + QT, pb, [&](int i) MM1_INLINE {
+          if constexpr (CUR) {
+            exp_at(2 * i);
+            exp_at(2 * i + 1);
+          }
+        });
+      } else if constexpr (CUR) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) exp_at(r);
-        }
-        if constexpr (CUR) {
-          mask();
-          product(tn, snext, [&](int ks) MM1_INLINE { pack_at(ks); });
-        }
-      } else {
-        if constexpr (CUR) {
-          product(tc, sv, nothing);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) exp_at(r);
-          mask();
-        }
-        if constexpr (PREV) {
-          // dV^T += dO(s-1)^T P(s-1), packing P(s) between its products
-          accumulate_tile(nfa, tp + QT, pb, [&](int i) MM1_INLINE {
-            if constexpr (CUR) pack_at(i);
-          });
-        } else if constexpr (CUR) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) pack_at(j);
-        }
+        for (int r = 0; r < 16; ++r) exp_at(r);
+      }
+      if constexpr (CUR) {
+        mask();
+        product(tn, snext, [&](int ks) MM1_INLINE { pack_at(ks); });
       }
       if constexpr (CUR) {
         float* mb = mbox + (s & 1) * (KB * MBOX / 4);
@@ -793,12 +682,12 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           dsv[kb][r] = x;
         }
       };
-      bf16x8 sbn[KB][2];
+      f16x8 sbn[KB][2];
       auto dspack_at = [&](int j) MM1_INLINE {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-          for (int e = 0; e < 2; ++e) sbn[kb][j >> 2][2 * (j & 3) + e] = (__bf16)dsv[kb][2 * j + e];
+          for (int e = 0; e < 2; ++e) sbn[kb][j >> 2][2 * (j & 3) + e] = (_Float16)dsv[kb][2 * j + e];
           if ((j & 3) == 3) pin(sbn[kb][j >> 2]);
         }
       };
@@ -890,27 +779,34 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
   };
   if (pwave) run(std::true_type{});
   else run(std::false_type{});
-  if constexpr (KB == 2) {
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) agpr_fence(acc[kb]);
-  }
 
   // D layout of dK^T / dV^T: register r of block db holds column
-  // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
+  // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.  The sums
+  // carry the factor 2^E of do16; times 2^-E (exact) they are dK, dV.
+  const float unscale = scale[0];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int key = kw0 + 32 * kb + l32;
     if (key >= S) continue;
-    if (nparts == 1 && !force_partials) {
-      __bf16* row = (pwave ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[kb][db] *= unscale;
+    if (nparts == 1) {
+      const long row = ((long)(b * S + key) * Hkv + g) * HD;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) {
-          bf16x4 o4;
+          if constexpr (F32OUT) {
+            f32x4 o4;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) o4[c] = (__bf16)acc[kb][db][4 * a4 + c];
-          *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
+            for (int c = 0; c < 4; ++c) o4[c] = acc[kb][db][4 * a4 + c];
+            *reinterpret_cast<f32x4*>(static_cast<float*>(pwave ? dv : dk) + row + 32 * db + 8 * a4 + 4 * h) = o4;
+          } else {
+            bf16x4 o4;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o4[c] = (__bf16)acc[kb][db][4 * a4 + c];
+            *reinterpret_cast<bf16x4*>(static_cast<__bf16*>(pwave ? dv : dk) + row + 32 * db + 8 * a4 + 4 * h) = o4;
+          }
         }
       }
     } else {
@@ -923,470 +819,6 @@ __global__ __launch_bounds__(512 / KB, 1) void attn_dkdv_pipe_kernel(
           f32x4 o4;
 #pragma unroll
           for (int c = 0; c < 4; ++c) o4[c] = acc[kb][db][4 * a4 + c];
-          *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
-        }
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// dK, dV in quads of single-product waves (the grouped walk of the pipelined
-// kernel: one workgroup per 128-key tile of (b, g), a chunk of the position-
-// major walk over the G heads of the group, 32-query tiles).
-//
-// The 8 waves form two quads of 64 keys.  Each wave of a quad computes one
-// product for both of the quad's 32-key blocks, so every LDS operand fragment
-// of the dK^T / dV^T products feeds two products and every row fragment of S
-// / dP two as well:
-//   S wave : S(s) = Q(s) K^T, P(s) = exp2(S scale2 - lse2), masked -> fp32 mailbox
-//   dP wave: Delta(s) - dP(s) = Delta + dO(s) (-V)^T; between its products
-//            dS(s-1) = (P(s-1) (-sm_scale)) (Delta - dP(s-1)) -> bf16 mailbox
-//   dV wave: dV^T += dO(s-2)^T bf16(P(s-2))
-//   dK wave: dK^T += Q(s-2)^T dS(s-2)
-// A quad issues 88 LDS instructions per 64 products (8 + 16 row reads, 32
-// transposed reads, 16 + 16 fp32 mailbox accesses, 8 bf16 mailbox accesses,
-// 8 vector reads) against 128 for two pairs of the pipelined kernel.  The
-// arithmetic is the pipelined kernel's, operation for operation, so the
-// results are bitwise the same.
-//
-// Waves w and w + 4 share SIMD w % 4: w = 0, 2 are the S waves of quads 0, 1
-// and w = 4, 6 their dV waves (the exponentials run under the dV products);
-// w = 1, 3 the dP waves and w = 5, 7 their dK waves (the dS arithmetic runs
-// under the dK products).  The dV and dK waves copy the ring's tiles.
-//
-// One barrier per segment.  The dV wave reads P(s-1) from the mailbox and
-// the first fragments of its next product (tile s-1) at the end of segment s,
-// before the barrier, and the dK wave the first fragments of its next
-// product: after a barrier only the S and dP waves (the new tile) and the dK
-// wave (the 4 dS reads) wait on the LDS.  Tile x is read in segments x (S,
-// dP, lse2, Delta), x+1 (the dV / dK waves' first fragments) and x+2; segment
-// s refills slot (s+3) % 6, tile s-3's, with tile s+3 and waits for tile s+1
-// before its barrier.
-template <bool CAUSAL, bool RAGGED>
-__global__ __launch_bounds__(512, 1) void attn_dkdv_quad_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
-    float* __restrict__ ws_dk, float* __restrict__ ws_dv,
-    __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    int B, int S, int H, int Hkv, int G, float scale2, float sm_scale,
-    int chunk_tiles, int max_chunks, const DispatchOrder ord, int force_partials, int ws_rows) {
-  constexpr int NSTAGE = 6;
-  constexpr int BQ = 32;                  // query positions per tile
-  constexpr int QT = BQ * HD * 2;         // one 32 x 128 bf16 operand tile
-  constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse2 x 32 | Delta x 32], 1 KiB aligned
-  constexpr int PBOX = 2 * 2 * 4096;      // P mailbox of a quad: 2 slots x 2 key blocks x 32 x 32 fp32
-  constexpr int DBOX = 2 * 4096;          // dS mailbox of a quad: 2 slots x 2 key blocks x 32 x 32 bf16
-  constexpr int QPW = 2;                  // row quads of a tile each copying wave copies
-  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + 2 * (PBOX + DBOX)];
-
-  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
-  const int quad = (w >> 1) & 1;
-  const int role = (w & 1) | ((w >> 1) & 2);   // 0 S, 1 dP, 2 dV, 3 dK
-  const int cw = w - 4;                        // copying wave index (dV, dK waves)
-  const int n_kt = (S + 127) / 128;
-  // the work of this workgroup, as in the grouped pipelined kernel
-  const int j = dispatch_item(ord);
-  if (j < 0) return;
-  const int nbg = B * Hkv;
-  const int bg = j % nbg, rr = j / nbg;
-  const int kt = rr / max_chunks;              // heaviest key tiles first
-  const int c = rr - kt * max_chunks;
-  if (kt >= n_kt) return;
-  const int b = bg / Hkv, g = bg - (bg / Hkv) * Hkv;
-  const int n_qt = dkdv_n_qt(S, kt, CAUSAL);
-  const int len = G * n_qt;
-  const int nparts = dkdv_chunks(len, chunk_tiles, max_chunks);
-  if (c >= nparts) return;                     // an empty item of the default numbering
-  const int ustep = nparts;
-  const int n_u = (len - c + nparts - 1) / nparts;
-  const int part = c;
-  const int kw0 = kt * 128 + 64 * quad;        // this quad's first key
-
-  const int q_begin = CAUSAL ? kt * 128 : 0;
-  const long qstride = (long)H * HD;
-  const long grp_rows = ((long)b * S * H + g * G) * HD;
-  const float* vec_src = (h ? delta : lse2) + ((long)b * H + g * G) * S + l32;
-  auto tile_p0 = [&](int t) MM1_INLINE { return q_begin + (n_qt - 1 - t) * BQ; };
-  auto advance = [&](int& hh, int& t) MM1_INLINE {
-    hh += ustep;
-    if (hh >= G) {
-      hh -= G;
-      ++t;
-    }
-  };
-  const uint32_t dma_off = tile_lane_off(qstride, tid);
-  const uint32_t lds_smem = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-  // LDS DMA by the copying waves: row quads cw, cw + 4 of Q and of dO; wave
-  // cw == 0 adds the lse2 | Delta vector.
-  auto issue = [&](int slot, int hh, int t) MM1_INLINE {
-    if (w < 4) return;
-    const int p0 = tile_p0(t);
-    const long rows = grp_rows + (long)hh * HD + (long)p0 * qstride;
-    const float* vs = vec_src + (long)hh * S;
-    const uint32_t l = lds_smem + slot * BUF;
-    if (!RAGGED || p0 + BQ <= S) {
-#pragma unroll
-      for (int i = 0; i < QPW; ++i) {
-        const int rq = cw + 4 * i;
-        dma16_sbase(dma_off, q + rows + (long)(4 * rq) * qstride, l + rq * 1024);
-        dma16_sbase(dma_off, dO + rows + (long)(4 * rq) * qstride, l + QT + rq * 1024);
-      }
-      if (cw == 0) dma4(vs + p0, l + 2 * QT);
-    } else {   // same DMA count per wave as a full tile
-#pragma unroll
-      for (int i = 0; i < QPW; ++i) {
-        const int rq = cw + 4 * i;
-        const int row = 4 * rq + (lane >> 4);
-        const int chunk = (lane & 15) ^ swz(row);
-        const long src = rows + (long)min(row, S - p0 - 1) * qstride + 8 * chunk;
-        dma16(q + src, l + rq * 1024);
-        dma16(dO + src, l + QT + rq * 1024);
-      }
-      if (cw == 0) dma4(vs + min(p0, S - 1 - l32), l + 2 * QT);
-    }
-  };
-  int itl = c / G, ih = c - itl * G;           // issue cursor
-  int ch = ih, ctl = itl;                      // compute cursor (tile s of the walk)
-  for (int it = 0; it < NSTAGE - 3 && it < n_u; ++it) {
-    issue(it, ih, itl);
-    advance(ih, itl);
-  }
-
-  // B operands: this lane's key rows of K (S wave) or -V (dP wave), one per
-  // key block
-  bf16x8 breg[2][8];
-  if (role < 2) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int kk = min(kw0 + 32 * kb + l32, S - 1);
-      const __bf16* src = (role == 0 ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
-      if (role == 1) {
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = neg8(breg[kb][ks]);
-      }
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) pin(breg[kb][ks]);
-    }
-  }
-  f32x16 acc[2][4];   // dV^T (dV wave) or dK^T (dK wave), per key block
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-    for (int db = 0; db < 4; ++db) acc[kb][db] = zero16();
-  }
-  const LdsBases lb = make_lds_bases(lane);
-  float* const pbox = reinterpret_cast<float*>(smem + NSTAGE * BUF + quad * PBOX) + lane * 4;
-  char* const dbox = smem + NSTAGE * BUF + 2 * PBOX + quad * DBOX + lane * 16;
-  const float neg_sm_scale = -sm_scale;
-  wait_dma();
-  __syncthreads();
-
-  constexpr int PFR = MM1_DKDV_PF_ROWS;
-  constexpr int PFT = MM1_DKDV_PF_TR;
-  // S = Q K^T / Delta - dP = Delta + dO (-V)^T of one tile for both key blocks
-  // (accumulated onto c0); each row fragment feeds both
-  auto product2 = [&](const char* t, f32x16 (&sacc)[2], const f32x16& c0, auto&& between) MM1_INLINE {
-    sacc[0] = c0;
-    sacc[1] = c0;
-    mfma_chain<8, PFR>(
-        [&](int ks) MM1_INLINE { return rows_a(t, lb, 0, ks); },
-        [&](int ks, const bf16x8& fa) MM1_INLINE {
-          sacc[0] = mfma32(fa, breg[0][ks], sacc[0]);
-          sacc[1] = mfma32(fa, breg[1][ks], sacc[1]);
-        },
-        between);
-  };
-  // dV^T += dO^T P / dK^T += Q^T dS of one tile: fragment i = 4*kh + db of
-  // tile t feeds the products of both key blocks with B operands bop[kb][kh];
-  // its first PFT fragments were read before the barrier
-  auto tr_frag = [&](const char* t, int i) MM1_INLINE { return tr_a(t, lb, i & 3, i >> 2); };
-  bf16x8 nfa[PFT];
-  auto read_first = [&](const char* t) MM1_INLINE {
-#pragma unroll
-    for (int i = 0; i < PFT; ++i) nfa[i] = tr_frag(t, i);
-  };
-  auto accumulate2 = [&](const char* t, const bf16x8 (&bop)[2][2]) MM1_INLINE {
-    mfma_chain_from<8, PFT>(
-        nfa, [&](int i) MM1_INLINE { return tr_frag(t, i); },
-        [&](int i, const bf16x8& a) MM1_INLINE {
-          acc[0][i & 3] = mfma32(a, bop[0][i >> 2], acc[0][i & 3]);
-          acc[1][i & 3] = mfma32(a, bop[1][i >> 2], acc[1][i & 3]);
-        },
-        [](int) MM1_INLINE {});
-  };
-  // the per-query vector of tile t (lanes 0-31: lse2, 32-63: Delta) in the
-  // D layout: register r holds query 8*(r/4) + 4*h + r%4
-  auto read_vec16 = [&](const char* t, int off) MM1_INLINE {
-    const float* vsrc = reinterpret_cast<const float*>(t + 2 * QT) + off;
-    f32x16 v16;
-#pragma unroll
-    for (int a4 = 0; a4 < 4; ++a4) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(vsrc + 8 * a4 + 4 * h);
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc) v16[4 * a4 + cc] = x[cc];
-    }
-    return v16;
-  };
-  // fp32 mailbox block (slot, kb): [a4][lane] x 4 floats, each 16-byte
-  // access of a wave one contiguous 1 KiB row
-  auto pbox_at = [&](int slot, int kb, int a4) MM1_INLINE { return pbox + slot * 2048 + kb * 1024 + 256 * a4; };
-  auto dbox_at = [&](int slot, int jj) MM1_INLINE { return dbox + slot * 4096 + jj * 1024; };
-
-  bf16x8 pb[2][2];      // dV wave: bf16 P(s-2) of both key blocks (B operands)
-  f32x16 dpp[2];        // dP wave: Delta - dP(s-1)
-  // bf16 pack of registers 2j, 2j+1 of x into y[j >> 2] element pair j & 3
-  auto pack_pair = [&](const f32x16& x, bf16x8 (&y)[2], int jj) MM1_INLINE {
-#pragma unroll
-    for (int e = 0; e < 2; ++e) y[jj >> 2][2 * (jj & 3) + e] = (__bf16)x[2 * jj + e];
-    if ((jj & 3) == 3) pin(y[jj >> 2]);
-  };
-
-  // Segment s.  tc, tp, tp2: ring slots of tiles s, s-1, s-2.  CUR: s < n_u;
-  // PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a later segment
-  // reads what this one publishes.
-  auto segment = [&](const char* tc, const char* tp, const char* tp2, int refill, int s, auto rl,
-                     auto cur, auto prev, auto prev2, auto sync) MM1_INLINE {
-    constexpr int RL = decltype(rl)::value;
-    constexpr bool CUR = decltype(cur)::value, PREV = decltype(prev)::value;
-    constexpr bool PREV2 = decltype(prev2)::value, SYNC = decltype(sync)::value;
-    if (CUR && s + NSTAGE - 3 < n_u) {
-      if constexpr (RL >= 2) issue(refill, ih, itl);
-      advance(ih, itl);
-    }
-    if constexpr (RL == 0) {
-      if constexpr (CUR) {
-        f32x16 sv_[2];
-        // the 8 Q fragments, each feeding both key blocks; key block 0's
-        // products first, then key block 1's with the exponentials of block 0
-        // between them (the dV wave's products on the same SIMD run under the
-        // rest of the exponentials)
-        bf16x8 qf[8];
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) qf[ks] = rows_a(tc, lb, 0, ks);
-        const f32x16 l16 = read_vec16(tc, 0);
-        auto exp_at = [&](int kb, int r) MM1_INLINE {
-          float x = exp2_fast(fmaf(sv_[kb][r], scale2, -l16[r]));
-          pin(x);
-          sv_[kb][r] = x;
-        };
-        f32x16 (&sv)[2] = sv_;
-        sv[0] = zero16();
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-          __builtin_amdgcn_sched_barrier(0);
-          sv[0] = mfma32(qf[ks], breg[0][ks], sv[0]);
-        }
-        sv[1] = zero16();
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-          __builtin_amdgcn_sched_barrier(0);
-          sv[1] = mfma32(qf[ks], breg[1][ks], sv[1]);
-          __builtin_amdgcn_sched_barrier(0);
-          exp_at(0, 2 * ks);
-          exp_at(0, 2 * ks + 1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) exp_at(1, r);
-        // causal / past-the-end mask, only in the tiles that need it
-        const int p0 = tile_p0(ctl);
-        if ((CAUSAL && p0 < kw0 + 63) || p0 + BQ > S) {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            const int key = kw0 + 32 * kb + l32;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int qpos = p0 + 8 * (r >> 2) + 4 * h + (r & 3);
-              sv[kb][r] = ((CAUSAL && key > qpos) || qpos >= S) ? 0.f : sv[kb][r];
-            }
-          }
-        }
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-            f32x4 v4;
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) v4[cc] = sv[kb][4 * a4 + cc];
-            *reinterpret_cast<f32x4*>(pbox_at(s & 1, kb, a4)) = v4;
-          }
-        }
-      }
-    } else if constexpr (RL == 1) {
-      // dS(s-1) from P(s-1) (mailbox) and Delta - dP(s-1), between the
-      // products of Delta - dP(s)
-      f32x16 psv[2];
-      auto read_p = [&]() MM1_INLINE {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-            const f32x4 p4 = *reinterpret_cast<const f32x4*>(pbox_at((s - 1) & 1, kb, a4));
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) psv[kb][4 * a4 + cc] = p4[cc];
-          }
-        }
-      };
-      bf16x8 sbn[2][2];
-      auto ds_pair = [&](int jj) MM1_INLINE {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int r = 2 * jj + e;
-            float x = psv[kb][r] * neg_sm_scale * dpp[kb][r];
-            pin(x);
-            psv[kb][r] = x;
-          }
-          pack_pair(psv[kb], sbn[kb], jj);
-        }
-      };
-      if constexpr (CUR) {
-        // the mailbox is read after the first product (the reads of the new
-        // tile go first) and dS computed two products late
-        const f32x16 d16 = read_vec16(tc, BQ);
-        f32x16 dpn[2];
-        product2(tc + QT, dpn, d16, [&](int ks) MM1_INLINE {
-          if constexpr (PREV) {
-            if (ks == 0) read_p();
-            if (ks >= 2) ds_pair(ks - 2);
-          }
-        });
-        if constexpr (PREV) {
-          ds_pair(6);
-          ds_pair(7);
-        }
-        dpp[0] = dpn[0];
-        dpp[1] = dpn[1];
-      } else if constexpr (PREV) {
-        read_p();
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) ds_pair(jj);
-      }
-      if constexpr (PREV) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh)
-            *reinterpret_cast<bf16x8*>(dbox_at((s - 1) & 1, 2 * kb + kh)) = sbn[kb][kh];
-        }
-      }
-    } else if constexpr (RL == 2) {
-      if constexpr (PREV2) accumulate2(tp2 + QT, pb);
-      if constexpr (PREV) {
-        // for the next segment: bf16 P(s-1) and the first fragments of dO(s-1)^T
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          f32x16 p16;
-#pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-            const f32x4 p4 = *reinterpret_cast<const f32x4*>(pbox_at((s - 1) & 1, kb, a4));
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) p16[4 * a4 + cc] = p4[cc];
-          }
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) pack_pair(p16, pb[kb], jj);
-        }
-        read_first(tp + QT);
-      }
-    } else {
-      if constexpr (PREV2) {
-        bf16x8 sbp[2][2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh)
-            sbp[kb][kh] = *reinterpret_cast<const bf16x8*>(dbox_at((s - 2) & 1, 2 * kb + kh));
-        }
-        accumulate2(tp2, sbp);
-      }
-      if constexpr (PREV) read_first(tp);   // Q(s-1)^T for the next segment
-    }
-    if constexpr (CUR) advance(ch, ctl);
-    if constexpr (SYNC) {
-      // tile s+1 must have landed; the newer prefetches stay in flight
-      // (2 * QPW copies per tile and copying wave, wave cw == 0 one more)
-      if (w >= 4) {
-        if (s + NSTAGE - 3 < n_u) {
-          if (cw == 0) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"((2 * QPW + 1) * 2) : "memory");
-          else __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * QPW * 2) : "memory");
-        } else {
-          wait_dma();
-        }
-      }
-      lds_barrier();
-    }
-  };
-
-  using T = std::true_type;
-  using F = std::false_type;
-  auto slot = [&](int cc) MM1_INLINE { return smem + cc * BUF; };
-  auto run = [&](auto rl) MM1_INLINE {
-    const char* s0p = slot(0);
-    if (n_u == 1) {
-      segment(s0p, s0p, s0p, NSTAGE - 3, 0, rl, T{}, F{}, F{}, T{});
-      segment(s0p, s0p, s0p, 0, 1, rl, F{}, T{}, F{}, T{});
-      segment(s0p, s0p, s0p, 0, 2, rl, F{}, F{}, T{}, F{});
-      return;
-    }
-    segment(s0p, s0p, s0p, NSTAGE - 3, 0, rl, T{}, F{}, F{}, T{});
-    segment(slot(1), s0p, s0p, NSTAGE - 2, 1, rl, T{}, T{}, F{}, T{});
-    for (int b0 = 2; b0 < n_u; b0 += NSTAGE) {
-      unroll_while<0, NSTAGE>([&](auto jj) MM1_INLINE {
-        constexpr int C = (2 + decltype(jj)::value) % NSTAGE;
-        const int s = b0 + decltype(jj)::value;
-        if (s >= n_u) return false;
-        segment(slot(C), slot((C + NSTAGE - 1) % NSTAGE), slot((C + NSTAGE - 2) % NSTAGE),
-                (C + 3) % NSTAGE, s, rl, T{}, T{}, T{}, T{});
-        return true;
-      });
-    }
-    const char* tl = slot((n_u - 1) % NSTAGE);
-    const char* tl2 = slot((n_u - 2) % NSTAGE);
-    segment(tl, tl, tl2, 0, n_u, rl, F{}, T{}, T{}, T{});
-    segment(tl, tl, tl, 0, n_u + 1, rl, F{}, F{}, T{}, F{});
-  };
-  switch (role) {
-    case 0: run(std::integral_constant<int, 0>{}); break;
-    case 1: run(std::integral_constant<int, 1>{}); break;
-    case 2: run(std::integral_constant<int, 2>{}); break;
-    default: run(std::integral_constant<int, 3>{}); break;
-  }
-  if (role < 2) return;
-
-  // D layout of dK^T / dV^T: register r of block db holds column
-  // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.
-  const bool dvw = role == 2;
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    const int key = kw0 + 32 * kb + l32;
-    if (key >= S) continue;
-    if (nparts == 1 && !force_partials) {
-      __bf16* row = (dvw ? dv : dk) + ((long)(b * S + key) * Hkv + g) * HD;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-          bf16x4 o4;
-#pragma unroll
-          for (int cc = 0; cc < 4; ++cc) o4[cc] = (__bf16)acc[kb][db][4 * a4 + cc];
-          *reinterpret_cast<bf16x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
-        }
-      }
-    } else {
-      const long wslot = (long)part * B * ws_rows * Hkv * HD;
-      float* row = (dvw ? ws_dv : ws_dk) + wslot + ((long)(b * ws_rows + key) * Hkv + g) * HD;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-          f32x4 o4;
-#pragma unroll
-          for (int cc = 0; cc < 4; ++cc) o4[cc] = acc[kb][db][4 * a4 + cc];
           *reinterpret_cast<f32x4*>(row + 32 * db + 8 * a4 + 4 * h) = o4;
         }
       }
@@ -1478,13 +910,15 @@ __device__ __forceinline__ void tail_reduce(const TailReduce& red, int tid, int 
 // ---------------------------------------------------------------------------
 // dQ: one workgroup per NW*32 packed query rows (32 per wave); K and V tiles
 // of 64 keys arrive by LDS DMA (row-major) in an NSTAGE-deep ring; K^T for
-// dQ^T = K^T dS^T is read transposed from the same K tile.
-// F32OUT: dq is fp32 (the fp32 backward), else bf16.
+// dQ^T = K^T dS^T is read transposed from the same K tile.  Operands are the
+// fp16 q16, k16, v16 and do16 = fp16(2^E dO) (Delta scaled alike); dQ is
+// multiplied by scale[0] = 2^-E on the way out.
+// F32OUT: dq is fp32 (the values the bf16 path rounds), else bf16.
 template <int NW, int NSTAGE, bool CAUSAL, bool F32OUT = false>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    const __bf16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
-    void* __restrict__ dq_out,
+    const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
+    const _Float16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
+    const float* __restrict__ scale, void* __restrict__ dq_out,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles, TailReduce red,
     const DispatchOrder ord) {
   constexpr int BM = NW * 32;
@@ -1517,8 +951,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
   const int pw_hi = wave_active ? min(S - 1, (min(rw0 + 32, R) - 1) / G) : -1;
 
   const long kvstride = (long)Hkv * HD;
-  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
-  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
+  const _Float16* kbase = k + ((long)b * S * Hkv + g) * HD;
+  const _Float16* vbase = v + ((long)b * S * Hkv + g) * HD;
   const uint32_t dma_off = tile_lane_off(kvstride, tid);
   auto issue_tile = [&](char* buf, int kt) {
     const int nk = kt * BN;
@@ -1534,17 +968,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
   const int hh = rr - qp * G;
   const bool row_valid = rr < R;
   const long roff = ((long)(b * S + qp) * H + g * G + hh) * HD;
-  bf16x8 qreg[8], doreg[8];
+  f16x8 qreg[8], doreg[8];
   float lse_i = INFINITY, dl_i = 0.f;
   if (row_valid) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      qreg[ks] = *reinterpret_cast<const bf16x8*>(q + roff + 16 * ks + 8 * h);
-      doreg[ks] = *reinterpret_cast<const bf16x8*>(dO + roff + 16 * ks + 8 * h);
+      qreg[ks] = *reinterpret_cast<const f16x8*>(q + roff + 16 * ks + 8 * h);
+      doreg[ks] = *reinterpret_cast<const f16x8*>(dO + roff + 16 * ks + 8 * h);
     }
     const long li = ((long)b * H + g * G + hh) * S + qp;
     // P sm_scale = exp2(s scale2 - (lse2 - log2 sm_scale)): dS comes out
-    // scaled, and is rounded to bf16 with the scale in it, as the reference's
+    // scaled, and is rounded to fp16 with the scale in it, as the reference's
     lse_i = lse2[li] - log2f(sm_scale);
     dl_i = delta[li];
 #pragma unroll
@@ -1554,7 +988,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) { qreg[ks][t] = (__bf16)0.f; doreg[ks][t] = (__bf16)0.f; }
+      for (int t = 0; t < 8; ++t) { qreg[ks][t] = (_Float16)0.f; doreg[ks][t] = (_Float16)0.f; }
     }
   }
 
@@ -1587,7 +1021,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
         wave_prio<1>();
         // K / V fragments read PF k-steps ahead of their products
         constexpr int PF = MM1_DQ_PREFETCH;
-        bf16x8 ka[PF + 1], va[PF + 1];
+        f16x8 ka[PF + 1], va[PF + 1];
 #pragma unroll
         for (int ks = 0; ks < PF; ++ks) {
           ka[ks] = rows_a(kl, lb, jb, ks);
@@ -1602,8 +1036,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
           // keep the reads ahead: the scheduler would otherwise sink them
           // to their products and expose the LDS latency on every pair
           __builtin_amdgcn_sched_barrier(0);
-          sv = mfma32(ka[ks % (PF + 1)], qreg[ks], sv);
-          dp = mfma32(va[ks % (PF + 1)], doreg[ks], dp);
+          sv = mfma32h(ka[ks % (PF + 1)], qreg[ks], sv);
+          dp = mfma32h(va[ks % (PF + 1)], doreg[ks], dp);
           __builtin_amdgcn_sched_barrier(0);
         }
         // dS^T = P^T (dP^T - Delta), masked only in the tiles that need it,
@@ -1625,10 +1059,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
         wave_prio<1>();
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-          const bf16x8 sb = pack8(sv, 8 * kh);
+          const f16x8 sb = pack8(sv, 8 * kh);
 #pragma unroll
           for (int db = 0; db < 4; ++db)
-            dqacc[db] = mfma32(tr_a(kl, lb, db, 2 * jb + kh), sb, dqacc[db]);
+            dqacc[db] = mfma32h(tr_a(kl, lb, db, 2 * jb + kh), sb, dqacc[db]);
         }
       }
     }
@@ -1647,11 +1081,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     }
   }
 
+  const float unscale = scale[0];   // 2^-E of do16
   if constexpr (!F32OUT) {
     // every slot is free after the last step's barrier: each wave's rows go
     // out through 8 KiB of it (store_tile_bf16)
     if (wave_active)
-      store_tile_bf16(dqacc, 1.f, smem + w * 8192, lane, [&](int i) -> __bf16* {
+      store_tile_bf16(dqacc, unscale, smem + w * 8192, lane, [&](int i) -> __bf16* {
         const int r = rw0 + i;
         if (r >= R) return nullptr;
         const int p = r / G;
@@ -1665,12 +1100,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
         if constexpr (F32OUT) {
           f32x4 val;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) val[c] = dqacc[db][4 * a4 + c];
+          for (int c = 0; c < 4; ++c) val[c] = dqacc[db][4 * a4 + c] * unscale;
           *reinterpret_cast<f32x4*>(static_cast<float*>(dq_out) + roff + 32 * db + 8 * a4 + 4 * h) = val;
         } else {
           bf16x4 val;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) val[c] = (__bf16)dqacc[db][4 * a4 + c];
+          for (int c = 0; c < 4; ++c) val[c] = (__bf16)(dqacc[db][4 * a4 + c] * unscale);
           *reinterpret_cast<bf16x4*>(static_cast<__bf16*>(dq_out) + roff + 32 * db + 8 * a4 + 4 * h) = val;
         }
       }
@@ -1691,10 +1126,24 @@ hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int 
   return hipGetLastError();
 }
 
-size_t bwd_workspace_bytes(int B, int S, int H, int Hkv) {
-  const int G = H / Hkv;
-  if (G <= 1) return 0;
-  return (size_t)2 * G * B * S * Hkv * HD * sizeof(float);
+// Delta (from o + o_lo, or the caller's delta_in when o is null), max|dO|,
+// then do16 = fp16(2^E dO), Delta *= 2^E and the scale cells: what the
+// dK/dV and dQ kernels read from the workspace.
+hipError_t launch_bwd_prep(const void* o, const uint8_t* o_lo, const void* dO, const float* delta_in,
+                           const float* vmax, char* ws, int B, int S, int H, int Hkv, float sm_scale,
+                           hipStream_t stream) {
+  const BwdWs w = bwd_ws(B, S, H, Hkv);
+  float* delta = reinterpret_cast<float*>(ws + w.delta);
+  float* dmax = reinterpret_cast<float*>(ws + w.dmax);
+  hipLaunchKernelGGL(attn_delta16_kernel, dim3(kDeltaBlocks), dim3(256), 0, stream,
+                     static_cast<const __bf16*>(o), o_lo, static_cast<const __bf16*>(dO), delta_in, delta,
+                     reinterpret_cast<_Float16*>(ws + w.do16), dmax, B, S, H);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attn_do16_kernel, dim3(1024), dim3(256), 0, stream, static_cast<const __bf16*>(dO),
+                     reinterpret_cast<_Float16*>(ws + w.do16), delta, dmax, kDeltaBlocks, vmax, kCvtBlocks,
+                     reinterpret_cast<float*>(ws + w.scale), sm_scale, (long)B * S * H * HD, (long)B * H * S);
+  return hipGetLastError();
 }
 
 // Where the partial sums of dK/dV tiling `variant` live in a workspace:
@@ -1716,8 +1165,8 @@ size_t bwd_partials_bytes(int B, int S, int H, int Hkv, bool causal, int variant
 }
 
 // The reduction that follows dK/dV tiling `dkdv_variant` (n_red = 0 when
-// there is nothing to sum).
-TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
+// there is nothing to sum); f32: the sums go to dk / dv as fp32.
+TailReduce make_reduce(const float* partials, void* dk, void* dv, bool f32, int B, int S, int H, int Hkv,
                        bool causal, int dkdv_variant) {
   const int G = H / Hkv;
   TailReduce red{};
@@ -1725,13 +1174,18 @@ TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, 
   red.S = S;
   red.Hkv = Hkv;
   red.causal = causal ? 1 : 0;
-  if (!workspace || G <= 1) return red;
+  if (!partials || G <= 1) return red;
   const WsSlots w = ws_slots(B, S, H, Hkv, causal, dkdv_variant);
   red.n = w.stride;
-  red.ws_dk = static_cast<const float*>(workspace);
+  red.ws_dk = partials;
   red.ws_dv = red.ws_dk + (long)w.slots * w.stride;
-  red.dk = static_cast<__bf16*>(dk);
-  red.dv = static_cast<__bf16*>(dv);
+  if (f32) {
+    red.dk32 = static_cast<float*>(dk);
+    red.dv32 = static_cast<float*>(dv);
+  } else {
+    red.dk = static_cast<__bf16*>(dk);
+    red.dv = static_cast<__bf16*>(dv);
+  }
   if (dkdv_grouped(dkdv_variant)) {
     const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
     red.chunk_tiles = plan.L;
@@ -1742,14 +1196,31 @@ TailReduce make_reduce(const void* workspace, void* dk, void* dv, int B, int S, 
   return red;
 }
 
+// The fp16 operands and scaled values the dK/dV and dQ kernels read.
+struct BwdOperands {
+  const _Float16 *q, *k, *v, *dO;
+  const float *lse2, *delta, *scale;
+};
+
+BwdOperands bwd_operands(const char* state, const char* ws, const float* lse2, int B, int S, int H, int Hkv) {
+  const FwdState f = fwd_state(B, S, H, Hkv);
+  const BwdWs w = bwd_ws(B, S, H, Hkv);
+  BwdOperands o;
+  o.q = reinterpret_cast<const _Float16*>(state + f.q16);
+  o.k = reinterpret_cast<const _Float16*>(state + f.k16);
+  o.v = reinterpret_cast<const _Float16*>(state + f.v16);
+  o.dO = reinterpret_cast<const _Float16*>(ws + w.do16);
+  o.lse2 = lse2;
+  o.delta = reinterpret_cast<const float*>(ws + w.delta);
+  o.scale = reinterpret_cast<const float*>(ws + w.scale);
+  return o;
+}
+
 // The pipelined dK/dV kernel for one tiling: GROUP (one workgroup per key
-// tile over the G heads of its KV group, chunked by dkdv_plan) or per head;
-// KB key blocks per wave.
-template <bool GROUP, int KB>
-static void launch_dkdv_pipe(const __bf16* qp, const __bf16* kp, const __bf16* vp, const __bf16* dop,
-                             const float* lse2, const float* delta, float* ws_dk, float* ws_dv,
-                             __bf16* dkp, __bf16* dvp, int B, int S, int H, int Hkv, bool causal,
-                             float scale2, float sm_scale, hipStream_t stream, int force_partials = 0) {
+// tile over the G heads of its KV group, chunked by dkdv_plan) or per head.
+template <bool GROUP, bool F32OUT>
+static void launch_dkdv_pipe(const BwdOperands& op, float* ws_dk, float* ws_dv, void* dk, void* dv, int B, int S,
+                             int H, int Hkv, bool causal, float scale2, float sm_scale, hipStream_t stream) {
   const int G = H / Hkv;
   const bool ragged = S % 32 != 0;
   const KeyTileOrder order = key_tile_order(B * H);
@@ -1767,12 +1238,12 @@ static void launch_dkdv_pipe(const __bf16* qp, const __bf16* kp, const __bf16* v
     grid = dim3(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
     ord = &dispatch_order(row_block_grid(0, B, S, H, Hkv), false);   // unused: default order
   }
-  const dim3 block(512 / KB);
+  const dim3 block(512);
   const int ws_rows = ws_slots(B, S, H, Hkv, causal, GROUP ? 0 : 1).rows;
-#define MM1_DKDV_PIPE(CS, RG)                                                                      \
-  hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, GROUP, RG, KB>), grid, block, 0, stream, qp, kp, vp, \
-                     dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale,      \
-                     order, L, C, *ord, force_partials, ws_rows)
+#define MM1_DKDV_PIPE(CS, RG)                                                                              \
+  hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, GROUP, RG, F32OUT>), grid, block, 0, stream, op.q, op.k, op.v, \
+                     op.dO, op.lse2, op.delta, op.scale, ws_dk, ws_dv, dk, dv, B, S, H, Hkv, G, scale2,         \
+                     sm_scale, order, L, C, *ord, ws_rows)
   if (causal) {
     if (ragged) MM1_DKDV_PIPE(true, true);
     else MM1_DKDV_PIPE(true, false);
@@ -1783,103 +1254,40 @@ static void launch_dkdv_pipe(const __bf16* qp, const __bf16* kp, const __bf16* v
 #undef MM1_DKDV_PIPE
 }
 
-// The quad kernel (grouped grid and chunk plan of the pipelined kernel).
-static void launch_dkdv_quad(const __bf16* qp, const __bf16* kp, const __bf16* vp, const __bf16* dop,
-                             const float* lse2, const float* delta, float* ws_dk, float* ws_dv,
-                             __bf16* dkp, __bf16* dvp, int B, int S, int H, int Hkv, bool causal,
-                             float scale2, float sm_scale, hipStream_t stream, int force_partials = 0) {
-  const int G = H / Hkv;
-  const bool ragged = S % 32 != 0;
-  const DkdvPlan& plan = dkdv_plan(B, S, H, Hkv, causal);
-  const dim3 grid(plan.order.n ? plan.order.n : plan.n_items), block(512);
-  const int ws_rows = ws_slots(B, S, H, Hkv, causal, 5).rows;
-#define MM1_DKDV_QUAD(CS, RG)                                                                        \
-  hipLaunchKernelGGL((attn_dkdv_quad_kernel<CS, RG>), grid, block, 0, stream, qp, kp, vp, dop, lse2,   \
-                     delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, plan.L, plan.C, \
-                     plan.order, force_partials, ws_rows)
-  if (causal) {
-    if (ragged) MM1_DKDV_QUAD(true, true);
-    else MM1_DKDV_QUAD(true, false);
-  } else {
-    if (ragged) MM1_DKDV_QUAD(false, true);
-    else MM1_DKDV_QUAD(false, false);
-  }
-#undef MM1_DKDV_QUAD
-}
-
-// variant: 0 = attn_dkdv_pipe_kernel over the whole GQA group per key tile
-//              (chunked by dkdv_plan), 8 waves x 32 keys,
-//          1 = attn_dkdv_pipe_kernel, one workgroup per (key tile, query
-//              head), 8 waves x 32 keys,
-//          2 = attn_dkdv_kernel (64-query tiles, two barriers per 32 queries),
-//          3 = as 0 with 4 waves x 64 keys (one wave per SIMD),
-//          4 = as 1 with 4 waves x 64 keys,
-//          5 = attn_dkdv_quad_kernel (grouped, quads of single-product waves).
-hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
-                           const float* lse2, const float* delta, void* dk, void* dv,
-                           void* workspace, int B, int S, int H, int Hkv, bool causal,
-                           float sm_scale, int variant, hipStream_t stream) {
-  const int G = H / Hkv;
+// dK/dV from the state and a prepared workspace.  variant: 0 = over the
+// whole GQA group per key tile (chunked by dkdv_plan), 1 = one workgroup per
+// (key tile, query head).  f32: dk / dv are fp32.
+hipError_t launch_bwd_dkdv(const char* state, char* ws, const float* lse2, void* dk, void* dv, bool f32,
+                           int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
+                           hipStream_t stream) {
   const float scale2 = sm_scale * 1.4426950408889634f;
+  const BwdOperands op = bwd_operands(state, ws, lse2, B, S, H, Hkv);
   const WsSlots w = ws_slots(B, S, H, Hkv, causal, variant);
-  float* ws_dk = static_cast<float*>(workspace);
+  float* ws_dk = H / Hkv > 1 ? reinterpret_cast<float*>(ws + bwd_ws(B, S, H, Hkv).partials) : nullptr;
   float* ws_dv = ws_dk ? ws_dk + (long)w.slots * w.stride : nullptr;
-  auto qp = static_cast<const __bf16*>(q);
-  auto kp = static_cast<const __bf16*>(k);
-  auto vp = static_cast<const __bf16*>(v);
-  auto dop = static_cast<const __bf16*>(dO);
-  auto dkp = static_cast<__bf16*>(dk);
-  auto dvp = static_cast<__bf16*>(dv);
-  switch (variant) {
-    case 0:
-      launch_dkdv_pipe<true, 1>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
-                                scale2, sm_scale, stream);
-      break;
-    case 1:
-      launch_dkdv_pipe<false, 1>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
-                                 scale2, sm_scale, stream);
-      break;
-    case 3:
-      launch_dkdv_pipe<true, 2>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
-                                scale2, sm_scale, stream);
-      break;
-    case 4:
-      launch_dkdv_pipe<false, 2>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal,
-                                 scale2, sm_scale, stream);
-      break;
-    case 5:
-      launch_dkdv_quad(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, causal, scale2,
-                       sm_scale, stream);
-      break;
-    default: {
-      const KeyTileOrder order = key_tile_order(B * H);
-      const int n_ktiles = (S + 127) / 128;
-      const dim3 grid(8 * order.m * ((n_ktiles + order.q - 1) / order.q));
-      if (causal)
-        hipLaunchKernelGGL(attn_dkdv_kernel<true>, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta,
-                           ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, order);
-      else
-        hipLaunchKernelGGL(attn_dkdv_kernel<false>, grid, dim3(512), 0, stream, qp, kp, vp, dop, lse2, delta,
-                           ws_dk, ws_dv, dkp, dvp, B, S, H, Hkv, G, scale2, sm_scale, order);
-    }
+  if (variant == 0) {
+    if (f32) launch_dkdv_pipe<true, true>(op, ws_dk, ws_dv, dk, dv, B, S, H, Hkv, causal, scale2, sm_scale, stream);
+    else launch_dkdv_pipe<true, false>(op, ws_dk, ws_dv, dk, dv, B, S, H, Hkv, causal, scale2, sm_scale, stream);
+  } else {
+    if (f32) launch_dkdv_pipe<false, true>(op, ws_dk, ws_dv, dk, dv, B, S, H, Hkv, causal, scale2, sm_scale, stream);
+    else launch_dkdv_pipe<false, false>(op, ws_dk, ws_dv, dk, dv, B, S, H, Hkv, causal, scale2, sm_scale, stream);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
+hipError_t launch_bwd_reduce(const char* ws, void* dk, void* dv, bool f32, int B, int S, int H, int Hkv,
                              bool causal, int dkdv_variant, hipStream_t stream) {
-  const TailReduce red = make_reduce(workspace, dk, dv, B, S, H, Hkv, causal, dkdv_variant);
+  const float* partials = reinterpret_cast<const float*>(ws + bwd_ws(B, S, H, Hkv).partials);
+  const TailReduce red = make_reduce(partials, dk, dv, f32, B, S, H, Hkv, causal, dkdv_variant);
   if (red.n_red == 0) return hipSuccess;
   const long blocks = (reduce_len(red) / 4 + 255) / 256;
   hipLaunchKernelGGL(attn_dkdv_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, red);
   return hipGetLastError();
 }
 
-template <int NW, int NSTAGE, bool F32OUT = false>
-static void launch_dq_t(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* dO,
-                        const float* lse2, const float* delta, void* dq, int B, int S, int H,
-                        int Hkv, bool causal, float scale2, float sm_scale, TailReduce red,
-                        const DispatchOrder& ord, hipStream_t stream) {
+template <int NW, int NSTAGE, bool F32OUT>
+static void launch_dq_t(const BwdOperands& op, void* dq, int B, int S, int H, int Hkv, bool causal, float scale2,
+                        float sm_scale, TailReduce red, const DispatchOrder& ord, hipStream_t stream) {
   const int G = H / Hkv;
   const int BM = NW * 32;
   const int n_qtiles = (G * S + BM - 1) / BM;
@@ -1887,77 +1295,34 @@ static void launch_dq_t(const __bf16* q, const __bf16* k, const __bf16* v, const
   if (red.n_red > 0) red.n_red = min(red.n_red, n_blocks);
   dim3 grid(n_blocks), block(NW * 64);
   if (causal)
-    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, true, F32OUT>), grid, block, 0, stream, q, k, v, dO, lse2,
-                       delta, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
+    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, true, F32OUT>), grid, block, 0, stream, op.q, op.k, op.v, op.dO,
+                       op.lse2, op.delta, op.scale, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
   else
-    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, false, F32OUT>), grid, block, 0, stream, q, k, v, dO, lse2,
-                       delta, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
+    hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, false, F32OUT>), grid, block, 0, stream, op.q, op.k, op.v, op.dO,
+                       op.lse2, op.delta, op.scale, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
 }
 
-// variant: 0 = 4 waves x 2-stage ring (two workgroups per CU),
-//          1 = 8 waves x 3-stage ring (one workgroup per CU).
-// workspace != nullptr: also sum the dK/dV partials that tiling dkdv_variant
-// left in it into dk, dv (what launch_bwd_reduce does), in the dQ grid's tail.
-hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
-                         const float* lse2, const float* delta, void* dq,
-                         const void* workspace, void* dk, void* dv,
-                         int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
-                         int dkdv_variant, hipStream_t stream) {
+// dQ from the state and a prepared workspace.  variant: 0 = 4 waves x
+// 2-stage ring (two workgroups per CU), 1 = 8 waves x 3-stage ring (one per
+// CU).  reduce: also sum the dK/dV partials that tiling dkdv_variant left in
+// the workspace into dk, dv (what launch_bwd_reduce does), in the dQ grid's
+// tail.  f32: dq (and dk, dv) are fp32.
+hipError_t launch_bwd_dq(const char* state, char* ws, const float* lse2, void* dq, bool reduce, void* dk,
+                         void* dv, bool f32, int B, int S, int H, int Hkv, bool causal, float sm_scale,
+                         int variant, int dkdv_variant, hipStream_t stream) {
   const float scale2 = sm_scale * 1.4426950408889634f;
-  auto qp = static_cast<const __bf16*>(q);
-  auto kp = static_cast<const __bf16*>(k);
-  auto vp = static_cast<const __bf16*>(v);
-  auto dop = static_cast<const __bf16*>(dO);
+  const BwdOperands op = bwd_operands(state, ws, lse2, B, S, H, Hkv);
+  const float* partials = reduce ? reinterpret_cast<const float*>(ws + bwd_ws(B, S, H, Hkv).partials) : nullptr;
   // with n_red = 1 << 30 every workgroup of the grid takes a slice
-  const TailReduce red = make_reduce(workspace, dk, dv, B, S, H, Hkv, causal, dkdv_variant);
+  const TailReduce red = make_reduce(partials, dk, dv, f32, B, S, H, Hkv, causal, dkdv_variant);
   const DispatchOrder& ord = dispatch_order(dq_grid(variant, B, S, H, Hkv), causal);
-  if (variant == 1)
-    launch_dq_t<8, 3>(qp, kp, vp, dop, lse2, delta, dq, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
-  else
-    launch_dq_t<4, 2>(qp, kp, vp, dop, lse2, delta, dq, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
-  return hipGetLastError();
-}
-
-// Bytes of fp32 scratch of the fp32 backward: G >= 1 slots of dK and dV
-// partials (the per-head layout, also for G == 1).
-size_t bwd_f32_workspace_bytes(int B, int S, int H, int Hkv) {
-  return (size_t)2 * (H / Hkv) * B * S * Hkv * HD * sizeof(float);
-}
-
-// fp32 gradients: the per-head dK/dV tiling with fp32 partials for every
-// head, their sum in slot order written in fp32, and dQ written in fp32 --
-// the values the bf16 backward rounds (up to the order of the fp32 sums of
-// the grouped tiling), as the reference kernel's fp32 dQ / dK / dV buffers
-// hold them before its casts.
-hipError_t launch_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
-                          const float* lse2, const float* delta, float* dq, float* dk, float* dv,
-                          void* workspace, int B, int S, int H, int Hkv, bool causal, float sm_scale,
-                          hipStream_t stream) {
-  const int G = H / Hkv;
-  const float scale2 = sm_scale * 1.4426950408889634f;
-  auto qp = static_cast<const __bf16*>(q);
-  auto kp = static_cast<const __bf16*>(k);
-  auto vp = static_cast<const __bf16*>(v);
-  auto dop = static_cast<const __bf16*>(dO);
-  const long n_kv = (long)B * S * Hkv * HD;
-  float* ws_dk = static_cast<float*>(workspace);
-  float* ws_dv = ws_dk + (long)G * n_kv;
-  launch_dkdv_pipe<false, 1>(qp, kp, vp, dop, lse2, delta, ws_dk, ws_dv, nullptr, nullptr, B, S, H, Hkv, causal,
-                             scale2, sm_scale, stream, 1);
-  TailReduce red{};
-  red.ws_dk = ws_dk;
-  red.ws_dv = ws_dv;
-  red.dk32 = dk;
-  red.dv32 = dv;
-  red.n = n_kv;
-  red.G = G;
-  red.S = S;
-  red.Hkv = Hkv;
-  red.causal = causal ? 1 : 0;
-  hipLaunchKernelGGL(attn_dkdv_reduce_kernel, dim3((unsigned)((n_kv / 4 + 255) / 256)), dim3(256), 0, stream, red);
-  TailReduce none{};
-  launch_dq_t<4, 2, true>(qp, kp, vp, dop, lse2, delta, dq, B, S, H, Hkv, causal, scale2, sm_scale, none,
-                          dispatch_order(dq_grid(0, B, S, H, Hkv), causal), stream);
+  if (variant == 1) {
+    if (f32) launch_dq_t<8, 3, true>(op, dq, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
+    else launch_dq_t<8, 3, false>(op, dq, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
+  } else {
+    if (f32) launch_dq_t<4, 2, true>(op, dq, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
+    else launch_dq_t<4, 2, false>(op, dq, B, S, H, Hkv, causal, scale2, sm_scale, red, ord, stream);
+  }
   return hipGetLastError();
 }
 

@@ -8,35 +8,31 @@
 #include "../../include/mm1_attn.h"
 #include "../../include/mm1_swiglu.h"
 #include "../../include/mm1_lm_head.h"
+#include "attn_layout.h"
 #include "dispatch_order.h"
 #include "mm1_common.h"
 
 namespace mm1 {
-hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
-                      int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
-                      hipStream_t stream);
-hipError_t launch_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2,
-                          int B, int S, int H, int Hkv, bool causal, float sm_scale, hipStream_t stream);
+hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2, bool f32,
+                      _Float16* q16, _Float16* k16, _Float16* v16, uint8_t* o_lo, float* vmax, bool save,
+                      int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant, hipStream_t stream);
+hipError_t launch_cvt_kv(const void* k, const void* v, _Float16* k16, _Float16* v16, float* kmax, float* vmax,
+                         long n, hipStream_t stream);
+hipError_t launch_cvt16(const void* x, _Float16* x16, long n, hipStream_t stream);
 hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int S, int H,
                         hipStream_t stream);
-size_t bwd_workspace_bytes(int B, int S, int H, int Hkv);
-hipError_t launch_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
-                           const float* lse2, const float* delta, void* dk, void* dv,
-                           void* workspace, int B, int S, int H, int Hkv, bool causal,
-                           float sm_scale, int variant, hipStream_t stream);
-hipError_t launch_bwd_reduce(const void* workspace, void* dk, void* dv, int B, int S, int H, int Hkv,
+hipError_t launch_bwd_prep(const void* o, const uint8_t* o_lo, const void* dO, const float* delta_in,
+                           const float* vmax, char* ws, int B, int S, int H, int Hkv, float sm_scale,
+                           hipStream_t stream);
+hipError_t launch_bwd_dkdv(const char* state, char* ws, const float* lse2, void* dk, void* dv, bool f32,
+                           int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
+                           hipStream_t stream);
+hipError_t launch_bwd_reduce(const char* ws, void* dk, void* dv, bool f32, int B, int S, int H, int Hkv,
                              bool causal, int dkdv_variant, hipStream_t stream);
-hipError_t launch_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
-                         const float* lse2, const float* delta, void* dq,
-                         const void* workspace, void* dk, void* dv,
-                         int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
-                         int dkdv_variant, hipStream_t stream);
-size_t bwd_f32_workspace_bytes(int B, int S, int H, int Hkv);
+hipError_t launch_bwd_dq(const char* state, char* ws, const float* lse2, void* dq, bool reduce, void* dk,
+                         void* dv, bool f32, int B, int S, int H, int Hkv, bool causal, float sm_scale,
+                         int variant, int dkdv_variant, hipStream_t stream);
 size_t bwd_partials_bytes(int B, int S, int H, int Hkv, bool causal, int variant);
-hipError_t launch_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
-                          const float* lse2, const float* delta, float* dq, float* dk, float* dv,
-                          void* workspace, int B, int S, int H, int Hkv, bool causal, float sm_scale,
-                          hipStream_t stream);
 size_t qknorm_bwd_workspace_bytes();
 hipError_t launch_qknorm_fwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
                              const float* sin_t, void* q, void* k, void* v, int B, int S, int H, int Hkv,
@@ -84,10 +80,6 @@ const char* const kFwdTiles[] = {
 const char* const kDkdvTiles[] = {
     "block_M=128 block_N=32 waves=8 stages=7 schedule=group",
     "block_M=128 block_N=32 waves=8 stages=7 schedule=pipelined",
-    "block_M=128 block_N=64 waves=8 stages=3 schedule=paired",
-    "block_M=128 block_N=32 waves=4 stages=7 schedule=group",
-    "block_M=128 block_N=32 waves=4 stages=7 schedule=pipelined",
-    "block_M=128 block_N=32 waves=8 stages=6 schedule=quad",
 };
 const char* const kDqTiles[] = {
     "block_M=128 block_N=64 waves=4 stages=2 schedule=ring",
@@ -172,12 +164,13 @@ bool layout_matches(const WsLayout& want) {
 int from_hip(hipError_t e) { return e == hipSuccess ? MM1_OK : static_cast<int>(e); }
 
 // ---------------------------------------------------------------------------
-// Scratch of mm1_attn_bwd_noalloc: the dK/dV partial sums of the default
-// backward tilings live in this static device array instead of a workspace
-// the caller allocates.  Every device the library runs on holds its own copy
-// (MM1_NOALLOC_SCRATCH_BYTES) until the process ends.  In host code `scratch`
-// is only a handle: its device address on the current device comes from
-// hipGetSymbolAddress, taken once per device and kept in g_scratch_addr.
+// Scratch of mm1_attn_bwd_noalloc: the backward workspace of the default
+// tilings (fp16 dO, Delta, the dK/dV partial sums) lives in this static
+// device array instead of a buffer the caller allocates.  Every device the
+// library runs on holds its own copy (MM1_NOALLOC_SCRATCH_BYTES) until the
+// process ends.  In host code `scratch` is only a handle: its device address
+// on the current device comes from hipGetSymbolAddress, taken once per
+// device and kept in g_scratch_addr.
 static __device__ __align__(256) char scratch[MM1_NOALLOC_SCRATCH_BYTES];
 
 constexpr int kMaxDevices = 64;
@@ -202,41 +195,179 @@ int scratch_addr(void** out) {
   return MM1_OK;
 }
 
+bool bad_scale(float sm_scale) { return !(sm_scale > 0.f) || !isfinite(sm_scale); }
+
+// Bytes of the backward workspace when its partial sums are those of dK/dV
+// tiling `variant` (the regions before them are fixed).
+size_t ws_bytes_for(int B, int S, int H, int Hkv, bool causal, int variant) {
+  return mm1::bwd_ws(B, S, H, Hkv).partials + mm1::bwd_partials_bytes(B, S, H, Hkv, causal, variant);
+}
+
+// Argument checks shared by the calls that read a forward state and a
+// prepared backward workspace.
+int check_state_ws(const void* state, size_t state_bytes, const void* ws, size_t ws_bytes, int B, int S, int H,
+                   int Hkv) {
+  if (!state || !ws) return MM1_E_NULL;
+  if (state_bytes < mm1::fwd_state(B, S, H, Hkv).bytes || ws_bytes < mm1::bwd_ws(B, S, H, Hkv).bytes)
+    return MM1_E_WORKSPACE;
+  if (!aligned16(state) || !aligned16(ws)) return MM1_E_ALIGN;
+  return MM1_OK;
+}
+
+int fwd_any(const void* q, const void* k, const void* v, void* o, float* lse2, bool f32, void* state,
+            size_t state_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale, int tiles,
+            void* stream) {
+  if (!q || !k || !v || !o || !lse2 || !state) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (bad_scale(sm_scale)) return MM1_E_SCALE;
+  if (state_bytes < mm1::fwd_state(B, S, H, Hkv).bytes) return MM1_E_WORKSPACE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(state)) return MM1_E_ALIGN;
+  const int variant = pick_tiles(MM1_TILES_FWD, tiles);
+  if (variant < 0) return MM1_E_TILES;
+  const mm1::FwdState f = mm1::fwd_state(B, S, H, Hkv);
+  char* st = static_cast<char*>(state);
+  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, f32, reinterpret_cast<_Float16*>(st + f.q16),
+                                  reinterpret_cast<_Float16*>(st + f.k16), reinterpret_cast<_Float16*>(st + f.v16),
+                                  reinterpret_cast<uint8_t*>(st + f.olo), reinterpret_cast<float*>(st + f.vmax), true,
+                                  B, S, H, Hkv, causal != 0, sm_scale, variant, static_cast<hipStream_t>(stream)));
+}
+
+int bwd_prep_any(const void* o, const void* dO, const float* delta_in, const void* state, size_t state_bytes,
+                 void* ws, size_t ws_bytes, int B, int S, int H, int Hkv, int D, float sm_scale, void* stream) {
+  if (!dO) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (bad_scale(sm_scale)) return MM1_E_SCALE;
+  if ((rc = check_state_ws(state, state_bytes, ws, ws_bytes, B, S, H, Hkv))) return rc;
+  if (!aligned16(dO) || (o && !aligned16(o))) return MM1_E_ALIGN;
+  const mm1::FwdState f = mm1::fwd_state(B, S, H, Hkv);
+  const char* st = static_cast<const char*>(state);
+  return from_hip(mm1::launch_bwd_prep(o, reinterpret_cast<const uint8_t*>(st + f.olo), dO, delta_in,
+                                       reinterpret_cast<const float*>(st + f.vmax), static_cast<char*>(ws), B, S,
+                                       H, Hkv, sm_scale, static_cast<hipStream_t>(stream)));
+}
+
+int bwd_dkdv(const float* lse2, const void* state, size_t state_bytes, void* dk, void* dv, bool f32, void* ws,
+             size_t ws_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale, int tiles,
+             void* stream) {
+  if (!lse2 || !dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (bad_scale(sm_scale)) return MM1_E_SCALE;
+  if ((rc = check_state_ws(state, state_bytes, ws, ws_bytes, B, S, H, Hkv))) return rc;
+  if (!aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
+  const int variant = pick_tiles(MM1_TILES_DKDV, tiles);
+  if (variant < 0) return MM1_E_TILES;
+  rc = from_hip(mm1::launch_bwd_dkdv(static_cast<const char*>(state), static_cast<char*>(ws), lse2, dk, dv, f32,
+                                     B, S, H, Hkv, causal != 0, sm_scale, variant,
+                                     static_cast<hipStream_t>(stream)));
+  if (rc == MM1_OK && H / Hkv > 1) record_layout(layout_of(ws, variant, B, S, H, Hkv, causal != 0));
+  return rc;
+}
+
+// dq, and with `reduce` the group sum of the dK/dV partials in the same launch.
+int bwd_dq(const float* lse2, const void* state, size_t state_bytes, void* dq, void* dk, void* dv, bool reduce,
+           bool f32, void* ws, size_t ws_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+           int tiles, int dkdv_tiles, void* stream) {
+  if (!lse2 || !dq) return MM1_E_NULL;
+  if (reduce && (!dk || !dv)) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (bad_scale(sm_scale)) return MM1_E_SCALE;
+  if ((rc = check_state_ws(state, state_bytes, ws, ws_bytes, B, S, H, Hkv))) return rc;
+  if (!aligned16(dq) || (reduce && (!aligned16(dk) || !aligned16(dv)))) return MM1_E_ALIGN;
+  const int variant = pick_tiles(MM1_TILES_DQ, tiles);
+  const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, dkdv_tiles);
+  if (variant < 0 || dkdv_variant < 0) return MM1_E_TILES;
+  if (reduce && H / Hkv > 1 && !layout_matches(layout_of(ws, dkdv_variant, B, S, H, Hkv, causal != 0)))
+    return MM1_E_LAYOUT;
+  return from_hip(mm1::launch_bwd_dq(static_cast<const char*>(state), static_cast<char*>(ws), lse2, dq, reduce,
+                                     dk, dv, f32, B, S, H, Hkv, causal != 0, sm_scale, variant, dkdv_variant,
+                                     static_cast<hipStream_t>(stream)));
+}
+
+int bwd_reduce(void* ws, size_t ws_bytes, void* dk, void* dv, int B, int S, int H, int Hkv, int D, int causal,
+               int dkdv_tiles, void* stream) {
+  if (!ws || !dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, dkdv_tiles);
+  if (dkdv_variant < 0) return MM1_E_TILES;
+  if (ws_bytes < mm1::bwd_ws(B, S, H, Hkv).bytes) return MM1_E_WORKSPACE;
+  if (!aligned16(ws) || !aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
+  if (H / Hkv <= 1) return MM1_OK;
+  if (!layout_matches(layout_of(ws, dkdv_variant, B, S, H, Hkv, causal != 0))) return MM1_E_LAYOUT;
+  return from_hip(mm1::launch_bwd_reduce(static_cast<const char*>(ws), dk, dv, false, B, S, H, Hkv, causal != 0,
+                                         dkdv_variant, static_cast<hipStream_t>(stream)));
+}
+
+// The whole backward: prep, dK/dV, dQ with the partial sum in its tail.
+int bwd_all(const void* o, const void* dO, const float* lse2, const void* state, size_t state_bytes, void* dq,
+            void* dk, void* dv, bool f32, void* ws, size_t ws_bytes, int B, int S, int H, int Hkv, int D,
+            int causal, float sm_scale, int dkdv_tiles, int dq_tiles, void* stream) {
+  // what only the later launches check is checked first, so that an
+  // argument error launches nothing
+  if (!o || !dO || !lse2 || !dq || !dk || !dv) return MM1_E_NULL;
+  int rc = check_shape(B, S, H, Hkv, D);
+  if (rc) return rc;
+  if (bad_scale(sm_scale)) return MM1_E_SCALE;
+  if ((rc = check_state_ws(state, state_bytes, ws, ws_bytes, B, S, H, Hkv))) return rc;
+  if (!aligned16(o) || !aligned16(dO) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
+  if (pick_tiles(MM1_TILES_DQ, dq_tiles) < 0 || pick_tiles(MM1_TILES_DKDV, dkdv_tiles) < 0) return MM1_E_TILES;
+  if ((rc = bwd_prep_any(o, dO, nullptr, state, state_bytes, ws, ws_bytes, B, S, H, Hkv, D, sm_scale, stream)))
+    return rc;
+  if ((rc = bwd_dkdv(lse2, state, state_bytes, dk, dv, f32, ws, ws_bytes, B, S, H, Hkv, D, causal, sm_scale,
+                     dkdv_tiles, stream)))
+    return rc;
+  return bwd_dq(lse2, state, state_bytes, dq, dk, dv, true, f32, ws, ws_bytes, B, S, H, Hkv, D, causal, sm_scale,
+                dq_tiles, dkdv_tiles, stream);
+}
+
 }  // namespace
 
 extern "C" {
 
 int mm1_attn_version(void) { return MM1_ATTN_VERSION; }
 
-int mm1_attn_fwd_tiles(const void* q, const void* k, const void* v, void* o, float* lse2,
-                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+size_t mm1_attn_fwd_state_size(int B, int S, int H, int Hkv, int D) {
+  if (check_shape(B, S, H, Hkv, D) != MM1_OK) return 0;
+  return mm1::fwd_state(B, S, H, Hkv).bytes;
+}
+
+int mm1_attn_fwd_tiles(const void* q, const void* k, const void* v, void* o, float* lse2, void* state,
+                       size_t state_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                        int tiles, void* stream) {
-  if (!q || !k || !v || !o || !lse2) return MM1_E_NULL;
-  int rc = check_shape(B, S, H, Hkv, D);
-  if (rc) return rc;
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MM1_E_ALIGN;
-  const int variant = pick_tiles(MM1_TILES_FWD, tiles);
-  if (variant < 0) return MM1_E_TILES;
-  return from_hip(mm1::launch_fwd(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale, variant,
-                                  static_cast<hipStream_t>(stream)));
+  return fwd_any(q, k, v, o, lse2, false, state, state_bytes, B, S, H, Hkv, D, causal, sm_scale, tiles, stream);
 }
 
-int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
-                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+int mm1_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse2, void* state,
+                 size_t state_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                  void* stream) {
-  return mm1_attn_fwd_tiles(q, k, v, o, lse2, B, S, H, Hkv, D, causal, sm_scale, -1, stream);
+  return fwd_any(q, k, v, o, lse2, false, state, state_bytes, B, S, H, Hkv, D, causal, sm_scale, -1, stream);
 }
 
-int mm1_attn_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2,
-                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream) {
-  if (!q || !k || !v || !o || !lse2) return MM1_E_NULL;
+int mm1_attn_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2, void* state,
+                     size_t state_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                     int tiles, void* stream) {
+  return fwd_any(q, k, v, o, lse2, true, state, state_bytes, B, S, H, Hkv, D, causal, sm_scale, tiles, stream);
+}
+
+int mm1_attn_prep(const void* q, const void* k, const void* v, void* state, size_t state_bytes,
+                  int B, int S, int H, int Hkv, int D, void* stream) {
+  if (!q || !k || !v || !state) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
   if (rc) return rc;
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MM1_E_ALIGN;
-  return from_hip(mm1::launch_fwd_f32(q, k, v, o, lse2, B, S, H, Hkv, causal != 0, sm_scale,
-                                      static_cast<hipStream_t>(stream)));
+  if (state_bytes < mm1::fwd_state(B, S, H, Hkv).bytes) return MM1_E_WORKSPACE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(state)) return MM1_E_ALIGN;
+  const mm1::FwdState f = mm1::fwd_state(B, S, H, Hkv);
+  char* st = static_cast<char*>(state);
+  const hipStream_t sm = static_cast<hipStream_t>(stream);
+  rc = from_hip(mm1::launch_cvt_kv(k, v, reinterpret_cast<_Float16*>(st + f.k16),
+                                   reinterpret_cast<_Float16*>(st + f.v16), nullptr,
+                                   reinterpret_cast<float*>(st + f.vmax), (long)B * S * Hkv * mm1::HD, sm));
+  if (rc) return rc;
+  return from_hip(mm1::launch_cvt16(q, reinterpret_cast<_Float16*>(st + f.q16), (long)B * S * H * mm1::HD, sm));
 }
 
 int mm1_attn_tile_count(int kind) { return tile_count(kind); }
@@ -261,202 +392,102 @@ int mm1_attn_delta(const void* o, const void* dO, float* delta, int B, int S, in
 
 size_t mm1_attn_bwd_workspace_size(int B, int S, int H, int Hkv, int D) {
   if (check_shape(B, S, H, Hkv, D) != MM1_OK) return 0;
-  return mm1::bwd_workspace_bytes(B, S, H, Hkv);
+  return mm1::bwd_ws(B, S, H, Hkv).bytes;
 }
 
-static int bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
-                    const float* lse2, const float* delta, void* dk, void* dv,
-                    void* workspace, size_t workspace_bytes,
-                    int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                    int tiles, void* stream) {
-  if (!q || !k || !v || !dO || !lse2 || !delta || !dk || !dv) return MM1_E_NULL;
-  int rc = check_shape(B, S, H, Hkv, D);
-  if (rc) return rc;
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
-  const size_t need = mm1::bwd_workspace_bytes(B, S, H, Hkv);
-  if (need > 0 && (!workspace || workspace_bytes < need)) return MM1_E_WORKSPACE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dk) ||
-      !aligned16(dv) || (need > 0 && !aligned16(workspace)))
-    return MM1_E_ALIGN;
-  const int variant = pick_tiles(MM1_TILES_DKDV, tiles);
-  if (variant < 0) return MM1_E_TILES;
-  rc = from_hip(mm1::launch_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, need > 0 ? workspace : nullptr,
-                                     B, S, H, Hkv, causal != 0, sm_scale, variant,
-                                     static_cast<hipStream_t>(stream)));
-  if (rc == MM1_OK && need > 0) record_layout(layout_of(workspace, variant, B, S, H, Hkv, causal != 0));
-  return rc;
+int mm1_attn_bwd_prep(const void* o, const void* dO, const void* state, size_t state_bytes, void* workspace,
+                      size_t workspace_bytes, int B, int S, int H, int Hkv, int D, float sm_scale, void* stream) {
+  if (!o) return MM1_E_NULL;
+  return bwd_prep_any(o, dO, nullptr, state, state_bytes, workspace, workspace_bytes, B, S, H, Hkv, D, sm_scale,
+                      stream);
 }
 
-// dq, and with dk/dv the group sum of the dK/dV partials in the same launch.
-static int bwd_dq(const void* q, const void* k, const void* v, const void* dO,
-                  const float* lse2, const float* delta, void* dq, void* dk, void* dv,
-                  const void* workspace, size_t workspace_bytes, bool reduce,
-                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                  int tiles, int dkdv_tiles, void* stream) {
-  if (!q || !k || !v || !dO || !lse2 || !delta || !dq) return MM1_E_NULL;
-  if (reduce && (!dk || !dv)) return MM1_E_NULL;
-  int rc = check_shape(B, S, H, Hkv, D);
-  if (rc) return rc;
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
-  const size_t need = reduce ? mm1::bwd_workspace_bytes(B, S, H, Hkv) : 0;
-  if (need > 0 && (!workspace || workspace_bytes < need)) return MM1_E_WORKSPACE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) ||
-      (reduce && (!aligned16(dk) || !aligned16(dv))) || (need > 0 && !aligned16(workspace)))
-    return MM1_E_ALIGN;
-  const int variant = pick_tiles(MM1_TILES_DQ, tiles);
-  const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, dkdv_tiles);
-  if (variant < 0 || dkdv_variant < 0) return MM1_E_TILES;
-  if (need > 0 && !layout_matches(layout_of(workspace, dkdv_variant, B, S, H, Hkv, causal != 0)))
-    return MM1_E_LAYOUT;
-  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, need > 0 ? workspace : nullptr,
-                                     reduce ? dk : nullptr, reduce ? dv : nullptr,
-                                     B, S, H, Hkv, causal != 0, sm_scale, variant, dkdv_variant,
-                                     static_cast<hipStream_t>(stream)));
+int mm1_attn_bwd_prep_delta(const void* dO, const float* delta, const void* state, size_t state_bytes,
+                            void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv, int D,
+                            float sm_scale, void* stream) {
+  if (!delta) return MM1_E_NULL;
+  return bwd_prep_any(nullptr, dO, delta, state, state_bytes, workspace, workspace_bytes, B, S, H, Hkv, D,
+                      sm_scale, stream);
 }
 
-static int bwd_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
-                      int B, int S, int H, int Hkv, int D, int causal, int dkdv_tiles, void* stream) {
-  if (!dk || !dv) return MM1_E_NULL;
-  int rc = check_shape(B, S, H, Hkv, D);
-  if (rc) return rc;
-  const int dkdv_variant = pick_tiles(MM1_TILES_DKDV, dkdv_tiles);
-  if (dkdv_variant < 0) return MM1_E_TILES;
-  const size_t need = mm1::bwd_workspace_bytes(B, S, H, Hkv);
-  if (need == 0) return MM1_OK;
-  if (!workspace || workspace_bytes < need) return MM1_E_WORKSPACE;
-  if (!aligned16(workspace) || !aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
-  if (!layout_matches(layout_of(workspace, dkdv_variant, B, S, H, Hkv, causal != 0))) return MM1_E_LAYOUT;
-  return from_hip(mm1::launch_bwd_reduce(workspace, dk, dv, B, S, H, Hkv, causal != 0, dkdv_variant,
-                                         static_cast<hipStream_t>(stream)));
+int mm1_attn_bwd_dkdv_tiles(const float* lse2, const void* state, size_t state_bytes, void* dk, void* dv,
+                            void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv, int D, int causal,
+                            float sm_scale, int dkdv_tiles, void* stream) {
+  return bwd_dkdv(lse2, state, state_bytes, dk, dv, false, workspace, workspace_bytes, B, S, H, Hkv, D, causal,
+                  sm_scale, dkdv_tiles, stream);
 }
 
-int mm1_attn_bwd_dkdv_tiles(const void* q, const void* k, const void* v, const void* dO,
-                            const float* lse2, const float* delta, void* dk, void* dv,
-                            void* workspace, size_t workspace_bytes,
-                            int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                            int dkdv_tiles, void* stream) {
-  return bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes, B, S, H, Hkv, D,
-                  causal, sm_scale, dkdv_tiles, stream);
-}
-
-int mm1_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dO,
-                      const float* lse2, const float* delta, void* dk, void* dv,
-                      void* workspace, size_t workspace_bytes,
-                      int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                      void* stream) {
-  return bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes, B, S, H, Hkv, D,
-                  causal, sm_scale, -1, stream);
-}
-
-int mm1_attn_bwd_dkdv_reduce_tiles(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
-                                   int B, int S, int H, int Hkv, int D, int causal, int dkdv_tiles,
-                                   void* stream) {
+int mm1_attn_bwd_dkdv_reduce_tiles(void* workspace, size_t workspace_bytes, void* dk, void* dv, int B, int S,
+                                   int H, int Hkv, int D, int causal, int dkdv_tiles, void* stream) {
   return bwd_reduce(workspace, workspace_bytes, dk, dv, B, S, H, Hkv, D, causal, dkdv_tiles, stream);
 }
 
-int mm1_attn_bwd_dkdv_reduce(const void* workspace, size_t workspace_bytes, void* dk, void* dv,
-                             int B, int S, int H, int Hkv, int D, int causal, void* stream) {
-  return bwd_reduce(workspace, workspace_bytes, dk, dv, B, S, H, Hkv, D, causal, -1, stream);
-}
-
-int mm1_attn_bwd_dq_tiles(const void* q, const void* k, const void* v, const void* dO,
-                          const float* lse2, const float* delta, void* dq,
-                          int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+int mm1_attn_bwd_dq_tiles(const float* lse2, const void* state, size_t state_bytes, void* dq, void* workspace,
+                          size_t workspace_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                           int dq_tiles, void* stream) {
-  return bwd_dq(q, k, v, dO, lse2, delta, dq, nullptr, nullptr, nullptr, 0, false, B, S, H, Hkv, D,
-                causal, sm_scale, dq_tiles, -1, stream);
+  return bwd_dq(lse2, state, state_bytes, dq, nullptr, nullptr, false, false, workspace, workspace_bytes, B, S, H,
+                Hkv, D, causal, sm_scale, dq_tiles, -1, stream);
 }
 
-int mm1_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dO,
-                    const float* lse2, const float* delta, void* dq,
-                    int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                    void* stream) {
-  return bwd_dq(q, k, v, dO, lse2, delta, dq, nullptr, nullptr, nullptr, 0, false, B, S, H, Hkv, D,
-                causal, sm_scale, -1, -1, stream);
+int mm1_attn_bwd_dq_reduce_tiles(const float* lse2, const void* state, size_t state_bytes, void* dq, void* dk,
+                                 void* dv, void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv,
+                                 int D, int causal, float sm_scale, int dkdv_tiles, int dq_tiles, void* stream) {
+  return bwd_dq(lse2, state, state_bytes, dq, dk, dv, true, false, workspace, workspace_bytes, B, S, H, Hkv, D,
+                causal, sm_scale, dq_tiles, dkdv_tiles, stream);
 }
 
-int mm1_attn_bwd_dq_reduce_tiles(const void* q, const void* k, const void* v, const void* dO,
-                                 const float* lse2, const float* delta, void* dq, void* dk, void* dv,
-                                 const void* workspace, size_t workspace_bytes,
-                                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                                 int dkdv_tiles, int dq_tiles, void* stream) {
-  return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
-                D, causal, sm_scale, dq_tiles, dkdv_tiles, stream);
+int mm1_attn_bwd_tiles(const void* o, const void* dO, const float* lse2, const void* state, size_t state_bytes,
+                       void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, int B, int S, int H,
+                       int Hkv, int D, int causal, float sm_scale, int dkdv_tiles, int dq_tiles, void* stream) {
+  return bwd_all(o, dO, lse2, state, state_bytes, dq, dk, dv, false, workspace, workspace_bytes, B, S, H, Hkv, D,
+                 causal, sm_scale, dkdv_tiles, dq_tiles, stream);
 }
 
-int mm1_attn_bwd_dq_reduce(const void* q, const void* k, const void* v, const void* dO,
-                           const float* lse2, const float* delta, void* dq, void* dk, void* dv,
-                           const void* workspace, size_t workspace_bytes,
-                           int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+int mm1_attn_bwd(const void* o, const void* dO, const float* lse2, const void* state, size_t state_bytes, void* dq,
+                 void* dk, void* dv, void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv, int D,
+                 int causal, float sm_scale, void* stream) {
+  return bwd_all(o, dO, lse2, state, state_bytes, dq, dk, dv, false, workspace, workspace_bytes, B, S, H, Hkv, D,
+                 causal, sm_scale, -1, -1, stream);
+}
+
+int mm1_attn_bwd_f32_tiles(const void* o, const void* dO, const float* lse2, const void* state, size_t state_bytes,
+                           float* dq, float* dk, float* dv, void* workspace, size_t workspace_bytes, int B, int S,
+                           int H, int Hkv, int D, int causal, float sm_scale, int dkdv_tiles, int dq_tiles,
                            void* stream) {
-  return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
-                D, causal, sm_scale, -1, -1, stream);
+  return bwd_all(o, dO, lse2, state, state_bytes, dq, dk, dv, true, workspace, workspace_bytes, B, S, H, Hkv, D,
+                 causal, sm_scale, dkdv_tiles, dq_tiles, stream);
 }
 
-int mm1_attn_bwd_tiles(const void* q, const void* k, const void* v, const void* dO,
-                       const float* lse2, const float* delta,
-                       void* dq, void* dk, void* dv,
-                       void* workspace, size_t workspace_bytes,
-                       int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                       int dkdv_tiles, int dq_tiles, void* stream) {
-  // What only the second launch checks is checked here, so that an argument
-  // error launches nothing.
-  if (!dq) return MM1_E_NULL;
-  if (!aligned16(dq)) return MM1_E_ALIGN;
-  if (pick_tiles(MM1_TILES_DQ, dq_tiles) < 0 || pick_tiles(MM1_TILES_DKDV, dkdv_tiles) < 0) return MM1_E_TILES;
-  int rc = bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, workspace, workspace_bytes, B, S, H, Hkv, D,
-                    causal, sm_scale, dkdv_tiles, stream);
-  if (rc) return rc;
-  return bwd_dq(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes, true, B, S, H, Hkv,
-                D, causal, sm_scale, dq_tiles, dkdv_tiles, stream);
-}
-
-int mm1_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* dO,
-                         const float* lse2, const float* delta, void* dq, void* dk, void* dv,
-                         int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream) {
-  if (!q || !k || !v || !dO || !lse2 || !delta || !dq || !dk || !dv) return MM1_E_NULL;
+int mm1_attn_bwd_noalloc(const void* o, const void* dO, const float* lse2, const void* state, size_t state_bytes,
+                         void* dq, void* dk, void* dv, int B, int S, int H, int Hkv, int D, int causal,
+                         float sm_scale, void* stream) {
+  if (!o || !dO || !lse2 || !state || !dq || !dk || !dv) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
   if (rc) return rc;
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) || !aligned16(dk) ||
-      !aligned16(dv))
+  if (bad_scale(sm_scale)) return MM1_E_SCALE;
+  if (state_bytes < mm1::fwd_state(B, S, H, Hkv).bytes) return MM1_E_WORKSPACE;
+  if (!aligned16(o) || !aligned16(dO) || !aligned16(state) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
     return MM1_E_ALIGN;
-  const size_t need = mm1::bwd_partials_bytes(B, S, H, Hkv, causal != 0, 0);
+  const size_t need = ws_bytes_for(B, S, H, Hkv, causal != 0, 0);
   if (need > MM1_NOALLOC_SCRATCH_BYTES) return MM1_E_SCRATCH;
   void* ws = nullptr;
-  if (need > 0 && (rc = scratch_addr(&ws)) != MM1_OK) return rc;
+  if ((rc = scratch_addr(&ws)) != MM1_OK) return rc;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = from_hip(mm1::launch_bwd_dkdv(q, k, v, dO, lse2, delta, dk, dv, ws, B, S, H, Hkv, causal != 0, sm_scale,
-                                     0, st));
+  const mm1::FwdState f = mm1::fwd_state(B, S, H, Hkv);
+  const char* sp = static_cast<const char*>(state);
+  char* wp = static_cast<char*>(ws);
+  rc = from_hip(mm1::launch_bwd_prep(o, reinterpret_cast<const uint8_t*>(sp + f.olo), dO, nullptr,
+                                     reinterpret_cast<const float*>(sp + f.vmax), wp, B, S, H, Hkv, sm_scale, st));
   if (rc) return rc;
-  return from_hip(mm1::launch_bwd_dq(q, k, v, dO, lse2, delta, dq, ws, dk, dv, B, S, H, Hkv, causal != 0,
-                                     sm_scale, 0, 0, st));
+  rc = from_hip(mm1::launch_bwd_dkdv(sp, wp, lse2, dk, dv, false, B, S, H, Hkv, causal != 0, sm_scale, 0, st));
+  if (rc) return rc;
+  return from_hip(mm1::launch_bwd_dq(sp, wp, lse2, dq, true, dk, dv, false, B, S, H, Hkv, causal != 0, sm_scale, 0,
+                                     0, st));
 }
 
 size_t mm1_attn_bwd_noalloc_scratch_size(int B, int S, int H, int Hkv, int D, int causal) {
   if (check_shape(B, S, H, Hkv, D) != MM1_OK) return 0;
-  return mm1::bwd_partials_bytes(B, S, H, Hkv, causal != 0, 0);
-}
-
-size_t mm1_attn_bwd_f32_workspace_size(int B, int S, int H, int Hkv, int D) {
-  if (check_shape(B, S, H, Hkv, D) != MM1_OK) return 0;
-  return mm1::bwd_f32_workspace_bytes(B, S, H, Hkv);
-}
-
-int mm1_attn_bwd_f32(const void* q, const void* k, const void* v, const void* dO,
-                     const float* lse2, const float* delta, float* dq, float* dk, float* dv,
-                     void* workspace, size_t workspace_bytes,
-                     int B, int S, int H, int Hkv, int D, int causal, float sm_scale, void* stream) {
-  if (!q || !k || !v || !dO || !lse2 || !delta || !dq || !dk || !dv) return MM1_E_NULL;
-  int rc = check_shape(B, S, H, Hkv, D);
-  if (rc) return rc;
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return MM1_E_SCALE;
-  if (!workspace || workspace_bytes < mm1::bwd_f32_workspace_bytes(B, S, H, Hkv)) return MM1_E_WORKSPACE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) || !aligned16(dk) ||
-      !aligned16(dv) || !aligned16(workspace))
-    return MM1_E_ALIGN;
-  return from_hip(mm1::launch_bwd_f32(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, B, S, H, Hkv,
-                                      causal != 0, sm_scale, static_cast<hipStream_t>(stream)));
+  return ws_bytes_for(B, S, H, Hkv, causal != 0, 0);
 }
 
 int mm1_attn_dispatch_order(int kind, int tiles, int B, int S, int H, int Hkv, int causal, int cus,
@@ -487,16 +518,6 @@ int mm1_attn_dkdv_plan(int B, int S, int H, int Hkv, int causal, int cus, int* o
   out[3] = plan.n_items;
   out[4] = plan.order.n;
   return MM1_OK;
-}
-
-int mm1_attn_bwd(const void* q, const void* k, const void* v, const void* dO,
-                 const float* lse2, const float* delta,
-                 void* dq, void* dk, void* dv,
-                 void* workspace, size_t workspace_bytes,
-                 int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                 void* stream) {
-  return mm1_attn_bwd_tiles(q, k, v, dO, lse2, delta, dq, dk, dv, workspace, workspace_bytes,
-                            B, S, H, Hkv, D, causal, sm_scale, -1, -1, stream);
 }
 
 static int check_qknorm(int B, int S, int H, int Hkv, int D, int rot_len, float eps, bool norm) {

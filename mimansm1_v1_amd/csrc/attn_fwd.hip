@@ -19,23 +19,149 @@
 //     per key tile; no staging registers.
 //   * The running max is only moved (and O, l rescaled) when a row's max
 //     grows by more than 2^8 (log2 units); otherwise P = exp2(s - m_old) <= 256
-//     stays exact in fp32 and bf16, and the final normalisation uses the same
-//     frame, so the result is unchanged.
+//     stays exact in fp32 and within fp16's range, and the final
+//     normalisation uses the same frame, so the result is unchanged.
+//   * Operands are fp16: K and V come as fp16 copies (attn_cvt16_kernel, in
+//     the forward state), Q is converted in registers, and P is rounded to
+//     fp16 (11 significant bits) before O^T += V^T P^T.  The reference rounds
+//     P to bf16 there (AT:178-180); the finer rounding keeps O, and the
+//     backward's Delta = rowsum(O dO), within the stated tolerance of the
+//     fp32 math also for peaky softmax rows.
+//   * For the backward the forward also leaves, in the state, the fp16 copy
+//     of Q and one byte per value of O (o_lo: the 8 fp32 mantissa bits after
+//     the bf16 truncation, lo8_bits): Delta is then computed from 15
+//     significant bits of O instead of the 8 of the bf16 output.
 #include <type_traits>
 
 #include "dispatch_order.h"
+#include "attn_layout.h"
 #include "mm1_common.h"
 
 namespace mm1 {
 
 constexpr float kRescaleThreshold = 8.0f;   // log2 units
 
+// ---------------------------------------------------------------------------
+// bf16 -> fp16 copies of K and V (blockIdx.y = tensor), with the largest |x|
+// of each workgroup's share in part_max[y][blockIdx.x] (the backward sizes
+// the scale of dO from max|V|).  8 values per thread per step, grid-stride.
+struct Cvt16 {
+  const __bf16* src[2];
+  _Float16* dst[2];
+  float* part_max[2];   // nullptr: no maxima
+  long n[2];            // elements, a multiple of 8
+};
+
+__global__ __launch_bounds__(256) void attn_cvt16_kernel(const Cvt16 c) {
+  const int y = blockIdx.y;
+  const __bf16* src = c.src[y];
+  _Float16* dst = c.dst[y];
+  const long n8 = c.n[y] / 8;
+  float mx = 0.f;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n8; i += (long)gridDim.x * 256) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(src + 8 * i);
+    f16x8 r;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float f = (float)x[t];
+      mx = fmaxf(mx, fabsf(f));
+      r[t] = (_Float16)f;
+    }
+    *reinterpret_cast<f16x8*>(dst + 8 * i) = r;
+  }
+  if (!c.part_max[y]) return;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  __shared__ float wmax[4];
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    c.part_max[y][blockIdx.x] = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+}
+
+// Query operands of a wave (B of S^T = K Q^T): row rr of the packed row
+// space, the 64 values 16*ks + 8*h .. +7 (ks = 0..7) of it, converted to
+// fp16; with q16 != nullptr also stored there (the backward's copy of Q).
+__device__ __forceinline__ void load_q16(f16x8 (&qreg)[8], const __bf16* q, _Float16* q16, long roff,
+                                         bool valid, int h) {
+  if (valid) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      qreg[ks] = bf16_to_f16(*reinterpret_cast<const bf16x8*>(q + roff + 16 * ks + 8 * h));
+    if (q16) {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) *reinterpret_cast<f16x8*>(q16 + roff + 16 * ks + 8 * h) = qreg[ks];
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) pin(qreg[ks]);
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) qreg[ks][t] = (_Float16)0.f;
+    }
+  }
+}
+
+// The outputs of a wave's 32 rows: bf16 O through LDS (store_tile_bf16, with
+// the residual bytes to o_lo when o_lo != nullptr), or fp32 O written
+// directly (F32OUT: the values the bf16 output rounds; o_lo then holds their
+// residual bytes as well); lse2 in both cases.
+template <bool F32OUT>
+__device__ __forceinline__ void store_fwd_rows(const f32x16 (&oacc)[4], float m_run, float l_run, float scale2,
+                                               void* o_out, uint8_t* o_lo, float* lse2, char* lds, int lane,
+                                               int b, int g, int S, int H, int G, int R, int rw0) {
+  const int h = lane >> 5, l32 = lane & 31;
+  const float l_tot = xhalf_sum(l_run);
+  const float inv = 1.f / l_tot;
+  const int rr = rw0 + l32;
+  const int qpos = rr / G, hq = rr - qpos * G;
+  if (rr < R && h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
+  auto row_of = [&](int i) -> long {
+    const int r = rw0 + i;
+    if (r >= R) return -1;
+    const int p = r / G;
+    return ((long)(b * S + p) * H + g * G + (r - p * G)) * HD;
+  };
+  if constexpr (!F32OUT) {
+    auto dst = [&](int i) -> __bf16* {
+      const long off = row_of(i);
+      return off < 0 ? nullptr : static_cast<__bf16*>(o_out) + off;
+    };
+    if (o_lo) {
+      store_tile_bf16_lo(oacc, inv, lds, lane, dst, [&](int i) -> uint8_t* {
+        const long off = row_of(i);
+        return off < 0 ? nullptr : o_lo + off;
+      });
+    } else {
+      store_tile_bf16(oacc, inv, lds, lane, dst);
+    }
+  } else if (rr < R) {
+    const long row = row_of(l32);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        f32x4 val;
+        uint32_t lo = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          val[c] = oacc[db][4 * a4 + c] * inv;
+          lo |= lo8_bits(val[c]) << (8 * c);
+        }
+        *reinterpret_cast<f32x4*>(static_cast<float*>(o_out) + row + 32 * db + 8 * a4 + 4 * h) = val;
+        if (o_lo) *reinterpret_cast<uint32_t*>(o_lo + row + 32 * db + 8 * a4 + 4 * h) = lo;
+      }
+    }
+  }
+}
+
 // NW waves x 32 packed query rows per workgroup; NSTAGE-deep K/V ring.
 // F32OUT: O is written in fp32 (the values the bf16 output rounds).
 template <int NW, int NSTAGE, bool CAUSAL, bool F32OUT = false>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    void* __restrict__ o_out, float* __restrict__ lse2,
+    const __bf16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
+    void* __restrict__ o_out, float* __restrict__ lse2, _Float16* __restrict__ q16, uint8_t* __restrict__ o_lo,
     int B, int S, int H, int Hkv, int G, float scale2, int n_tiles, const DispatchOrder ord) {
   constexpr int BM = NW * 32;     // packed rows per workgroup
   constexpr int BN = TILE_ROWS;   // keys per iteration
@@ -64,8 +190,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   const int pw_hi = wave_active ? min(S - 1, (min(rw0 + 32, R) - 1) / G) : -1;
 
   const long kvstride = (long)Hkv * HD;
-  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
-  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
+  const _Float16* kbase = k + ((long)b * S * Hkv + g) * HD;
+  const _Float16* vbase = v + ((long)b * S * Hkv + g) * HD;
   const uint32_t dma_off = tile_lane_off(kvstride, tid);
   auto issue_tile = [&](char* buf, int kt) {
     const int nk = kt * BN;
@@ -77,23 +203,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
     if (st < n_kt) issue_tile(smem + st * BUF, st);
 
   // Query operands (B of S^T = K Q^T), loaded once.
-  bf16x8 qreg[8];
+  f16x8 qreg[8];
   const int rr = rw0 + l32;
   const int qpos = rr / G;
   const int hq = rr - qpos * G;
-  if (rr < R) {
-    const __bf16* src = q + ((long)(b * S + qpos) * H + g * G + hq) * HD + 8 * h;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) pin(qreg[ks]);
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) qreg[ks][t] = (__bf16)0.f;
-    }
-  }
+  load_q16(qreg, q, q16, ((long)(b * S + qpos) * H + g * G + hq) * HD, rr < R, h);
 
   f32x16 oacc[4];
 #pragma unroll
@@ -160,9 +274,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
       l_run += sum;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 pb = pack8(sacc[ks >> 1], 8 * (ks & 1));
+        const f16x8 pb = pack8(sacc[ks >> 1], 8 * (ks & 1));
 #pragma unroll
-        for (int db = 0; db < 4; ++db) oacc[db] = mfma32(tr_a(vl, lb, db, ks), pb, oacc[db]);
+        for (int db = 0; db < 4; ++db) oacc[db] = mfma32h(tr_a(vl, lb, db, ks), pb, oacc[db]);
       }
     }
     // tile kt+1 must have landed; the newer prefetches stay in flight
@@ -182,41 +296,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   }
 
   if (!wave_active) return;
-  const float l_tot = xhalf_sum(l_run);
-  const float inv = 1.f / l_tot;
-  if constexpr (!F32OUT) {
-    // every slot is free after the last step's barrier: each wave's rows go
-    // out through 8 KiB of it (store_tile_bf16)
-    if (rr < R && h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
-    store_tile_bf16(oacc, inv, smem + w * 8192, lane, [&](int i) -> __bf16* {
-      const int r = rw0 + i;
-      if (r >= R) return nullptr;
-      const int p = r / G;
-      return static_cast<__bf16*>(o_out) + ((long)(b * S + p) * H + g * G + (r - p * G)) * HD;
-    });
-    return;
-  }
-  if (rr < R) {
-    const long row = ((long)(b * S + qpos) * H + g * G + hq) * HD;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        if constexpr (F32OUT) {
-          f32x4 val;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) val[c] = oacc[db][4 * a4 + c] * inv;
-          *reinterpret_cast<f32x4*>(static_cast<float*>(o_out) + row + 32 * db + 8 * a4 + 4 * h) = val;
-        } else {
-          bf16x4 val;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) val[c] = (__bf16)(oacc[db][4 * a4 + c] * inv);
-          *reinterpret_cast<bf16x4*>(static_cast<__bf16*>(o_out) + row + 32 * db + 8 * a4 + 4 * h) = val;
-        }
-      }
-    }
-    if (h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
-  }
+  // every slot is free after the last step's barrier: each wave's rows go
+  // out through 8 KiB of it
+  store_fwd_rows<F32OUT>(oacc, m_run, l_run, scale2, o_out, o_lo, lse2, smem + w * 8192, lane, b, g, S, H, G,
+                         R, rw0);
 }
 
 // Ping-pong forward: one workgroup of 8 waves per CU over 256 packed query
@@ -235,10 +318,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
 // for each: the group running part 2 issues the copies of the phase (B
 // refills K(t+2) in phase 2t+2, A refills V(t+2) in phase 2t+3) and waits for
 // them at the end of the next phase, two phases ahead of their first use.
-template <bool CAUSAL>
+template <bool CAUSAL, bool F32OUT = false>
 __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
-    __bf16* __restrict__ o, float* __restrict__ lse2,
+    const __bf16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
+    void* __restrict__ o, float* __restrict__ lse2, _Float16* __restrict__ q16, uint8_t* __restrict__ o_lo,
     int B, int S, int H, int Hkv, int G, float scale2, int n_tiles, const DispatchOrder ord) {
   constexpr int BM = 256;         // packed rows per workgroup
   constexpr int BN = TILE_ROWS;   // keys per tile
@@ -264,18 +347,18 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   const int pw_lo = rw0 / G;
 
   const long kvstride = (long)Hkv * HD;
-  const __bf16* kbase = k + ((long)b * S * Hkv + g) * HD;
-  const __bf16* vbase = v + ((long)b * S * Hkv + g) * HD;
+  const _Float16* kbase = k + ((long)b * S * Hkv + g) * HD;
+  const _Float16* vbase = v + ((long)b * S * Hkv + g) * HD;
   const uint32_t dma_off = tile_lane_off(kvstride, tid);
   auto kslot = [&](int j) { return smem + j * TILE_BYTES; };
   auto vslot = [&](int j) { return smem + (2 + j) * TILE_BYTES; };
   // all 8 waves (prologue) or the 4 waves of one group (in the loop; the
   // quad a wave copies depends on w & 3 only, as tile_dma<4> requires)
-  auto copy8 = [&](char* dst, const __bf16* base, int kt) {
+  auto copy8 = [&](char* dst, const _Float16* base, int kt) {
     const int nk = kt * BN;
     tile_dma<8>(dst, base + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
   };
-  auto copy4 = [&](char* dst, const __bf16* base, int kt) {
+  auto copy4 = [&](char* dst, const _Float16* base, int kt) {
     const int nk = kt * BN;
     tile_dma<4>(dst, base + (long)nk * kvstride, kvstride, S - nk, dma_off, tid & 255);
   };
@@ -287,29 +370,17 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   }
 
   // Query operands (B of S^T = K Q^T), loaded once.
-  bf16x8 qreg[8];
+  f16x8 qreg[8];
   const int rr = rw0 + l32;
   const int qpos = rr / G;
   const int hq = rr - qpos * G;
-  if (rr < R) {
-    const __bf16* src = q + ((long)(b * S + qpos) * H + g * G + hq) * HD + 8 * h;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const bf16x8*>(src + 16 * ks);
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) pin(qreg[ks]);
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) qreg[ks][t] = (__bf16)0.f;
-    }
-  }
+  load_q16(qreg, q, q16, ((long)(b * S + qpos) * H + g * G + hq) * HD, rr < R, h);
 
   f32x16 oacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) oacc[db] = zero16();
   float m_run = -INFINITY, l_run = 0.f;
-  bf16x8 pb[4];   // P(t) of part 1, the B operand of part 2
+  f16x8 pb[4];    // P(t) of part 1, the B operand of part 2
   const LdsBases lb = make_lds_bases(lane);
   wait_dma();
   __syncthreads();
@@ -370,7 +441,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-      for (int db = 0; db < 4; ++db) oacc[db] = mfma32(tr_a(vl, lb, db, ks), pb[ks], oacc[db]);
+      for (int db = 0; db < 4; ++db) oacc[db] = mfma32h(tr_a(vl, lb, db, ks), pb[ks], oacc[db]);
     }
   };
 
@@ -417,15 +488,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   // barrier.
   auto store_rows = [&](char* region) {
     if (!wave_active) return;
-    const float l_tot = xhalf_sum(l_run);
-    const float inv = 1.f / l_tot;
-    if (rr < R && h == 0) lse2[((long)b * H + g * G + hq) * S + qpos] = m_run * scale2 + log2f(l_tot);
-    store_tile_bf16(oacc, inv, region + (w & 3) * 8192, lane, [&](int i) -> __bf16* {
-      const int r = rw0 + i;
-      if (r >= R) return nullptr;
-      const int p = r / G;
-      return o + ((long)(b * S + p) * H + g * G + (r - p * G)) * HD;
-    });
+    store_fwd_rows<F32OUT>(oacc, m_run, l_run, scale2, o, o_lo, lse2, region + (w & 3) * 8192, lane, b, g, S,
+                           H, G, R, rw0);
   };
   if (grp == 0) {
     store_rows(kslot(0));
@@ -436,57 +500,88 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   }
 }
 
-template <int NW, int NSTAGE, bool F32OUT = false>
-static void launch_fwd_t(const __bf16* q, const __bf16* k, const __bf16* v, void* o, float* lse2,
-                         int B, int S, int H, int Hkv, bool causal, float scale2, const DispatchOrder& ord,
-                         hipStream_t stream) {
+// K, V -> k16, v16 (with max|V| partials in vmax when it is not null).
+hipError_t launch_cvt_kv(const void* k, const void* v, _Float16* k16, _Float16* v16, float* kmax, float* vmax,
+                         long n, hipStream_t stream) {
+  Cvt16 c{};
+  c.src[0] = static_cast<const __bf16*>(k);
+  c.src[1] = static_cast<const __bf16*>(v);
+  c.dst[0] = k16;
+  c.dst[1] = v16;
+  c.part_max[0] = kmax;
+  c.part_max[1] = vmax;
+  c.n[0] = c.n[1] = n;
+  hipLaunchKernelGGL(attn_cvt16_kernel, dim3(kCvtBlocks, 2), dim3(256), 0, stream, c);
+  return hipGetLastError();
+}
+
+// One bf16 tensor -> fp16 (Q of a backward without a forward state).
+hipError_t launch_cvt16(const void* x, _Float16* x16, long n, hipStream_t stream) {
+  Cvt16 c{};
+  c.src[0] = static_cast<const __bf16*>(x);
+  c.dst[0] = x16;
+  c.n[0] = n;
+  hipLaunchKernelGGL(attn_cvt16_kernel, dim3(kCvtBlocks, 1), dim3(256), 0, stream, c);
+  return hipGetLastError();
+}
+
+template <int NW, int NSTAGE, bool F32OUT>
+static void launch_fwd_t(const __bf16* q, const _Float16* k, const _Float16* v, void* o, float* lse2,
+                         _Float16* q16, uint8_t* o_lo, int B, int S, int H, int Hkv, bool causal, float scale2,
+                         const DispatchOrder& ord, hipStream_t stream) {
   const int G = H / Hkv;
   const int BM = NW * 32;
   const int n_tiles = (G * S + BM - 1) / BM;
   dim3 grid(ord.n ? ord.n : n_tiles * B * Hkv), block(NW * 64);
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, true, F32OUT>), grid, block, 0, stream, q, k, v, o, lse2, B, S,
-                       H, Hkv, G, scale2, n_tiles, ord);
+    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, true, F32OUT>), grid, block, 0, stream, q, k, v, o, lse2, q16,
+                       o_lo, B, S, H, Hkv, G, scale2, n_tiles, ord);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, false, F32OUT>), grid, block, 0, stream, q, k, v, o, lse2, B, S,
-                       H, Hkv, G, scale2, n_tiles, ord);
+    hipLaunchKernelGGL((attn_fwd_kernel<NW, NSTAGE, false, F32OUT>), grid, block, 0, stream, q, k, v, o, lse2,
+                       q16, o_lo, B, S, H, Hkv, G, scale2, n_tiles, ord);
 }
 
-// The forward with fp32 O (the 4-wave ring tiling): the values a bf16
-// forward rounds, for parity checks of O where one bf16 half-ulp of |O|
-// already exceeds the tolerance.
-hipError_t launch_fwd_f32(const void* q, const void* k, const void* v, float* o, float* lse2,
-                          int B, int S, int H, int Hkv, bool causal, float sm_scale, hipStream_t stream) {
-  const float scale2 = sm_scale * 1.4426950408889634f;
-  launch_fwd_t<4, 2, true>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
-                           static_cast<const __bf16*>(v), o, lse2, B, S, H, Hkv, causal, scale2,
-                           dispatch_order(row_block_grid(1, B, S, H, Hkv), causal), stream);
-  return hipGetLastError();
-}
-
-// variant: 0 = attn_fwd_pp_kernel (8 waves, two groups half a tile apart),
-//          1 = 4 waves x 2-stage ring (two workgroups per CU),
-//          2 = 8 waves x 3-stage ring (one workgroup per CU).
-hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2,
-                      int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
-                      hipStream_t stream) {
-  const float scale2 = sm_scale * 1.4426950408889634f;
-  auto qp = static_cast<const __bf16*>(q);
-  auto kp = static_cast<const __bf16*>(k);
-  auto vp = static_cast<const __bf16*>(v);
+template <bool F32OUT>
+static void launch_fwd_v(const __bf16* qp, const _Float16* kp, const _Float16* vp, void* o, float* lse2,
+                         _Float16* q16, uint8_t* o_lo, int B, int S, int H, int Hkv, bool causal, float scale2,
+                         int variant, hipStream_t stream) {
   const DispatchOrder& ord = dispatch_order(row_block_grid(variant, B, S, H, Hkv), causal);
   if (variant == 0) {
     const int G = H / Hkv;
     const int n_tiles = (G * S + 255) / 256;
     dim3 grid(ord.n ? ord.n : n_tiles * B * Hkv), block(512);
     if (causal)
-      hipLaunchKernelGGL(attn_fwd_pp_kernel<true>, grid, block, 0, stream, qp, kp, vp, static_cast<__bf16*>(o), lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
+      hipLaunchKernelGGL((attn_fwd_pp_kernel<true, F32OUT>), grid, block, 0, stream, qp, kp, vp, o, lse2, q16, o_lo,
+                         B, S, H, Hkv, G, scale2, n_tiles, ord);
     else
-      hipLaunchKernelGGL(attn_fwd_pp_kernel<false>, grid, block, 0, stream, qp, kp, vp, static_cast<__bf16*>(o), lse2, B, S, H, Hkv, G, scale2, n_tiles, ord);
-  } else if (variant == 2)
-    launch_fwd_t<8, 3>(qp, kp, vp, o, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
+      hipLaunchKernelGGL((attn_fwd_pp_kernel<false, F32OUT>), grid, block, 0, stream, qp, kp, vp, o, lse2, q16,
+                         o_lo, B, S, H, Hkv, G, scale2, n_tiles, ord);
+  } else if (variant == 2) {
+    launch_fwd_t<8, 3, F32OUT>(qp, kp, vp, o, lse2, q16, o_lo, B, S, H, Hkv, causal, scale2, ord, stream);
+  } else {
+    launch_fwd_t<4, 2, F32OUT>(qp, kp, vp, o, lse2, q16, o_lo, B, S, H, Hkv, causal, scale2, ord, stream);
+  }
+}
+
+// The forward over a state (mm1_attn_fwd_state_size): K and V are converted
+// into it first; the kernels then read k16 / v16 and, with `save`, write q16
+// and o_lo for the backward.  F32 (o is float*): fp32 O, same kernels.
+// variant: 0 = attn_fwd_pp_kernel (8 waves, two groups half a tile apart),
+//          1 = 4 waves x 2-stage ring (two workgroups per CU),
+//          2 = 8 waves x 3-stage ring (one workgroup per CU).
+hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o, float* lse2, bool f32,
+                      _Float16* q16, _Float16* k16, _Float16* v16, uint8_t* o_lo, float* vmax, bool save,
+                      int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant, hipStream_t stream) {
+  const float scale2 = sm_scale * 1.4426950408889634f;
+  hipError_t e = launch_cvt_kv(k, v, k16, v16, nullptr, vmax, (long)B * S * Hkv * HD, stream);
+  if (e != hipSuccess) return e;
+  auto qp = static_cast<const __bf16*>(q);
+  if (f32)
+    launch_fwd_v<true>(qp, k16, v16, o, lse2, save ? q16 : nullptr, save ? o_lo : nullptr, B, S, H, Hkv, causal,
+                       scale2, variant, stream);
   else
-    launch_fwd_t<4, 2>(qp, kp, vp, o, lse2, B, S, H, Hkv, causal, scale2, ord, stream);
+    launch_fwd_v<false>(qp, k16, v16, o, lse2, save ? q16 : nullptr, save ? o_lo : nullptr, B, S, H, Hkv, causal,
+                        scale2, variant, stream);
   return hipGetLastError();
 }
 

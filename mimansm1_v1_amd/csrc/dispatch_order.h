@@ -102,9 +102,8 @@ __host__ __device__ inline int dkdv_chunks(int len, int L, int C) {
 }
 
 // dK/dV tilings (mm1_attn_tile_desc order) that run the grouped grid and so
-// leave the chunked partial-sum layout: 0 (8 waves x 32 keys), 3 (4 waves x
-// 64 keys) and 5 (quads of single-product waves).
-__host__ __device__ inline bool dkdv_grouped(int variant) { return variant == 0 || variant == 3 || variant == 5; }
+// leave the chunked partial-sum layout: 0 (the per-head tiling is 1).
+__host__ __device__ inline bool dkdv_grouped(int variant) { return variant == 0; }
 
 // Partial-sum slots of a dK/dV tiling in the backward workspace.
 struct WsSlots {

@@ -2,11 +2,19 @@
 //
 // Tensor layouts (all contiguous, matching the reference's BSHD convention,
 // CODE/mimans/model/attention_tilelang.py:119-124 and :253-261):
-//   Q, O, dO, dQ : [B, S, H,   128] bf16
-//   K, V, dK, dV : [B, S, Hkv, 128] bf16
+//   Q, O, dO, dQ : [B, S, H,   128] bf16 at the interface
+//   K, V, dK, dV : [B, S, Hkv, 128] bf16 at the interface
 //   lse2, delta  : [B, H, S]        fp32   (lse2 in log2 units, :186-188)
 //
-// Matrix-core convention (v_mfma_f32_32x32x16_bf16, wave64):
+// Operand precision.  The attention products run on fp16 operands
+// (v_mfma_f32_32x32x16_f16, the same rate as the bf16 form on gfx950):
+// Q, K, V and dO are converted once to fp16 copies (exact for bf16 values in
+// [2^-17, 65504]; dO is first scaled by a power of two), and the rounded
+// intermediates P (softmax weights) and dS are fp16, with 11 significant bits
+// against bf16's 8.  The GEMMs of the SwiGLU / head kernels keep bf16
+// operands (bf16x8, mfma32).
+//
+// Matrix-core convention (32x32x16 MFMA, wave64):
 //   A operand (32 x 16): lane l holds row (l & 31), eight k values;
 //   B operand (16 x 32): lane l holds column (l & 31), eight k values;
 //   the k values a lane holds are the same set for A and B, so any fixed
@@ -17,13 +25,13 @@
 // k-step s with row 16*s + 8*(t/4) + 4*(l/32) + (t%4): the "pi" order.  A
 // operands that meet such a B operand are read in the same pi order.
 //
-// LDS tiles are 64 rows x 128 bf16 (256 B per row, 16 KiB), row-major, with
-// the sixteen 16-byte chunks of row r permuted by chunk ^ swz(r).  They are
-// filled straight from global memory by the LDS DMA path
-// (global_load_lds_dwordx4: lane L of a wave lands at base + 16*L), and read
-// either row-wise (ds_read_b128: a row of 8 k values per lane) or transposed
-// (two ds_read_b64_tr_b16: a column of 8 rows per lane).  swz() is chosen so
-// that both read patterns touch each bank once per 16-lane phase:
+// LDS tiles are 64 rows x 128 16-bit values (256 B per row, 16 KiB),
+// row-major, with the sixteen 16-byte chunks of row r permuted by
+// chunk ^ swz(r).  They are filled straight from global memory by the LDS DMA
+// path (global_load_lds_dwordx4: lane L of a wave lands at base + 16*L), and
+// read either row-wise (ds_read_b128: a row of 8 k values per lane) or
+// transposed (two ds_read_b64_tr_b16: a column of 8 rows per lane).  swz() is
+// chosen so that both read patterns touch each bank once per 16-lane phase:
 //   * row reads: 16 consecutive rows at one logical chunk -> 16 chunks;
 //   * transposed reads: 4 consecutive rows (aligned to 4) x 4 consecutive
 //     8-byte columns -> 16 different chunk slots.
@@ -44,6 +52,11 @@ namespace mm1 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// the operand type of the fp16 LDS transpose read builtin
+typedef __fp16 fp16x4_tr __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -59,25 +72,9 @@ __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// acc += A B with the accumulator held in AGPRs (a 16-register accumulator
-// tuple the compiler keeps in the accumulation registers for the whole loop).
-// For kernels with one wave per SIMD whose long-lived accumulators exceed the
-// 256 architectural VGPRs: the compiler's own MFMAs (built with VGPR-form
-// MFMA selection) keep the short-lived products in VGPRs, where the VALU
-// reads them.  Dependent accumulations into the same tuple are interlocked
-// by the hardware, as for the compiler's own chains.  The compiler does not
-// see this as an MFMA, so before the accumulators are read by any other
-// instruction the caller runs agpr_fence() (the MFMA write -> read wait states).
-__device__ __forceinline__ void mfma32_acc(const bf16x8& a, const bf16x8& b, f32x16& acc) {
-  __asm__("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-
-// 32 wait states, ordered before every later use of the fenced accumulators.
-template <int N>
-__device__ __forceinline__ void agpr_fence(f32x16 (&acc)[N]) {
-  __asm__ volatile("s_nop 15\n\ts_nop 15" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < N; ++i) __asm__ volatile("" : "+a"(acc[i]));
+// The attention products: fp16 operands, fp32 accumulation.
+__device__ __forceinline__ f32x16 mfma32h(const f16x8& a, const f16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -102,7 +99,7 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 // products ahead of its use.
 template <int N, int PF, class Load, class Mma, class Between>
 __device__ __forceinline__ void mfma_chain(Load&& load, Mma&& mma, Between&& between) {
-  bf16x8 fa[PF + 1];
+  decltype(load(0)) fa[PF + 1];
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     fa[i] = load(i);
@@ -121,11 +118,11 @@ __device__ __forceinline__ void mfma_chain(Load&& load, Mma&& mma, Between&& bet
 
 // mfma_chain whose first PF fragments the caller read earlier (before a
 // barrier, say), so the first product waits for no read.
-template <int N, int PF, class Load, class Mma, class Between>
-__device__ __forceinline__ void mfma_chain_from(const bf16x8 (&first)[PF], Load&& load, Mma&& mma,
+template <int N, int PF, class Frag, class Load, class Mma, class Between>
+__device__ __forceinline__ void mfma_chain_from(const Frag (&first)[PF], Load&& load, Mma&& mma,
                                                 Between&& between) {
   static_assert(PF >= 1 && PF < N, "prefetch depth");
-  bf16x8 fa[PF + 1];
+  Frag fa[PF + 1];
 #pragma unroll
   for (int i = 0; i < PF; ++i) fa[i] = first[i];
 #pragma unroll
@@ -150,8 +147,8 @@ __device__ __forceinline__ void wave_prio() {
 }
 
 // -x, elementwise (flips the sign bits: exact)
-__device__ __forceinline__ bf16x8 neg8(const bf16x8& x) {
-  return __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, x) ^ 0x80008000u);
+__device__ __forceinline__ f16x8 neg8(const f16x8& x) {
+  return __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, x) ^ 0x80008000u);
 }
 
 __device__ __forceinline__ f32x16 zero16() {
@@ -161,12 +158,20 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-// Eight consecutive accumulator registers (base .. base+7) as a bf16 MFMA
-// operand (round to nearest even).
-__device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
-  bf16x8 r;
+// Eight consecutive accumulator registers (base .. base+7) as an fp16 MFMA
+// operand (round to nearest even, v_cvt_pk_f16_f32).
+__device__ __forceinline__ f16x8 pack8(const f32x16& v, int base) {
+  f16x8 r;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) r[t] = (__bf16)v[base + t];
+  for (int t = 0; t < 8; ++t) r[t] = (_Float16)v[base + t];
+  return r;
+}
+
+// Eight bf16 values as fp16 (exact for |x| in [2^-17, 65504]).
+__device__ __forceinline__ f16x8 bf16_to_f16(const bf16x8& x) {
+  f16x8 r;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) r[t] = (_Float16)(float)x[t];
   return r;
 }
 
@@ -186,6 +191,7 @@ __device__ __forceinline__ void lds_barrier() {
 // Materialise a loaded operand here: the compiler may not sink the load into
 // a loop, where its wait would also drain the LDS DMA copies in flight.
 __device__ __forceinline__ void pin(bf16x8& x) { __asm__ volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(f16x8& x) { __asm__ volatile("" : "+v"(x)); }
 __device__ __forceinline__ void pin(float& x) { __asm__ volatile("" : "+v"(x)); }
 
 __device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
@@ -225,7 +231,7 @@ __device__ __forceinline__ void dma16_sbase(uint32_t lane_off, const void* sbase
                    :: "v"(lane_off), "s"(sbase), "s"(lds_base) : "memory", "m0");
 }
 
-// Copy a 64 x 128 bf16 tile into LDS with the DMA path.  Row r of the tile is
+// Copy a 64 x 128 tile of 16-bit values into LDS with the DMA path.  Row r of the tile is
 // at base + r*stride elements; rows at or beyond nvalid re-read row nvalid-1
 // (finite data the kernels mask out).  NW waves share the 16 row quads; wave
 // w copies quads w, w + NW, ...
@@ -243,10 +249,11 @@ __device__ __forceinline__ uint32_t tile_lane_off(long stride, int tid) {
   return (uint32_t)((rr * stride + 8 * chunk) * 2);
 }
 
-template <int NW>
-__device__ __forceinline__ void tile_dma(char* lds, const __bf16* base, long stride, int nvalid,
+template <int NW, class T>
+__device__ __forceinline__ void tile_dma(char* lds, const T* base, long stride, int nvalid,
                                          uint32_t lane_off, int tid) {
   static_assert(NW % 4 == 0, "row-quad swizzle needs a multiple of 4 waves");
+  static_assert(sizeof(T) == 2, "16-bit elements");
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
   if (nvalid >= TILE_ROWS) {
@@ -270,10 +277,12 @@ __device__ __forceinline__ void tile_dma(char* lds, const __bf16* base, long str
   }
 }
 
-// Copy a 32 x 128 bf16 tile (the layout of the first 32 rows of a 64-row
-// tile) with the LDS DMA path; issued by all 8 waves, wave w copies row quad
-// w (so swz(row) = 4*(L/16) + (w & 3) and tile_lane_off() applies as above).
-__device__ __forceinline__ void tile32_dma(char* lds, const __bf16* base, long stride, int nvalid,
+// Copy a 32 x 128 tile of 16-bit values (the layout of the first 32 rows of
+// a 64-row tile) with the LDS DMA path; issued by all 8 waves, wave w copies
+// row quad w (so swz(row) = 4*(L/16) + (w & 3) and tile_lane_off() applies
+// as above).
+template <class T>
+__device__ __forceinline__ void tile32_dma(char* lds, const T* base, long stride, int nvalid,
                                            uint32_t lane_off, int tid) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + w * 1024;
@@ -295,42 +304,22 @@ __device__ __forceinline__ void vec64_dma(char* lds, const float* base, int nval
   dma4(base + min(lane, nvalid - 1), __builtin_amdgcn_readfirstlane(lds_addr(lds)));
 }
 
-// A operand from a tile whose rows are the MFMA M axis: rows 32*blk + (lane&31),
-// k-step ks = columns 16*ks .. +15 (natural order).
-__device__ __forceinline__ bf16x8 lds_a_rows(const char* lds, int blk, int ks, int lane) {
-  return *reinterpret_cast<const bf16x8*>(lds + row_off(32 * blk + (lane & 31), 2 * ks + (lane >> 5)));
-}
-
-// A operand from a tile whose rows are the k axis (read transposed): M index
-// (column of the tile) 32*blk + (lane&31), k-step ks = tile rows 16*ks .. +15
-// in pi order.  Within each 16-lane group, ds_read_b64_tr_b16 gives lane i
-// element (i & 3) of the 8-byte chunks addressed by lanes 4t + (i >> 2),
-// t = 0..3; lane j of the group therefore addresses row
-// 16ks + 8r + 4h + (j >> 2), columns 4(j & 3) .. +3 of its 16-column strip.
-__device__ __forceinline__ bf16x8 lds_a_tr(const char* lds, int blk, int ks, int lane) {
-  const int h = lane >> 5, g = (lane >> 4) & 1, j = lane & 15;
-  const int col = 32 * blk + 16 * g + 4 * (j & 3);
-  const int chunk = col >> 3, half = (col >> 2) & 1;
-  bf16x8 out;
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int row = 16 * ks + 8 * r + 4 * h + (j >> 2);
-    const char* p = lds + row * 256 + ((chunk ^ swz(row)) << 4) + 8 * half;
-    const bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MM1_LDS bf16x4*)p);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) out[4 * r + t] = v[t];
-  }
-  return out;
-}
-
 // ---------------------------------------------------------------------------
 // Precomputed per-lane LDS addressing.  Every operand read of a tile is one of
 // a few per-lane byte offsets plus a compile-time constant, so loops need no
 // address arithmetic and the constants fold into the ds_read offset field.
 //
-// Row reads (lds_a_rows): offset = blk*8192 + (row_base ^ 32*ks), with
+// Row reads (rows_a: the A operand from a tile whose rows are the MFMA M
+//   axis, rows 32*blk + (lane&31), k-step ks = columns 16*ks .. +15):
+//   offset = blk*8192 + (row_base ^ 32*ks), with
 //   row_base = (lane&31)*256 + 16*((lane>>5) ^ swz(lane&31)).
-// Transposed reads (lds_a_tr): offset = 4096*ks + tr_base[blk][r], r = 0, 1.
+// Transposed reads (tr_a: the A operand from a tile whose rows are the k
+//   axis, M index = tile column 32*blk + (lane&31), k-step ks = tile rows
+//   16*ks .. +15 in pi order): offset = 4096*ks + tr_base[blk][r], r = 0, 1.
+//   Within each 16-lane group, ds_read_b64_tr_b16 gives lane i element
+//   (i & 3) of the 8-byte chunks addressed by lanes 4t + (i >> 2), t = 0..3;
+//   lane j of the group therefore addresses row 16ks + 8r + 4h + (j >> 2),
+//   columns 4(j & 3) .. +3 of its 16-column strip.
 struct LdsBases {
   int row;
   int tr[4][2];
@@ -351,8 +340,8 @@ __device__ __forceinline__ LdsBases make_lds_bases(int lane) {
   return b;
 }
 
-__device__ __forceinline__ bf16x8 rows_a(const char* tile, const LdsBases& lb, int blk, int ks) {
-  return *reinterpret_cast<const bf16x8*>(tile + blk * 8192 + (lb.row ^ (32 * ks)));
+__device__ __forceinline__ f16x8 rows_a(const char* tile, const LdsBases& lb, int blk, int ks) {
+  return *reinterpret_cast<const f16x8*>(tile + blk * 8192 + (lb.row ^ (32 * ks)));
 }
 
 // acc[jb] += A B over the 8 k-steps for the two 32-row blocks jb = 0, 1 of a
@@ -360,10 +349,10 @@ __device__ __forceinline__ bf16x8 rows_a(const char* tile, const LdsBases& lb, i
 // k-step ahead of their products.  The scheduling barriers keep them there:
 // the compiler would otherwise sink each read to its product, so every
 // product pair would wait for the full LDS latency.
-__device__ __forceinline__ void rows_chain2(const char* tile, const LdsBases& lb, const bf16x8 (&b)[8],
+__device__ __forceinline__ void rows_chain2(const char* tile, const LdsBases& lb, const f16x8 (&b)[8],
                                             f32x16 (&acc)[2]) {
   constexpr int PF = MM1_FWD_PREFETCH;
-  bf16x8 fa[PF + 1][2];
+  f16x8 fa[PF + 1][2];
 #pragma unroll
   for (int ks = 0; ks < PF; ++ks) {
     fa[ks][0] = rows_a(tile, lb, 0, ks);
@@ -376,8 +365,8 @@ __device__ __forceinline__ void rows_chain2(const char* tile, const LdsBases& lb
       fa[(ks + PF) % (PF + 1)][1] = rows_a(tile, lb, 1, ks + PF);
     }
     __builtin_amdgcn_sched_barrier(0);
-    acc[0] = mfma32(fa[ks % (PF + 1)][0], b[ks], acc[0]);
-    acc[1] = mfma32(fa[ks % (PF + 1)][1], b[ks], acc[1]);
+    acc[0] = mfma32h(fa[ks % (PF + 1)][0], b[ks], acc[0]);
+    acc[1] = mfma32h(fa[ks % (PF + 1)][1], b[ks], acc[1]);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -400,9 +389,10 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <class Dst>
-__device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4], float scale, char* lds, int lane,
-                                                Dst&& dst) {
+// One pass of store_tile_bf16: value(db, r) of every register through LDS
+// to the rows dst(i).
+template <class Val, class Dst>
+__device__ __forceinline__ void store_tile_pass(Val&& value, char* lds, int lane, Dst&& dst) {
   const int l32 = lane & 31, h = lane >> 5;
 #pragma unroll
   for (int db = 0; db < 4; ++db) {
@@ -410,7 +400,7 @@ __device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4], float sc
     for (int a4 = 0; a4 < 4; ++a4) {
       bf16x4 val;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) val[c] = (__bf16)(acc[db][4 * a4 + c] * scale);
+      for (int c = 0; c < 4; ++c) val[c] = value(db, 4 * a4 + c);
       const int chunk = (4 * db + a4) ^ (l32 & 15);
       *reinterpret_cast<bf16x4*>(lds + l32 * 256 + chunk * 16 + 8 * h) = val;
     }
@@ -425,12 +415,66 @@ __device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4], float sc
   }
 }
 
-__device__ __forceinline__ bf16x8 tr_a(const char* tile, const LdsBases& lb, int blk, int ks) {
-  bf16x8 out;
+template <class Dst>
+__device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4], float scale, char* lds, int lane,
+                                                Dst&& dst) {
+  store_tile_pass([&](int db, int r) MM1_INLINE { return (__bf16)(acc[db][r] * scale); }, lds, lane, dst);
+}
+
+// The 8 mantissa bits of an fp32 x that follow its truncation to bf16:
+// bits 16..9 of x (bit 7 of the byte is the truncation's last bit).  With
+// the round-to-nearest bf16 output o, o and this byte give 15 mantissa bits
+// of x back (lo8_decode); the residual costs one byte per value.
+__device__ __forceinline__ uint32_t lo8_bits(float x) { return (__float_as_uint(x) >> 9) & 0xffu; }
+
+// x from o = bf16(x) (round to nearest even) and q = lo8_bits(x): o is the
+// truncation T of x or T + 1 (as sign-magnitude integers); q's top bit is T's
+// last bit, which tells the two apart.  The 9 bits below the byte are taken
+// at the middle of their range: |result - x| <= 2^-15 |x|.
+__device__ __forceinline__ float lo8_decode(uint32_t o_bits, uint32_t q) {
+  const uint32_t t = o_bits - ((o_bits ^ (q >> 7)) & 1u);
+  return __uint_as_float((t << 16) | ((q & 0x7fu) << 9) | 0x100u);
+}
+
+// store_tile_bf16, and then lo8_bits of every value x = acc * scale to the
+// 128-byte rows dst_lo(i), also through the wave's 8 KiB (once its
+// first-pass reads are done): a lane writes its 4-value groups as dwords at
+// 16-byte chunk (c ^ (i & 7)) of row i, then reads back 16-byte pieces, so a
+// store instruction covers eight whole rows.
+template <class Dst, class DstLo>
+__device__ __forceinline__ void store_tile_bf16_lo(const f32x16 (&acc)[4], float scale, char* lds, int lane,
+                                                   Dst&& dst, DstLo&& dst_lo) {
+  store_tile_pass([&](int db, int r) MM1_INLINE { return (__bf16)(acc[db][r] * scale); }, lds, lane, dst);
+  wave_sync();
+  const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) w |= lo8_bits(acc[db][4 * a4 + c] * scale) << (8 * c);
+      const int col = 32 * db + 8 * a4 + 4 * h;   // byte column of the 4 values
+      const int chunk = (col >> 4) ^ (l32 & 7);
+      *reinterpret_cast<uint32_t*>(lds + l32 * 128 + (chunk << 4) + (col & 15)) = w;
+    }
+  }
+  wave_sync();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int row = 8 * k + (lane >> 3), ch = lane & 7;
+    const u32x4 x = *reinterpret_cast<const u32x4*>(lds + row * 128 + ((ch ^ (row & 7)) << 4));
+    uint8_t* p = dst_lo(row);
+    if (p) *reinterpret_cast<u32x4*>(p + 16 * ch) = x;
+  }
+}
+
+__device__ __forceinline__ f16x8 tr_a(const char* tile, const LdsBases& lb, int blk, int ks) {
+  f16x8 out;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (MM1_LDS bf16x4*)(tile + 4096 * ks + lb.tr[blk][r]));
+    const f16x4 v = __builtin_bit_cast(
+        f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM1_LDS fp16x4_tr*)(tile + 4096 * ks + lb.tr[blk][r])));
 #pragma unroll
     for (int t = 0; t < 4; ++t) out[4 * r + t] = v[t];
   }

@@ -33,14 +33,13 @@ def main(argv=None):
         seen.add(key)
         rows.append(r)
     rows.sort(key=lambda r: (r["case"], ORDER.get(r["out"], 9)))
-    print("| case | out | max-abs | rel-L2 | floor | pre-cast max-abs | pre-cast rel-L2 | alg | alg rel-L2 "
-          "| vs emul max-abs | vs emul rel-L2 | gate |")
-    print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|")
+    print("| case | out | max-abs | rel-L2 | floor | pre-cast max-abs | pre-cast rel-L2 "
+          "| reference-kernel rounding max-abs | ... rel-L2 | gate |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|---|")
     for r in rows:
         print(f"| {r['case']} | {r['out']} | {fmt(r['max_abs'])} | {fmt(r['rel_l2'])} | {fmt(r.get('floor'))} "
               f"| {fmt(r.get('precast_max_abs'))} | {fmt(r.get('precast_rel_l2'))} | {fmt(r.get('alg'))} "
-              f"| {fmt(r.get('alg_rel'))} | {fmt(r.get('vs_emul_max_abs'))} | {fmt(r.get('vs_emul_rel_l2'))} "
-              f"| {r.get('gate')} |")
+              f"| {fmt(r.get('alg_rel'))} | {r.get('gate')} |")
 
 
 if __name__ == "__main__":

@@ -62,100 +62,159 @@ def test_error_codes_and_messages(lib):
     assert b"unknown" in lib.mm1_attn_strerror(-99)
 
 
-def fwd(lib, q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=FAKE, B=1, S=64, H=10, Hkv=2, D=128,
+def _state_bytes(lib, B=1, S=64, H=10, Hkv=2):
+    return lib.mm1_attn_fwd_state_size(B, S, H, Hkv, 128)
+
+
+def fwd(lib, q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=FAKE, st=FAKE, st_bytes=None, B=1, S=64, H=10, Hkv=2, D=128,
         causal=1, scale=0.088):
-    return lib.mm1_attn_fwd(q, k, v, o, lse, B, S, H, Hkv, D, causal, scale, None)
+    nb = _state_bytes(lib, B, S, H, Hkv) if st_bytes is None else st_bytes
+    return lib.mm1_attn_fwd(q, k, v, o, lse, st, nb, B, S, H, Hkv, D, causal, scale, None)
+
+
+def test_state_and_workspace_sizes(lib):
+    """The forward state holds fp16 Q, K, V (2 bytes a value), the O residual
+    (1 byte) and the max|V| partials; the backward workspace fp16 dO, the
+    scaled Delta, the dO maxima and scale, and 2 * G fp32 slots of partial
+    sums (none when G == 1).  Every region is 256-byte aligned."""
+    up = lambda x: (x + 255) // 256 * 256
+    B, S, H, Hkv = 2, 100, 10, 2
+    nq, nkv = B * S * H * 128, B * S * Hkv * 128
+    assert lib.mm1_attn_fwd_state_size(B, S, H, Hkv, 128) == up(2 * nq) + 2 * up(2 * nkv) + up(nq) + up(512 * 4)
+    base = up(2 * nq) + up(4 * B * H * S) + up(1024 * 4) + 256
+    assert lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128) == base + up(2 * 5 * nkv * 4)
+    assert lib.mm1_attn_bwd_workspace_size(B, S, 4, 4, 128) == up(2 * B * S * 4 * 128) + up(4 * B * 4 * S) \
+        + up(1024 * 4) + 256
+    assert lib.mm1_attn_bwd_workspace_size(B, S, 10, 3, 128) == 0   # invalid shape
+    assert lib.mm1_attn_fwd_state_size(B, S, 10, 2, 64) == 0
 
 
 def test_fwd_argument_errors(lib):
     assert fwd(lib, q=None) == -1
     assert fwd(lib, lse=None) == -1
+    assert fwd(lib, st=None) == -1
     assert fwd(lib, H=10, Hkv=3) == -2
     assert fwd(lib, B=0) == -2
     assert fwd(lib, S=0) == -2
     assert fwd(lib, D=64) == -3
+    assert fwd(lib, st_bytes=_state_bytes(lib) - 1) == -4
     assert fwd(lib, scale=0.0) == -5
     assert fwd(lib, scale=float("nan")) == -5
     assert fwd(lib, q=FAKE + 8) == -6
+    assert fwd(lib, st=FAKE + 4) == -6
+    nb = _state_bytes(lib)
+    assert lib.mm1_attn_fwd_f32(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, nb, 1, 64, 10, 2, 128, 1, 0.1, 9, None) == -7
+    assert lib.mm1_attn_fwd_f32(FAKE, FAKE, FAKE, None, FAKE, FAKE, nb, 1, 64, 10, 2, 128, 1, 0.1, 0, None) == -1
+    assert lib.mm1_attn_prep(FAKE, FAKE, None, FAKE, nb, 1, 64, 10, 2, 128, None) == -1
+    assert lib.mm1_attn_prep(FAKE, FAKE, FAKE, FAKE, nb - 256, 1, 64, 10, 2, 128, None) == -4
+    assert lib.mm1_attn_prep(FAKE, FAKE, FAKE, FAKE, nb, 1, 64, 10, 2, 64, None) == -3
 
 
 def test_bwd_argument_errors(lib):
-    need = lib.mm1_attn_bwd_workspace_size(2, 100, 10, 2, 128)
-    assert need == 2 * 5 * 2 * 100 * 2 * 128 * 4
-    assert lib.mm1_attn_bwd_workspace_size(2, 100, 4, 4, 128) == 0
-    assert lib.mm1_attn_bwd_workspace_size(2, 100, 10, 3, 128) == 0   # invalid shape
+    B, S, H, Hkv = 2, 100, 10, 2
+    need = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
+    nst = _state_bytes(lib, B, S, H, Hkv)
 
-    def bwd(ws=FAKE, ws_bytes=None, **kw):
-        a = dict(B=2, S=100, H=10, Hkv=2, D=128, causal=1, scale=0.088)
+    def bwd(o=FAKE, st=FAKE, st_bytes=None, ws=FAKE, ws_bytes=None, dq=FAKE, **kw):
+        a = dict(B=B, S=S, H=H, Hkv=Hkv, D=128, causal=1, scale=0.088)
         a.update(kw)
-        nb = need if ws_bytes is None else ws_bytes
-        return lib.mm1_attn_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, nb,
-                                a["B"], a["S"], a["H"], a["Hkv"], a["D"], a["causal"], a["scale"],
-                                None)
+        return lib.mm1_attn_bwd(o, FAKE, FAKE, st, nst if st_bytes is None else st_bytes, dq, FAKE, FAKE, ws,
+                                need if ws_bytes is None else ws_bytes, a["B"], a["S"], a["H"], a["Hkv"], a["D"],
+                                a["causal"], a["scale"], None)
 
-    assert bwd(ws=None) == -4
+    assert bwd(o=None) == -1
+    assert bwd(dq=None) == -1
+    assert bwd(st=None) == -1
+    assert bwd(ws=None) == -1
     assert bwd(ws_bytes=need - 1) == -4
+    assert bwd(st_bytes=nst - 1) == -4
     assert bwd(D=256) == -3
     assert bwd(H=9) == -2
     assert bwd(scale=-1.0) == -5
     assert bwd(ws=FAKE + 4) == -6
-    assert lib.mm1_attn_bwd_dq(FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE,
-                               1, 64, 10, 2, 128, 1, 0.1, None) == -1
-    assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE,
-                                      FAKE, need, 2, 100, 10, 2, 128, 1, 0.1, None) == -1
-    assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
-                                      None, 0, 2, 100, 10, 2, 128, 1, 0.1, None) == -4
-    assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
-                                      FAKE + 4, need, 2, 100, 10, 2, 128, 1, 0.1, None) == -6
-    assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 10, 2, 128, 1, None) == -4
+    assert bwd(dq=FAKE + 2) == -6
+    sz = (B, S, H, Hkv, 128)
+    assert lib.mm1_attn_bwd_prep(None, FAKE, FAKE, nst, FAKE, need, *sz, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_prep(FAKE, FAKE, FAKE, nst, FAKE, need - 8, *sz, 0.1, None) == -4
+    assert lib.mm1_attn_bwd_prep(FAKE, FAKE, FAKE, nst, FAKE, need, *sz, 0.0, None) == -5
+    assert lib.mm1_attn_bwd_prep_delta(FAKE, None, FAKE, nst, FAKE, need, *sz, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_prep_delta(FAKE + 2, FAKE, FAKE, nst, FAKE, need, *sz, 0.1, None) == -6
+    cs = sz + (1, 0.1)
+    assert lib.mm1_attn_bwd_dq_tiles(FAKE, FAKE, nst, None, FAKE, need, *cs, 0, None) == -1
+    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, nst, FAKE, FAKE, None, FAKE, need, *cs, 0, 0, None) == -1
+    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, nst, FAKE, FAKE, FAKE, None, 0, *cs, 0, 0, None) == -1
+    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, nst, FAKE, FAKE, FAKE, FAKE + 4, need, *cs, 0, 0,
+                                            None) == -6
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(None, 0, FAKE, FAKE, *sz, 1, 0, None) == -1
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(FAKE, need - 1, FAKE, FAKE, *sz, 1, 0, None) == -4
     # nothing to reduce without groups: success without a device call
-    assert lib.mm1_attn_bwd_dkdv_reduce(None, 0, FAKE, FAKE, 1, 64, 4, 4, 128, 1, None) == 0
+    need1 = lib.mm1_attn_bwd_workspace_size(1, 64, 4, 4, 128)
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(FAKE, need1, FAKE, FAKE, 1, 64, 4, 4, 128, 1, 0, None) == 0
+    f32 = lib.mm1_attn_bwd_f32_tiles
+    assert f32(FAKE, FAKE, FAKE, FAKE, nst, FAKE, FAKE, FAKE, FAKE, need, *cs, 5, 0, None) == -7
+    assert f32(FAKE, FAKE, FAKE, FAKE, nst, FAKE, None, FAKE, FAKE, need, *cs, 0, 0, None) == -1
 
 
 def test_reduce_refuses_a_workspace_without_matching_partials(lib):
     """The calls that sum dK/dV partials check the layout record of the
-    workspace (written by a successful mm1_attn_bwd_dkdv* launch) and return
-    MM1_E_LAYOUT, launching nothing, when there is none for that address --
-    here no dK/dV call ever ran on it.  On the GPU the mismatched-tiling and
-    mismatched-shape cases are checked after real dK/dV launches."""
+    workspace (written by a successful mm1_attn_bwd_dkdv_tiles launch) and
+    return MM1_E_LAYOUT, launching nothing, when there is none for that
+    address -- here no dK/dV call ever ran on it.  On the GPU the
+    mismatched-tiling and mismatched-shape cases are checked after real dK/dV
+    launches."""
     E_LAYOUT = -8
-    need = lib.mm1_attn_bwd_workspace_size(2, 100, 10, 2, 128)
+    B, S, H, Hkv = 2, 100, 10, 2
+    need = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
+    nst = _state_bytes(lib, B, S, H, Hkv)
     ws = FAKE + (1 << 20)
+    cs = (B, S, H, Hkv, 128, 1, 0.1)
     for t in range(lib.mm1_attn_tile_count(1)):
-        assert lib.mm1_attn_bwd_dkdv_reduce_tiles(ws, need, FAKE, FAKE, 2, 100, 10, 2, 128, 1, t, None) == E_LAYOUT
-        assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, need,
-                                                2, 100, 10, 2, 128, 1, 0.1, t, 0, None) == E_LAYOUT
-    assert lib.mm1_attn_bwd_dkdv_reduce(ws, need, FAKE, FAKE, 2, 100, 10, 2, 128, 1, None) == E_LAYOUT
-    assert lib.mm1_attn_bwd_dq_reduce(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, need,
-                                      2, 100, 10, 2, 128, 1, 0.1, None) == E_LAYOUT
+        assert lib.mm1_attn_bwd_dkdv_reduce_tiles(ws, need, FAKE, FAKE, B, S, H, Hkv, 128, 1, t, None) == E_LAYOUT
+        assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, nst, FAKE, FAKE, FAKE, ws, need, *cs, t, 0,
+                                                None) == E_LAYOUT
     # argument errors still come first, and a tiling out of range is MM1_E_TILES
-    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(ws, need, FAKE, FAKE, 2, 100, 10, 2, 128, 1, 99, None) == -7
-    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(None, 0, FAKE, FAKE, 2, 100, 10, 2, 128, 1, 0, None) == -4
-    # the dQ call without the sum needs no workspace and no record
-    assert lib.mm1_attn_bwd_dq_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None,
-                                     2, 100, 10, 2, 128, 1, 0.1, 0, None) == -1
-    assert lib.mm1_attn_bwd_dq_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
-                                     2, 100, 10, 2, 128, 1, 0.1, 9, None) == -7
-    assert lib.mm1_attn_bwd_dkdv_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ws, need,
-                                       2, 100, 10, 2, 128, 1, 0.1, 9, None) == -7
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(ws, need, FAKE, FAKE, B, S, H, Hkv, 128, 1, 99, None) == -7
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(None, 0, FAKE, FAKE, B, S, H, Hkv, 128, 1, 0, None) == -1
+    # the dQ call without the sum needs no record
+    assert lib.mm1_attn_bwd_dq_tiles(FAKE, FAKE, nst, FAKE, ws, need, *cs, 9, None) == -7
+    assert lib.mm1_attn_bwd_dkdv_tiles(FAKE, FAKE, nst, FAKE, FAKE, ws, need, *cs, 9, None) == -7
+
+
+def test_layout_record_is_keyed_by_address_only():
+    """The layout record behind MM1_E_LAYOUT is host state keyed by the
+    workspace address (include/mm1_attn.h: a workspace freed and reallocated
+    at the same address with no dK/dV call since passes the check).  This
+    test reads the behaviour from the source of the check, which it cannot
+    exercise without a device: the record holds no allocation identity."""
+    src = (ROOT / "mimansm1_v1_amd" / "csrc" / "attn_capi.hip").read_text()
+    fields = re.search(r"struct WsLayout \{(.*?)\};", src, flags=re.S).group(1)
+    assert "const void* ws;" in fields
+    same = re.search(r"bool same\(const WsLayout& o\) const \{(.*?)\}", fields, flags=re.S).group(1)
+    assert "ws" not in re.sub(r"\bo\.", "", same).split()          # the address is the key, not compared
+    assert "a workspace freed and reallocated" in re.sub(r"\s*\n \*\s*", " ", HEADER.read_text())
 
 
 def test_noalloc_refuses_shapes_beyond_its_scratch(lib):
     """mm1_attn_bwd_noalloc checks its arguments and the static scratch's
-    size before any device call: MM1_E_SCRATCH for a shape whose dK/dV partial
-    sums exceed MM1_NOALLOC_SCRATCH_BYTES, the usual codes otherwise."""
-    cap = 128 << 20
-    assert f"(size_t)128 << 20" in HEADER.read_text()
+    size before any device call: MM1_E_SCRATCH for a shape whose backward
+    workspace exceeds MM1_NOALLOC_SCRATCH_BYTES, the usual codes otherwise."""
+    cap = 256 << 20
+    assert f"(size_t)256 << 20" in HEADER.read_text()
     need = lib.mm1_attn_bwd_noalloc_scratch_size
     for B, S in ((8, 2048), (2, 8192), (4, 4096), (1, 16384)):
         assert 0 < need(B, S, 10, 2, 128, 1) <= cap, (B, S)
-    assert need(2, 8192, 4, 4, 128, 1) == 0          # G = 1: no partials
-    assert need(1, 32768, 10, 2, 128, 1) > cap      # 214 MiB of partials
-    args = (FAKE,) * 9
-    assert lib.mm1_attn_bwd_noalloc(*args, 1, 32768, 10, 2, 128, 1, 0.1, None) == -9
-    assert lib.mm1_attn_bwd_noalloc(None, *args[1:], 2, 64, 10, 2, 128, 1, 0.1, None) == -1
-    assert lib.mm1_attn_bwd_noalloc(*args, 2, 64, 10, 3, 128, 1, 0.1, None) == -2
-    assert lib.mm1_attn_bwd_noalloc(*args, 2, 64, 10, 2, 128, 1, 0.0, None) == -5
+    # G = 1: no partials, only fp16 dO, Delta, the maxima and the scale
+    assert need(2, 8192, 4, 4, 128, 1) == lib.mm1_attn_bwd_workspace_size(2, 8192, 4, 4, 128)
+    assert need(1, 32768, 10, 2, 128, 1) > cap
+    nst = _state_bytes(lib, 1, 32768, 10, 2)
+    args = (FAKE,) * 3
+    assert lib.mm1_attn_bwd_noalloc(*args, FAKE, nst, FAKE, FAKE, FAKE, 1, 32768, 10, 2, 128, 1, 0.1, None) == -9
+    nst = _state_bytes(lib, 2, 64, 10, 2)
+    assert lib.mm1_attn_bwd_noalloc(None, *args[1:], FAKE, nst, FAKE, FAKE, FAKE, 2, 64, 10, 2, 128, 1, 0.1,
+                                    None) == -1
+    assert lib.mm1_attn_bwd_noalloc(*args, FAKE, nst, FAKE, FAKE, FAKE, 2, 64, 10, 3, 128, 1, 0.1, None) == -2
+    assert lib.mm1_attn_bwd_noalloc(*args, FAKE, nst, FAKE, FAKE, FAKE, 2, 64, 10, 2, 128, 1, 0.0, None) == -5
+    assert lib.mm1_attn_bwd_noalloc(*args, FAKE, nst - 1, FAKE, FAKE, FAKE, 2, 64, 10, 2, 128, 1, 0.1, None) == -4
     assert b"static scratch" in lib.mm1_attn_strerror(-9)
 
 
@@ -225,7 +284,8 @@ def test_tilings_queries_and_errors_without_device(lib):
     def fwd_t(tiles, **kw):
         a = dict(q=FAKE, B=1, S=64, H=10, Hkv=2, D=128)
         a.update(kw)
-        return lib.mm1_attn_fwd_tiles(a["q"], FAKE, FAKE, FAKE, FAKE, a["B"], a["S"], a["H"],
+        nb = lib.mm1_attn_fwd_state_size(1, 64, 10, 2, 128)
+        return lib.mm1_attn_fwd_tiles(a["q"], FAKE, FAKE, FAKE, FAKE, FAKE, nb, a["B"], a["S"], a["H"],
                                       a["Hkv"], a["D"], 1, 0.088, tiles, None)
 
     assert fwd_t(counts[0]) == -7
@@ -233,16 +293,17 @@ def test_tilings_queries_and_errors_without_device(lib):
     assert fwd_t(counts[0], q=None) == -1          # argument checks come first
     assert fwd_t(0, D=64) == -3
     need = lib.mm1_attn_bwd_workspace_size(2, 100, 10, 2, 128)
+    nst = lib.mm1_attn_fwd_state_size(2, 100, 10, 2, 128)
 
     def bwd_t(dkdv, dq, dq_ptr=FAKE, ws=FAKE):
-        return lib.mm1_attn_bwd_tiles(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, dq_ptr, FAKE, FAKE, ws,
+        return lib.mm1_attn_bwd_tiles(FAKE, FAKE, FAKE, FAKE, nst, dq_ptr, FAKE, FAKE, ws,
                                       need, 2, 100, 10, 2, 128, 1, 0.088, dkdv, dq, None)
 
     assert bwd_t(counts[1], 0) == -7
-    assert bwd_t(0, counts[2]) == -7               # refused before the dK/dV launch
+    assert bwd_t(0, counts[2]) == -7               # refused before the first launch
     assert bwd_t(0, 0, dq_ptr=None) == -1
     assert bwd_t(0, 0, dq_ptr=FAKE + 2) == -6
-    assert bwd_t(0, 0, ws=None) == -4
+    assert bwd_t(0, 0, ws=None) == -1
     assert b"tiling" in lib.mm1_attn_strerror(-7)
 
 
@@ -321,12 +382,11 @@ def _order(lib, kind, tiles, B, S, H=10, Hkv=2, causal=1, cus=256):
 def _items_and_costs(kind, tiles, B, S, H=10, Hkv=2):
     """Default numbering and relative work of a grid's items: forward / dQ row
     blocks walk their causal key tiles (64 keys), dK/dV key tiles their query
-    tiles (32 or 64 queries); the kernels' own index arithmetic."""
+    tiles (32 queries); the kernels' own index arithmetic."""
     G = H // Hkv
     if kind == 1:
-        bq = 64 if tiles == 2 else 32
         nbh, nkt = B * H, (S + 127) // 128
-        return [((S - (j // nbh) * 128 + bq - 1) // bq) * (bq // 32) for j in range(nkt * nbh)]
+        return [(S - (j // nbh) * 128 + 31) // 32 for j in range(nkt * nbh)]
     bm = 128 if tiles == (1 if kind == 0 else 0) else 256
     nbg, R = B * Hkv, G * S
     nt = (R + bm - 1) // bm
@@ -355,9 +415,9 @@ def _makespan(order, costs, slots_per_se):
     return worst
 
 
-# (kind, tiling): forward 0-2, the per-head dK/dV tilings 1-2 (the grouped
+# (kind, tiling): forward 0-2, the per-head dK/dV tiling 1 (the grouped
 # tiling 0 has its own plan test below), dQ 0-1
-GRIDS = [(0, 0), (0, 1), (0, 2), (1, 1), (1, 2), (2, 0), (2, 1)]
+GRIDS = [(0, 0), (0, 1), (0, 2), (1, 1), (2, 0), (2, 1)]
 SHAPES = [(2, 8192), (8, 2048), (4, 4096), (1, 1000), (3, 777)]
 
 

@@ -64,20 +64,19 @@ def test_attention_step_graph_replays(hip_device, B, S, tiles):
     q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, D, seed=S))
     o = torch.empty_like(q)
     lse = torch.empty(B, H, S, dtype=torch.float32, device=hip_device)
-    delta = torch.empty_like(lse)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, D)
-    ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=hip_device)
+    st = torch.empty(lib.mm1_attn_fwd_state_size(B, S, H, Hkv, D), dtype=torch.uint8, device=hip_device)
+    ws = torch.empty(lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, D), dtype=torch.uint8, device=hip_device)
     p = lambda t: t.data_ptr()
     args = (B, S, H, Hkv, D, 1, D ** -0.5)
 
     def step(sp):
-        _lib.check(lib.mm1_attn_fwd_tiles(p(q), p(k), p(v), p(o), p(lse), *args, tiles[0], sp), "fwd")
-        _lib.check(lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, D, sp), "delta")
-        _lib.check(lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk), p(dv),
-                                          p(ws), nws, *args, tiles[1], tiles[2], sp), "bwd")
+        _lib.check(lib.mm1_attn_fwd_tiles(p(q), p(k), p(v), p(o), p(lse), p(st), st.numel(), *args, tiles[0], sp),
+                   "fwd")
+        _lib.check(lib.mm1_attn_bwd_tiles(p(o), p(do), p(lse), p(st), st.numel(), p(dq), p(dk), p(dv), p(ws),
+                                          ws.numel(), *args, tiles[1], tiles[2], sp), "bwd")
 
-    _replay_and_compare(step, [o, lse, delta, dq, dk, dv])
+    _replay_and_compare(step, [o, lse, dq, dk, dv])
 
 
 @pytest.mark.parametrize("S", [777, 2048])
@@ -90,14 +89,13 @@ def test_overlapped_backward_graph_replays(hip_device, S):
     log(f"[case] overlapped backward graph B=1 S={S}")
     q, k, v, do = (t.to(hip_device) for t in R.make_inputs(1, S, H, Hkv, D, seed=S + 3))
     shape = (1, H, S, D, True, H // Hkv)
-    o, lse = A.FwdKernel(shape, A.FWD_TILES)(q, k, v)
-    delta = A.DeltaKernel(1, H, S, D)(o, do)
+    o, lse, state = A.FwdKernel(shape, A.FWD_TILES).run(q, k, v)
     config = dict(A.BWD_TILES, dq_block_M=256, dq_waves=8, dq_stages=3, overlap_dq=True)
     bwd = A.BwdKernel(shape, config)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
     def step(_sp):   # the handle launches on torch's current stream (and its side stream)
-        bwd(q, k, v, do, lse, delta, dq, dk, dv)
+        bwd.run_saved(o, do, lse, state, dq, dk, dv)
 
     _replay_and_compare(step, [dq, dk, dv])
 

@@ -4,10 +4,12 @@ Small shapes are checked against the CPU oracle (fp32 autograd through the
 restated reference attention).  The BASELINE.json configs 2-4 are checked at
 full size against the oracle's chunked closed-form fp32 math run on the GPU
 (itself pinned to the CPU oracle in test_gpu_oracle_device_agrees).  Every
-backward check also takes the kernel's pre-cast fp32 gradients
-(mm1_attn_bwd_f32) and the oracle's emulation of the reference kernel's bf16
-rounding points (grads_analytic(bf16_products=True), Delta from the oracle's
-own O): tests/parity.py says how a bf16 output passes."""
+check also takes the kernels' pre-cast fp32 outputs (mm1_attn_fwd_f32,
+mm1_attn_bwd_f32_tiles: the same kernels and tilings as the bf16 outputs, so
+the bf16 outputs must equal their rounding bitwise) and, for the gradients,
+the oracle's emulation of the reference kernel's bf16 rounding points
+(grads_analytic(bf16_products=True)) as a reported column: tests/parity.py
+says how an output passes."""
 from __future__ import annotations
 
 import ctypes
@@ -45,41 +47,48 @@ def hip_run(q, k, v, do, causal, groups, device, backward=True):
     return cpu(out), cpu(lse), *(cpu(g) for g in grads)
 
 
-def precast(q, k, v, do, causal, device):
-    """The kernels' fp32 values before their bf16 casts: O (mm1_attn_fwd_f32)
-    and dQ, dK, dV (mm1_attn_bwd_f32, on the library's own bf16 forward's lse2
-    and Delta, as the bf16 backward runs); CPU fp32 tensors (o, dq, dk, dv),
-    the gradients None when do is None."""
+def _tiles_of(B, S, H, D, causal, G):
+    """(forward tiling, (dK/dV tiling, dQ tiling)) of the kernel handles the
+    drop-in op runs for this shape (the tile record or the autotuner's pick)."""
+    import mimansm1_v1_amd as mm
+    return (mm.get_kernel("fwd", B, H, S, D, causal, G).tiles,
+            mm.get_kernel("bwd", B, H, S, D, causal, G).tiles)
+
+
+def precast(q, k, v, do, causal, device, tiles=None):
+    """The kernels' fp32 values before their bf16 casts, from the tilings the
+    drop-in op runs for this shape (or `tiles` = (fwd, (dkdv, dq))): O
+    (mm1_attn_fwd_f32) and dQ, dK, dV (mm1_attn_bwd_f32_tiles on the state of
+    that forward and its O rounded to bf16, which is the bf16 forward's O);
+    CPU fp32 tensors (o, dq, dk, dv), the gradients None when do is None."""
     from mimansm1_v1_amd import _lib
     lib = _lib.load()
     qd, kd, vd = (t.to(device).contiguous() for t in (q, k, v))
     B, S, H, D = qd.shape
     Hkv = kd.shape[2]
+    ft, (dkt, dqt) = tiles if tiles is not None else _tiles_of(B, S, H, D, causal, H // Hkv)
     sp = torch.cuda.current_stream(device).cuda_stream
     p = lambda t: t.data_ptr()
-    o = torch.empty_like(qd)
     o32 = torch.empty(qd.shape, dtype=torch.float32, device=device)
     lse = torch.empty(B, H, S, dtype=torch.float32, device=device)
-    lse32 = torch.empty_like(lse)
+    st = torch.empty(lib.mm1_attn_fwd_state_size(B, S, H, Hkv, D), dtype=torch.uint8, device=device)
     args = (B, S, H, Hkv, D, int(causal), D ** -0.5)
-    _lib.check(lib.mm1_attn_fwd(p(qd), p(kd), p(vd), p(o), p(lse), *args, sp), "fwd")
-    _lib.check(lib.mm1_attn_fwd_f32(p(qd), p(kd), p(vd), p(o32), p(lse32), *args, sp), "fwd_f32")
+    _lib.check(lib.mm1_attn_fwd_f32(p(qd), p(kd), p(vd), p(o32), p(lse), p(st), st.numel(), *args, ft, sp),
+               "fwd_f32")
     if do is None:
         torch.cuda.synchronize()
         return o32.cpu(), None, None, None
     dod = do.to(device).contiguous()
-    delta = torch.empty_like(lse)
-    _lib.check(lib.mm1_attn_delta(p(o), p(dod), p(delta), B, S, H, D, sp), "delta")
-    nws = lib.mm1_attn_bwd_f32_workspace_size(B, S, H, Hkv, D)
-    ws = torch.empty(nws // 4, dtype=torch.float32, device=device)
+    ob = o32.to(torch.bfloat16)
+    ws = torch.empty(lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, D), dtype=torch.uint8, device=device)
     dq = torch.empty(qd.shape, dtype=torch.float32, device=device)
     dk = torch.empty(kd.shape, dtype=torch.float32, device=device)
     dv = torch.empty(vd.shape, dtype=torch.float32, device=device)
-    _lib.check(lib.mm1_attn_bwd_f32(p(qd), p(kd), p(vd), p(dod), p(lse), p(delta), p(dq), p(dk), p(dv),
-                                    p(ws), nws, *args, sp), "bwd_f32")
+    _lib.check(lib.mm1_attn_bwd_f32_tiles(p(ob), p(dod), p(lse), p(st), st.numel(), p(dq), p(dk), p(dv),
+                                          p(ws), ws.numel(), *args, dkt, dqt, sp), "bwd_f32")
     torch.cuda.synchronize()
     out = (o32.cpu(), dq.cpu(), dk.cpu(), dv.cpu())
-    del ws, dq, dk, dv, o32
+    del ws, dq, dk, dv, o32, st
     return out
 
 
@@ -152,65 +161,75 @@ def test_tilings_vs_cpu_oracle(hip_device, monkeypatch, kind, index):
                     R.grads_analytic(q, k, v, do, causal, G, bf16_products=True))
 
 
-def _bwd_buffers(lib, q, k, v, H, Hkv, device):
-    B, S = q.shape[0], q.shape[1]
+def _fwd_state(lib, q, k, v, causal, device, tiles=-1):
+    """Forward through the C ABI: (o, lse2, state)."""
+    B, S, H = q.shape[0], q.shape[1], q.shape[2]
+    Hkv = k.shape[2]
     o, lse = torch.empty_like(q), torch.empty(B, H, S, dtype=torch.float32, device=device)
-    nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
-    ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=device)
-    return o, lse, torch.empty_like(lse), ws, nws
+    st = torch.empty(lib.mm1_attn_fwd_state_size(B, S, H, Hkv, 128), dtype=torch.uint8, device=device)
+    sp = torch.cuda.current_stream(device).cuda_stream
+    assert lib.mm1_attn_fwd_tiles(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                  st.data_ptr(), st.numel(), B, S, H, Hkv, 128, int(causal), 128 ** -0.5,
+                                  tiles, sp) == 0
+    return o, lse, st
 
 
-@pytest.mark.parametrize("dkdv_tiles", [0, 1, 2, 3, 4, 5])
+def _workspace(lib, B, S, H, Hkv, device):
+    return torch.empty(lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128), dtype=torch.uint8, device=device)
+
+
+@pytest.mark.parametrize("dkdv_tiles", [0, 1])
 def test_staged_tiling_calls_and_layout_check(hip_device, dkdv_tiles):
-    """The staged calls with an explicit tiling (dK/dV, then the separate sum,
-    then dQ; and dK/dV, then dQ with the sum in its tail) give the combined
-    mm1_attn_bwd_tiles result bitwise.  A summing call that names another
-    dK/dV tiling, shape or `causal` than the dK/dV call that filled the
-    workspace returns MM1_E_LAYOUT and launches nothing: dk/dv keep their
-    contents."""
+    """The staged calls with an explicit tiling (prep; dK/dV, then the
+    separate sum, then dQ; and dK/dV, then dQ with the sum in its tail) give
+    the combined mm1_attn_bwd_tiles result bitwise.  A summing call that
+    names another dK/dV tiling, shape or `causal` than the dK/dV call that
+    filled the workspace returns MM1_E_LAYOUT and launches nothing: dk/dv
+    keep their contents."""
     from mimansm1_v1_amd import _lib
     lib = _lib.load()
     E_LAYOUT = -8
     B, S, H, Hkv, causal = 2, 1111, 10, 2, True
     log(f"[case] staged calls, dK/dV tiling {dkdv_tiles}, B={B} S={S}")
     q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=17))
-    o, lse, delta, ws, nws = _bwd_buffers(lib, q, k, v, H, Hkv, hip_device)
+    o, lse, st = _fwd_state(lib, q, k, v, causal, hip_device)
+    ws = _workspace(lib, B, S, H, Hkv, hip_device)
     sp = torch.cuda.current_stream(hip_device).cuda_stream
     p = lambda t: t.data_ptr()
     args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5)
-    assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), *args, sp) == 0
-    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+    S_ = (p(st), st.numel())
+    W_ = (p(ws), ws.numel())
     ref = [torch.empty_like(t) for t in (q, k, v)]
-    assert lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), *(p(t) for t in ref),
-                                  p(ws), nws, *args, dkdv_tiles, 1, sp) == 0
+    assert lib.mm1_attn_bwd_tiles(p(o), p(do), p(lse), *S_, *(p(t) for t in ref), *W_, *args, dkdv_tiles, 1,
+                                  sp) == 0
     for tail in (False, True):
         dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
-        assert lib.mm1_attn_bwd_dkdv_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dk), p(dv),
-                                           p(ws), nws, *args, dkdv_tiles, sp) == 0
+        assert lib.mm1_attn_bwd_prep(p(o), p(do), *S_, *W_, *args[:5], args[6], sp) == 0
+        assert lib.mm1_attn_bwd_dkdv_tiles(p(lse), *S_, p(dk), p(dv), *W_, *args, dkdv_tiles, sp) == 0
         if tail:
-            assert lib.mm1_attn_bwd_dq_reduce_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk),
-                                                    p(dv), p(ws), nws, *args, dkdv_tiles, 1, sp) == 0
+            assert lib.mm1_attn_bwd_dq_reduce_tiles(p(lse), *S_, p(dq), p(dk), p(dv), *W_, *args, dkdv_tiles, 1,
+                                                    sp) == 0
         else:
-            assert lib.mm1_attn_bwd_dkdv_reduce_tiles(p(ws), nws, p(dk), p(dv), B, S, H, Hkv, 128, int(causal),
+            assert lib.mm1_attn_bwd_dkdv_reduce_tiles(*W_, p(dk), p(dv), B, S, H, Hkv, 128, int(causal),
                                                       dkdv_tiles, sp) == 0
-            assert lib.mm1_attn_bwd_dq_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), *args, 1, sp) == 0
+            assert lib.mm1_attn_bwd_dq_tiles(p(lse), *S_, p(dq), *W_, *args, 1, sp) == 0
         torch.cuda.synchronize()
         for name, x, y in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
             assert torch.equal(x, y), (name, tail)
     # a summing call that disagrees with the layout in the workspace
-    grouped = dkdv_tiles in (0, 3, 5)
+    grouped = dkdv_tiles == 0
     other = 1 if grouped else 0
     sk, sv = torch.full_like(k, 7.0), torch.full_like(v, 7.0)
-    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(p(ws), nws, p(sk), p(sv), B, S, H, Hkv, 128, int(causal),
-                                              other, sp) == E_LAYOUT
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(*W_, p(sk), p(sv), B, S, H, Hkv, 128, int(causal), other,
+                                              sp) == E_LAYOUT
     sq = torch.full_like(q, 7.0)
-    assert lib.mm1_attn_bwd_dq_reduce_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(sq), p(sk), p(sv),
-                                            p(ws), nws, *args, other, 1, sp) == E_LAYOUT
-    if grouped:   # the chunk plan of a grouped tiling depends on `causal` too
-        assert lib.mm1_attn_bwd_dkdv_reduce_tiles(p(ws), nws, p(sk), p(sv), B, S, H, Hkv, 128, 0,
-                                                  dkdv_tiles, sp) == E_LAYOUT
+    assert lib.mm1_attn_bwd_dq_reduce_tiles(p(lse), *S_, p(sq), p(sk), p(sv), *W_, *args, other, 1,
+                                            sp) == E_LAYOUT
+    if grouped:   # the chunk plan of the grouped tiling depends on `causal` too
+        assert lib.mm1_attn_bwd_dkdv_reduce_tiles(*W_, p(sk), p(sv), B, S, H, Hkv, 128, 0, dkdv_tiles,
+                                                  sp) == E_LAYOUT
     # another shape (fewer positions, same workspace address)
-    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(p(ws), nws, p(sk), p(sv), B, S - 100, H, Hkv, 128, int(causal),
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(*W_, p(sk), p(sv), B, S - 100, H, Hkv, 128, int(causal),
                                               dkdv_tiles, sp) == E_LAYOUT
     torch.cuda.synchronize()
     assert bool((sk == 7.0).all()) and bool((sv == 7.0).all()) and bool((sq == 7.0).all()), \
@@ -227,48 +246,29 @@ def test_backward_dq_overlap_matches_single_stream(hip_device, monkeypatch, B, S
     log(f"[case] dQ overlap vs one stream B{B} S{S} H{H} Hkv{Hkv}")
     q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S + 1))
     shape = (B, H, S, 128, True, H // Hkv)
-    o, lse = A.FwdKernel(shape, A.FWD_TILES)(q, k, v)
+    o, lse, state = A.FwdKernel(shape, A.FWD_TILES).run(q, k, v)
     delta = A.DeltaKernel(B, H, S, 128)(o, do)
     outs = []
     for config, default in ((dict(A.BWD_TILES, overlap_dq=False), True),
                             (dict(A.BWD_TILES, overlap_dq=True), False),
                             (dict(A.BWD_TILES), True)):
         monkeypatch.setattr(A, "OVERLAP_DQ", default)   # the record's entry wins
-        grads = [torch.full_like(t, 3.0) for t in (q, k, v)]
-        A.BwdKernel(shape, config)(q, k, v, do, lse, delta, *grads)
-        torch.cuda.synchronize()
-        outs.append(grads)
+        for saved in (True, False):   # the autograd op's call, and the reference signature's
+            grads = [torch.full_like(t, 3.0) for t in (q, k, v)]
+            if saved:
+                A.BwdKernel(shape, config).run_saved(o, do, lse, state, *grads)
+            else:
+                A.BwdKernel(shape, config)(q, k, v, do, lse, delta, *grads)
+            torch.cuda.synchronize()
+            outs.append(grads)
+    outs = outs[0::2] + outs[1::2]
+    for other in outs[1:3]:
+        for name, x, y in zip(("dq", "dk", "dv"), outs[0], other):
+            assert torch.equal(x, y), name
+    outs = outs[3:]
     for other in outs[1:]:
         for name, x, y in zip(("dq", "dk", "dv"), outs[0], other):
             assert torch.equal(x, y), name
-
-
-@pytest.mark.parametrize("B,S,H,Hkv,causal", [(2, 300, 10, 2, True), (1, 200, 6, 3, False), (1, 77, 4, 4, True),
-                                              (2, 1111, 10, 2, True), (8, 2048, 10, 2, True)],
-                         ids=["B2S300", "B1S200full", "B1S77mha", "B2S1111", "config2"])
-def test_quad_dkdv_tiling_bitwise_equal_to_pair_tiling(hip_device, B, S, H, Hkv, causal):
-    """The quad dK/dV tiling (5) runs the arithmetic of the pipelined pair
-    tiling (0) operation for operation in the same order, on the same chunk
-    plan: dQ, dK and dV are bitwise equal."""
-    from mimansm1_v1_amd import _lib
-    lib = _lib.load()
-    log(f"[case] quad vs pair dK/dV tiling B{B} S{S} H{H} Hkv{Hkv} causal={causal}")
-    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S + H))
-    o, lse, delta, ws, nws = _bwd_buffers(lib, q, k, v, H, Hkv, hip_device)
-    sp = torch.cuda.current_stream(hip_device).cuda_stream
-    p = lambda t: t.data_ptr()
-    args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5)
-    assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), *args, sp) == 0
-    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
-    outs = []
-    for dkdv_tiles in (0, 5):
-        r = [torch.empty_like(t) for t in (q, k, v)]
-        assert lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), *(p(t) for t in r),
-                                      p(ws), nws, *args, dkdv_tiles, 1, sp) == 0
-        torch.cuda.synchronize()
-        outs.append(r)
-    for name, x, y in zip(("dq", "dk", "dv"), *outs):
-        assert torch.equal(x, y), name
 
 
 @pytest.mark.parametrize("B,S,H,Hkv", [(8, 2048, 10, 2), (2, 8192, 10, 2), (4, 4096, 10, 2), (3, 2999, 10, 2),
@@ -300,7 +300,109 @@ def test_delta_kernel_vs_oracle(hip_device, B, S, H, Hkv):
     assert m["max_abs"] <= bound, (m["max_abs"], bound)
 
 
-@pytest.mark.parametrize("dkdv_tiles,dq_tiles", [(0, 0), (1, 1), (3, 1)], ids=["t00", "t11", "t31"])
+def _ws_regions(lib, B, S, H, Hkv):
+    """Byte offsets of the backward workspace's regions (the layout
+    include/mm1_attn.h describes): fp16 dO, 2^E Delta, the scale."""
+    up = lambda x: (x + 255) // 256 * 256
+    do16 = 0
+    delta = up(2 * B * S * H * 128)
+    dmax = delta + up(4 * B * H * S)
+    scale = dmax + up(1024 * 4)
+    return do16, delta, scale
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,dscale", [(2, 1000, 10, 2, 1.0), (1, 333, 6, 3, 2.0 ** -20),
+                                               (1, 77, 4, 4, 2.0 ** 12), (8, 2048, 10, 2, 1.0)],
+                         ids=["B2S1000", "B1S333tiny", "B1S77huge", "config2"])
+def test_bwd_prep_delta_and_scaled_do(hip_device, B, S, H, Hkv, dscale):
+    """mm1_attn_bwd_prep leaves in the workspace: 2^E with E from max|dO| and
+    max|V| by the rule of the library's do_scale_exp (E = 0 for dO of
+    ordinary size, a power of two that brings tiny or huge dO back into
+    fp16's range otherwise); do16 = fp16(2^E dO) exactly; and 2^E Delta, with
+    Delta = rowsum(O dO) from the forward's fp32 O (mm1_attn_fwd_f32, the
+    values the bf16 O rounds): within 2^-14 of sum_d |O_d dO_d| (15
+    significant bits of O), where the bf16 O alone is about 2^-9 away."""
+    from mimansm1_v1_amd import _lib
+    lib = _lib.load()
+    case = f"bwd prep B{B} S{S} H{H} Hkv{Hkv} dO x {dscale:g}"
+    log(f"[case] {case}")
+    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S + 3))
+    do = (do.float() * dscale).to(torch.bfloat16)
+    o, lse, st = _fwd_state(lib, q, k, v, True, hip_device)
+    ws = _workspace(lib, B, S, H, Hkv, hip_device)
+    sp = torch.cuda.current_stream(hip_device).cuda_stream
+    o32 = torch.empty(q.shape, dtype=torch.float32, device=hip_device)
+    st2 = torch.empty_like(st)
+    l2 = torch.empty_like(lse)
+    assert lib.mm1_attn_fwd_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), o32.data_ptr(), l2.data_ptr(),
+                                st2.data_ptr(), st2.numel(), B, S, H, Hkv, 128, 1, 128 ** -0.5, -1, sp) == 0
+    assert lib.mm1_attn_bwd_prep(o.data_ptr(), do.data_ptr(), st.data_ptr(), st.numel(), ws.data_ptr(),
+                                 ws.numel(), B, S, H, Hkv, 128, 128 ** -0.5, sp) == 0
+    torch.cuda.synchronize()
+    r_do, r_delta, r_scale = _ws_regions(lib, B, S, H, Hkv)
+    do16 = ws[r_do:r_do + 2 * do.numel()].view(torch.float16).view(do.shape).cpu()
+    delta = ws[r_delta:r_delta + 4 * B * H * S].view(torch.float32).view(B, H, S).cpu()
+    scale = ws[r_scale:r_scale + 8].view(torch.float32).cpu()
+    # the rule, on the host
+    mdo, mv = do.float().abs().max().item(), v.float().abs().max().item()
+    bound = 2 * 128 * 128 ** -0.5 * mdo * mv
+    if 2 ** -8 <= mdo <= 2 ** 8 and bound < 2 ** 15:
+        e = 0
+    else:
+        e = -(math.frexp(mdo)[1] - 1)
+        e = min(e, 14 - (math.frexp(bound)[1] - 1))
+    log(f"    max|dO| {mdo:.3e} max|V| {mv:.3e} -> E = {e}; scale cells {scale.tolist()}")
+    assert scale[0].item() == 2.0 ** -e and scale[1].item() == 2.0 ** e
+    assert torch.equal(do16, (do.float().cpu() * 2.0 ** e).to(torch.float16))
+    o32c, doc = o32.cpu(), do.float().cpu()
+    want = (o32c * doc).sum(-1).permute(0, 2, 1) * 2.0 ** e
+    mag = (o32c * doc).abs().sum(-1).permute(0, 2, 1) * 2.0 ** e
+    err = (delta - want).abs()
+    log(f"    Delta max err {err.max().item():.3e}, relative to sum|O dO| "
+        f"{(err / mag.clamp_min(1e-30)).max().item():.3e}")
+    assert bool((err <= 2 ** -14 * mag + 1e-30).all())
+    # the bf16 O alone: several times further off
+    err_bf = ((o.float().cpu() * doc).sum(-1).permute(0, 2, 1) * 2.0 ** e - want).abs()
+    assert err_bf.max().item() > 4 * err.max().item()
+
+
+@pytest.mark.parametrize("s1,s2", [(2.0 ** -20, 2.0 ** -24), (2.0 ** 10, 2.0 ** 14), (1.0, 2.0 ** -20),
+                                   (1.0, 2.0 ** -130)], ids=["tiny", "huge", "ordinary-tiny", "subnormal"])
+def test_backward_is_linear_in_do(hip_device, s1, s2):
+    """The gradients are linear in dO.  dO outside [2^-8, 2^8] is brought to
+    max|2^E dO| in [1, 2) before its fp16 rounding, so two such dO that differ
+    by a power of two have the same fp16 copy and every intermediate is the
+    same: dQ, dK, dV differ by exactly that power of two, bitwise.  Against
+    dO of ordinary size (E = 0) the fp16 roundings of the smallest dS values
+    (fp16 subnormals) differ, and with them a few bf16 roundings of the
+    outputs: equal up to rel-L2 1e-3.  dO of 2^-130 (bf16 subnormals: the
+    input itself has lost bits) must give finite results within 2e-2 of the
+    linear answer."""
+    import mimansm1_v1_amd as mm
+    B, S, H, Hkv = 2, 640, 10, 2
+    log(f"[case] backward with dO x {s1:g} and x {s2:g}")
+    q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=31))
+    outs = []
+    for sc in (s1, s2):
+        qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+        out = mm.flash_attention(qd, kd, vd, True, 5)
+        out.backward((do.float() * sc).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        outs.append([t.grad.float().cpu() for t in (qd, kd, vd)])
+    for name, a, b in zip(("dq", "dk", "dv"), *outs):
+        assert torch.isfinite(b).all(), name
+        # in float64 and back in a's units: (s2 / s1) a may not be a normal float32
+        rel = ((b.double() * (s1 / s2) - a.double()).norm() / a.double().norm()).item()
+        log(f"    {name}: rel-L2 vs linear {rel:.2e}")
+        if s1 != 1.0:
+            assert torch.equal(b, a * (s2 / s1)), name
+        elif s2 >= 2.0 ** -100:
+            assert rel <= 1e-3, name     # fp16 subnormal dS, then a bf16 rounding flipped here and there
+        else:
+            assert rel < 2e-2, name
+
+
+@pytest.mark.parametrize("dkdv_tiles,dq_tiles", [(0, 0), (1, 1), (0, 1)], ids=["t00", "t11", "t01"])
 @pytest.mark.parametrize("B,S", [(8, 2048), (4, 4096)])
 def test_dispatch_order_is_bitwise_neutral(hip_device, monkeypatch, B, S, dkdv_tiles, dq_tiles):
     """The dispatch order only changes which workgroup runs which item: every
@@ -313,24 +415,20 @@ def test_dispatch_order_is_bitwise_neutral(hip_device, monkeypatch, B, S, dkdv_t
         tables = [lib.mm1_attn_dispatch_order(0, fwd_tiles, B, S, H, Hkv, 1, 256, None, 0),
                   lib.mm1_attn_dispatch_order(1, dkdv_tiles, B, S, H, Hkv, 1, 256, None, 0),
                   lib.mm1_attn_dispatch_order(2, dq_tiles, B, S, H, Hkv, 1, 256, None, 0)]
-        log(f"[case] dispatch order B={B} S={S} tiles=({fwd_tiles},{dkdv_tiles},{dq_tiles}) table sizes {tables}")
+        log(f"[case] dispatch order B={B} S={S} tiles=({fwd_tiles},{dkdv_tiles},{dq_tiles}) "
+            f"table sizes {tables}")
         q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=B + S))
-        scale = 128 ** -0.5
         sp = torch.cuda.current_stream(hip_device).cuda_stream
         p = lambda t: t.data_ptr()
-        nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
-        ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=hip_device)
+        ws = _workspace(lib, B, S, H, Hkv, hip_device)
 
         def run(order):
             monkeypatch.setenv("MM1_DISPATCH_ORDER", "1" if order else "0")
-            o, lse = torch.empty_like(q), torch.empty(B, H, S, dtype=torch.float32, device=hip_device)
-            delta = torch.empty_like(lse)
+            o, lse, st = _fwd_state(lib, q, k, v, True, hip_device, fwd_tiles)
             dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-            args = (B, S, H, Hkv, 128, 1, scale)
-            assert lib.mm1_attn_fwd_tiles(p(q), p(k), p(v), p(o), p(lse), *args, fwd_tiles, sp) == 0
-            assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
-            assert lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk), p(dv),
-                                          p(ws), nws, *args, dkdv_tiles, dq_tiles, sp) == 0
+            assert lib.mm1_attn_bwd_tiles(p(o), p(do), p(lse), p(st), st.numel(), p(dq), p(dk), p(dv),
+                                          p(ws), ws.numel(), B, S, H, Hkv, 128, 1, 128 ** -0.5, dkdv_tiles,
+                                          dq_tiles, sp) == 0
             torch.cuda.synchronize()
             monkeypatch.delenv("MM1_DISPATCH_ORDER")
             return [x.cpu() for x in (o, lse, dq, dk, dv)]
@@ -340,57 +438,42 @@ def test_dispatch_order_is_bitwise_neutral(hip_device, monkeypatch, B, S, dkdv_t
             assert torch.equal(x, y), name
 
 
-def test_fp32_forward_rounds_to_the_bf16_forward(hip_device):
-    """mm1_attn_fwd_f32 writes the values the 4-wave ring forward (tiling 1)
-    rounds: bf16 of its O is that tiling's O bitwise, with the same lse2; the
-    other tilings differ from it by at most one bf16 rounding."""
+def test_fp32_outputs_round_to_the_bf16_outputs(hip_device):
+    """mm1_attn_fwd_f32 / mm1_attn_bwd_f32_tiles run the kernels of the bf16
+    calls with fp32 stores: for every tiling, bf16 of their O, dQ, dK, dV is
+    the bf16 call's output bitwise, with the same lse2 and forward state."""
     from mimansm1_v1_amd import _lib
     lib = _lib.load()
     for (B, S, H, Hkv, causal) in [(2, 1500, 10, 2, True), (1, 333, 6, 3, False), (4, 4096, 10, 2, True)]:
-        log(f"[case] fp32 forward B={B} S={S} H={H} Hkv={Hkv} causal={causal}")
-        q, k, v, _ = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S, rope_sigma=S == 4096))
+        log(f"[case] fp32 outputs B={B} S={S} H={H} Hkv={Hkv} causal={causal}")
+        q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S, rope_sigma=S == 4096))
         sp = torch.cuda.current_stream(hip_device).cuda_stream
         p = lambda t: t.data_ptr()
         args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5)
-        o32 = torch.empty(q.shape, dtype=torch.float32, device=hip_device)
-        l32 = torch.empty(B, H, S, dtype=torch.float32, device=hip_device)
-        assert lib.mm1_attn_fwd_f32(p(q), p(k), p(v), p(o32), p(l32), *args, sp) == 0
+        ws = _workspace(lib, B, S, H, Hkv, hip_device)
         for t in range(lib.mm1_attn_tile_count(0)):
-            o = torch.empty_like(q)
-            lse = torch.empty_like(l32)
-            assert lib.mm1_attn_fwd_tiles(p(q), p(k), p(v), p(o), p(lse), *args, t, sp) == 0
+            o32 = torch.empty(q.shape, dtype=torch.float32, device=hip_device)
+            l32 = torch.empty(B, H, S, dtype=torch.float32, device=hip_device)
+            st32 = torch.empty(lib.mm1_attn_fwd_state_size(B, S, H, Hkv, 128), dtype=torch.uint8,
+                               device=hip_device)
+            assert lib.mm1_attn_fwd_f32(p(q), p(k), p(v), p(o32), p(l32), p(st32), st32.numel(), *args, t,
+                                        sp) == 0
+            o, lse, st = _fwd_state(lib, q, k, v, causal, hip_device, t)
             torch.cuda.synchronize()
-            if t == 1:
-                assert torch.equal(o, o32.to(torch.bfloat16)) and torch.equal(lse, l32), t
-            ulp = o32.abs().clamp(min=2 ** -126) * 2 ** -7
-            assert bool(((o.float() - o32).abs() <= ulp * 1.01 + 1e-6).all()), t
-
-
-def test_dkdv_tilings_agree_bitwise(hip_device):
-    """The 64-keys-per-wave dK/dV tilings (3, 4: one wave per SIMD, AGPR
-    accumulators) do each key's arithmetic in the same order as the
-    32-keys-per-wave tilings (0, 1): every gradient is bitwise equal."""
-    from mimansm1_v1_amd import _lib
-    lib = _lib.load()
-    for (B, S, H, Hkv, causal) in [(2, 3000, 10, 2, True), (1, 1000, 6, 3, False), (1, 77, 4, 4, True)]:
-        log(f"[case] dK/dV tilings 0/3 and 1/4, B={B} S={S} H={H} Hkv={Hkv} causal={causal}")
-        q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=S))
-        o, lse, delta, ws, nws = _bwd_buffers(lib, q, k, v, H, Hkv, hip_device)
-        sp = torch.cuda.current_stream(hip_device).cuda_stream
-        p = lambda t: t.data_ptr()
-        args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5)
-        assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), *args, sp) == 0
-        assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
-        outs = {}
-        for t in (0, 3, 1, 4):
-            g = [torch.empty_like(x) for x in (q, k, v)]
-            assert lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), *(p(x) for x in g),
-                                          p(ws), nws, *args, t, 0, sp) == 0
-            torch.cuda.synchronize()
-            outs[t] = [x.cpu() for x in g]
-        for a, b in ((0, 3), (1, 4)):
-            for name, x, y in zip(("dq", "dk", "dv"), outs[a], outs[b]):
-                assert torch.equal(x, y), (a, b, name)
+            assert torch.equal(o, o32.to(torch.bfloat16)) and torch.equal(lse, l32), t
+            assert torch.equal(st, st32), t            # the same state, residual bytes included
+        for dkt in range(lib.mm1_attn_tile_count(1)):
+            for dqt in range(lib.mm1_attn_tile_count(2)):
+                g = [torch.empty_like(x) for x in (q, k, v)]
+                g32 = [torch.empty(x.shape, dtype=torch.float32, device=hip_device) for x in (q, k, v)]
+                assert lib.mm1_attn_bwd_tiles(p(o), p(do), p(lse), p(st), st.numel(), *(p(x) for x in g),
+                                              p(ws), ws.numel(), *args, dkt, dqt, sp) == 0
+                assert lib.mm1_attn_bwd_f32_tiles(p(o), p(do), p(lse), p(st), st.numel(),
+                                                  *(p(x) for x in g32), p(ws), ws.numel(), *args, dkt, dqt,
+                                                  sp) == 0
+                torch.cuda.synchronize()
+                for name, x, y in zip(("dq", "dk", "dv"), g, g32):
+                    assert torch.equal(x, y.to(torch.bfloat16)), (dkt, dqt, name)
 
 
 def test_autotune_records_a_compiled_winner(hip_device, monkeypatch, tmp_path):
@@ -499,20 +582,19 @@ def test_large_ragged_vs_gpu_oracle(hip_device, B, S, H, Hkv):
 
 
 def _capi_run(lib, q, k, v, do, H, Hkv, causal, dkdv_tiles, dq_tiles, device):
-    """Forward + backward through the C ABI with explicit tilings (GPU tensors)."""
+    """Forward (default tiling) + backward through the C ABI with explicit
+    backward tilings (GPU tensors): o, lse2, state, dq, dk, dv."""
     B, S = q.shape[0], q.shape[1]
-    scale = 128 ** -0.5
     sp = torch.cuda.current_stream(device).cuda_stream
     p = lambda t: t.data_ptr()
-    o, lse, delta, ws, nws = _bwd_buffers(lib, q, k, v, H, Hkv, device)
+    o, lse, st = _fwd_state(lib, q, k, v, causal, device, 0)
+    ws = _workspace(lib, B, S, H, Hkv, device)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    args = (B, S, H, Hkv, 128, int(causal), scale)
-    assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), *args, sp) == 0
-    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
-    assert lib.mm1_attn_bwd_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk), p(dv),
-                                  p(ws), nws, *args, dkdv_tiles, dq_tiles, sp) == 0
+    args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5)
+    assert lib.mm1_attn_bwd_tiles(p(o), p(do), p(lse), p(st), st.numel(), p(dq), p(dk), p(dv),
+                                  p(ws), ws.numel(), *args, dkdv_tiles, dq_tiles, sp) == 0
     torch.cuda.synchronize()
-    return o, lse, dq, dk, dv
+    return o, lse, st, dq, dk, dv
 
 
 GROUPED = [(8, 2048, 10, 2, True), (2, 8192, 10, 2, True), (2, 7777, 10, 2, True),
@@ -537,24 +619,22 @@ def test_grouped_dkdv_vs_gpu_oracle(hip_device, B, S, H, Hkv, causal):
     G = H // Hkv
     qc, kc, vc, doc = R.make_inputs(B, S, H, Hkv, 128, seed=S + B)
     q, k, v, do = (t.to(hip_device) for t in (qc, kc, vc, doc))
-    o, lse, dq, dk, dv = _capi_run(lib, q, k, v, do, H, Hkv, causal, 0, 1, hip_device)
-    pre = precast(qc, kc, vc, doc, causal, hip_device)
+    o, lse, st, dq, dk, dv = _capi_run(lib, q, k, v, do, H, Hkv, causal, 0, 1, hip_device)
+    pre = precast(qc, kc, vc, doc, causal, hip_device, tiles=(0, (0, 1)))
     want = [t.cpu() for t in R.grads_analytic(q, k, v, do, causal, G)]
     emu = [t.cpu() for t in R.grads_analytic(q, k, v, do, causal, G, bf16_products=True)]
     check_grads(case, (dq.cpu(), dk.cpu(), dv.cpu()), want, pre, emu)
     del want, emu
-    # staged: dK/dV, then the separate reduction
+    # staged: prep, dK/dV, then the separate reduction
     sp = torch.cuda.current_stream(hip_device).cuda_stream
     p = lambda t: t.data_ptr()
-    nws = lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128)
-    ws = torch.empty(max(nws // 4, 1), dtype=torch.float32, device=hip_device)
-    delta = torch.empty_like(lse)
-    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+    ws = _workspace(lib, B, S, H, Hkv, hip_device)
     sk, sv = torch.empty_like(k), torch.empty_like(v)
     args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5)
-    assert lib.mm1_attn_bwd_dkdv_tiles(p(q), p(k), p(v), p(do), p(lse), p(delta), p(sk), p(sv),
-                                       p(ws), nws, *args, 0, sp) == 0
-    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(p(ws), nws, p(sk), p(sv), B, S, H, Hkv, 128,
+    assert lib.mm1_attn_bwd_prep(p(o), p(do), p(st), st.numel(), p(ws), ws.numel(), *args[:5], args[6], sp) == 0
+    assert lib.mm1_attn_bwd_dkdv_tiles(p(lse), p(st), st.numel(), p(sk), p(sv), p(ws), ws.numel(), *args, 0,
+                                       sp) == 0
+    assert lib.mm1_attn_bwd_dkdv_reduce_tiles(p(ws), ws.numel(), p(sk), p(sv), B, S, H, Hkv, 128,
                                               int(causal), 0, sp) == 0
     torch.cuda.synchronize()
     assert torch.equal(sk, dk) and torch.equal(sv, dv)
@@ -572,45 +652,55 @@ def test_backward_deterministic(hip_device):
 @pytest.mark.parametrize("shape", [(2, 1000, 10, 2, True), (1, 333, 6, 3, False), (1, 256, 4, 4, True)],
                          ids=["B2S1000G5causal", "B1S333G2full", "B1S256G1causal"])
 def test_backward_stages_match_combined(hip_device, shape):
-    """mm1_attn_bwd (dK/dV, then dQ with the group sum in its tail) and the
-    separate stages (dK/dV, group sum, dQ) write bitwise-identical gradients;
-    the fp32 backward rounds to them within one bf16 rounding."""
+    """mm1_attn_bwd (prep, dK/dV, then dQ with the group sum in its tail) and
+    the separate stages (prep, dK/dV, group sum, dQ) write bitwise-identical
+    gradients, and so does the reference-signature path (mm1_attn_prep +
+    mm1_attn_bwd_prep_delta) given the Delta the state-based prep computed."""
     from mimansm1_v1_amd import _lib
     B, S, H, Hkv, causal = shape
     log(f"[case] stages vs combined {shape}")
     lib = _lib.load()
     q, k, v, do = (t.to(hip_device) for t in R.make_inputs(B, S, H, Hkv, 128, seed=9))
-    scale = 128 ** -0.5
-    o, lse, delta, ws, nws = _bwd_buffers(lib, q, k, v, H, Hkv, hip_device)
     sp = torch.cuda.current_stream(hip_device).cuda_stream
     p = lambda t: t.data_ptr()
-    assert lib.mm1_attn_fwd(p(q), p(k), p(v), p(o), p(lse), B, S, H, Hkv, 128, int(causal), scale, sp) == 0
-    assert lib.mm1_attn_delta(p(o), p(do), p(delta), B, S, H, 128, sp) == 0
+    o, lse, st = _fwd_state(lib, q, k, v, causal, hip_device)
+    ws = _workspace(lib, B, S, H, Hkv, hip_device)
+    args = (B, S, H, Hkv, 128, int(causal), 128 ** -0.5)
+    S_, W_ = (p(st), st.numel()), (p(ws), ws.numel())
     outs = []
-    for combined in (True, False):
+    for mode in ("combined", "staged", "reference"):
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        args = (B, S, H, Hkv, 128, int(causal), scale, sp)
-        if combined:
-            rc = lib.mm1_attn_bwd(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), p(dk), p(dv),
-                                  p(ws), nws, *args)
-            assert rc == 0
+        if mode == "combined":
+            assert lib.mm1_attn_bwd(p(o), p(do), p(lse), *S_, p(dq), p(dk), p(dv), *W_, *args, sp) == 0
+        elif mode == "staged":
+            assert lib.mm1_attn_bwd_prep(p(o), p(do), *S_, *W_, *args[:5], args[6], sp) == 0
+            assert lib.mm1_attn_bwd_dkdv_tiles(p(lse), *S_, p(dk), p(dv), *W_, *args, -1, sp) == 0
+            assert lib.mm1_attn_bwd_dkdv_reduce_tiles(*W_, p(dk), p(dv), B, S, H, Hkv, 128, int(causal), -1,
+                                                      sp) == 0
+            assert lib.mm1_attn_bwd_dq_tiles(p(lse), *S_, p(dq), *W_, *args, -1, sp) == 0
         else:
-            assert lib.mm1_attn_bwd_dkdv(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dk), p(dv),
-                                         p(ws), nws, *args) == 0
-            assert lib.mm1_attn_bwd_dkdv_reduce(p(ws), nws, p(dk), p(dv), B, S, H, Hkv, 128, int(causal), sp) == 0
-            assert lib.mm1_attn_bwd_dq(p(q), p(k), p(v), p(do), p(lse), p(delta), p(dq), *args) == 0
+            # Delta as the state-based prep computed it (2^E Delta in the
+            # workspace, E = 0 for these inputs), through the reference
+            # signature's path
+            r_do, r_delta, r_scale = _ws_regions(lib, B, S, H, Hkv)
+            torch.cuda.synchronize()
+            assert ws[r_scale:r_scale + 4].view(torch.float32).item() == 1.0
+            delta = ws[r_delta:r_delta + 4 * B * H * S].view(torch.float32).view(B, H, S).clone()
+            st2 = torch.empty_like(st)
+            ws2 = torch.empty_like(ws)
+            assert lib.mm1_attn_prep(p(q), p(k), p(v), p(st2), st2.numel(), *args[:5], sp) == 0
+            assert lib.mm1_attn_bwd_prep_delta(p(do), p(delta), p(st2), st2.numel(), p(ws2), ws2.numel(),
+                                               *args[:5], args[6], sp) == 0
+            assert lib.mm1_attn_bwd_dkdv_tiles(p(lse), p(st2), st2.numel(), p(dk), p(dv), p(ws2), ws2.numel(),
+                                               *args, -1, sp) == 0
+            assert lib.mm1_attn_bwd_dq_reduce_tiles(p(lse), p(st2), st2.numel(), p(dq), p(dk), p(dv), p(ws2),
+                                                    ws2.numel(), *args, -1, -1, sp) == 0
         torch.cuda.synchronize()
         outs.append((dq.cpu(), dk.cpu(), dv.cpu()))
-    for name, x, y in zip(("dq", "dk", "dv"), *outs):
-        assert torch.equal(x, y), name
-        assert torch.isfinite(x.float()).all(), name
-    # fp32 gradients: within one bf16 rounding of the bf16 ones (the dK/dV
-    # sums of the grouped default tiling and the per-head fp32 path differ in
-    # fp32 summation order only)
-    pre = precast(q.cpu(), k.cpu(), v.cpu(), do.cpu(), causal, hip_device)
-    for name, x, y in zip(("dq", "dk", "dv"), outs[0], pre[1:]):
-        ulp = y.abs().clamp(min=2 ** -126) * 2 ** -7
-        assert bool(((x.float() - y).abs() <= ulp * 1.01 + 1e-6).all()), name
+    for other in outs[1:]:
+        for name, x, y in zip(("dq", "dk", "dv"), outs[0], other):
+            assert torch.equal(x, y), name
+            assert torch.isfinite(x.float()).all(), name
 
 
 def test_lse_lower_bound_and_rows_sum(hip_device):
@@ -619,8 +709,9 @@ def test_lse_lower_bound_and_rows_sum(hip_device):
     q, k, _, _ = R.make_inputs(1, 777, 10, 2, 128, seed=9)
     v = torch.ones(1, 777, 2, 128, dtype=torch.bfloat16)
     o, lse, *_ = hip_run(q, k, v, None, True, 5, hip_device, backward=False)
-    # P is rounded to bf16 for the MFMA while l sums the fp32 values (as the
-    # reference does, AT:173-180), so O = 1 holds to bf16 rounding only.
+    # P is rounded to fp16 for the MFMA while l sums the fp32 values (the
+    # reference rounds to bf16 there, AT:173-180), so O = 1 holds to the
+    # rounding of P and of the bf16 output only.
     assert (o.float() - 1).abs().max().item() <= 8e-3
     smax = R.scores(q, k, True, 5).amax(-1) * R.LOG2E
     assert (lse - smax).min().item() >= -1e-4
@@ -632,16 +723,14 @@ def test_capi_errors_on_device(hip_device):
     q = torch.zeros(1, 64, 10, 128, dtype=torch.bfloat16, device=hip_device)
     kv = torch.zeros(1, 64, 2, 128, dtype=torch.bfloat16, device=hip_device)
     lse = torch.zeros(1, 10, 64, dtype=torch.float32, device=hip_device)
-    d = torch.zeros_like(lse)
-    need = lib.mm1_attn_bwd_workspace_size(1, 64, 10, 2, 128)
-    assert need == 2 * 5 * 64 * 2 * 128 * 4
-    ws = torch.empty(need // 4, dtype=torch.float32, device=hip_device)
-    rc = lib.mm1_attn_bwd(q.data_ptr(), kv.data_ptr(), kv.data_ptr(), q.data_ptr(), lse.data_ptr(),
-                          d.data_ptr(), q.data_ptr(), kv.data_ptr(), kv.data_ptr(), ws.data_ptr(),
-                          need - 4, 1, 64, 10, 2, 128, 1, 0.1, None)
+    st = torch.empty(lib.mm1_attn_fwd_state_size(1, 64, 10, 2, 128), dtype=torch.uint8, device=hip_device)
+    ws = _workspace(lib, 1, 64, 10, 2, hip_device)
+    rc = lib.mm1_attn_bwd(q.data_ptr(), q.data_ptr(), lse.data_ptr(), st.data_ptr(), st.numel(), q.data_ptr(),
+                          kv.data_ptr(), kv.data_ptr(), ws.data_ptr(), ws.numel() - 4, 1, 64, 10, 2, 128, 1, 0.1,
+                          None)
     assert rc == -4
-    rc = lib.mm1_attn_fwd(q.data_ptr() + 2, kv.data_ptr(), kv.data_ptr(), q.data_ptr(),
-                          lse.data_ptr(), 1, 64, 10, 2, 128, 1, 0.1, None)
+    rc = lib.mm1_attn_fwd(q.data_ptr() + 2, kv.data_ptr(), kv.data_ptr(), q.data_ptr(), lse.data_ptr(),
+                          st.data_ptr(), st.numel(), 1, 64, 10, 2, 128, 1, 0.1, None)
     assert rc == -6
     torch.cuda.synchronize()
 
