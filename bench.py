@@ -37,6 +37,7 @@ PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA, published
 HBM_TBPS = 8.0
 
 CONFIGS = {
+    1: dict(batch=1, seq=512),      # forward only
     2: dict(batch=8, seq=2048),
     3: dict(batch=2, seq=8192),
     4: dict(batch=4, seq=4096),
@@ -55,9 +56,10 @@ def parse(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
-    ap.add_argument("--also", type=int, nargs="*", default=[2, 4, 5],
-                    help="extra configs reported beside the main one (5 = the attention sublayer)")
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4])
+    ap.add_argument("--also", type=int, nargs="*", default=[1, 2, 4, 5],
+                    help="extra configs reported beside the main one (1 = forward only, 5 = the "
+                         "attention sublayer)")
     ap.add_argument("--repeats", type=int, default=5,
                     help="timed loops of --steps steps; the reported figures are their median")
     ap.add_argument("--tiles", default=None, metavar="FWD,DKDV,DQ",
@@ -183,7 +185,8 @@ class Workload:
                                  t["fwd"], sp), "fwd")
         if marks is not None:
             marks[0].record(self.stream)
-        chk(L.mm1_attn_bwd_prep(p(self.o), p(self.do), *st, *ws, B, S, H, Hkv, D, self.scale, sp), "prep")
+        chk(L.mm1_attn_bwd_prep(p(self.o), p(self.do), p(self.lse), *st, *ws, B, S, H, Hkv, D, self.scale, sp),
+            "prep")
         if marks is not None:
             marks[1].record(self.stream)
         if marks is None and t.get("overlap"):
@@ -191,26 +194,108 @@ class Workload:
             fork = torch.cuda.Event()
             fork.record(self.stream)
             self.side.wait_event(fork)
-            chk(L.mm1_attn_bwd_dq_tiles(p(self.lse), *st, p(self.dq), *ws, *shape, t["dq"],
-                                        self.side.cuda_stream), "dq")
-            chk(L.mm1_attn_bwd_dkdv_tiles(p(self.lse), *st, p(self.dk), p(self.dv), *ws, *shape, t["dkdv"], sp),
-                "dkdv")
+            chk(L.mm1_attn_bwd_dq_tiles(*st, p(self.dq), *ws, *shape, t["dq"], self.side.cuda_stream), "dq")
+            chk(L.mm1_attn_bwd_dkdv_tiles(*st, p(self.dk), p(self.dv), *ws, *shape, t["dkdv"], sp), "dkdv")
             chk(L.mm1_attn_bwd_dkdv_reduce_tiles(*ws, p(self.dk), p(self.dv), B, S, H, Hkv, D, 1, t["dkdv"], sp),
                 "dkdv reduce")
             join = torch.cuda.Event()
             join.record(self.side)
             self.stream.wait_event(join)
             return
-        chk(L.mm1_attn_bwd_dkdv_tiles(p(self.lse), *st, p(self.dk), p(self.dv), *ws, *shape, t["dkdv"], sp),
-            "dkdv")
+        chk(L.mm1_attn_bwd_dkdv_tiles(*st, p(self.dk), p(self.dv), *ws, *shape, t["dkdv"], sp), "dkdv")
         if marks is not None:
             marks[2].record(self.stream)
         # dQ, with the dK/dV group sum folded into the same launch (what
         # mm1_attn_bwd runs after the dK/dV stage)
-        chk(L.mm1_attn_bwd_dq_reduce_tiles(p(self.lse), *st, p(self.dq), p(self.dk), p(self.dv), *ws, *shape,
-                                           t["dkdv"], t["dq"], sp), "dq")
+        chk(L.mm1_attn_bwd_dq_reduce_tiles(*st, p(self.dq), p(self.dk), p(self.dv), *ws, *shape, t["dkdv"],
+                                           t["dq"], sp), "dq")
         if marks is not None:
             marks[3].record(self.stream)
+
+
+class ClockSampler:
+    """Samples the GPU's shader (GFX) clock from a host thread while the
+    timed loops run: amdsmi's current clock, else the sysfs DPM table's
+    current level.  Reports the median, min and max of the samples in MHz."""
+
+    def __init__(self, period_s=0.01):
+        import threading
+        self.period, self.samples, self.source = period_s, [], None
+        self._stop = threading.Event()
+        self._thread = None
+        self._read = self._probe()
+
+    def _probe(self):
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            handle = amdsmi.amdsmi_get_processor_handles()[0]
+            read = lambda: float(amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.GFX)["clk"])
+            read()
+            self.source = "amdsmi GFX clock"
+            return read
+        except Exception:
+            pass
+        import glob
+        import re
+        paths = sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+        if paths:
+            def read():
+                for line in open(paths[0]):
+                    if line.strip().endswith("*"):
+                        return float(re.search(r"(\d+)\s*Mhz", line, re.I).group(1))
+                return float("nan")
+            try:
+                read()
+                self.source = f"sysfs {paths[0]}"
+                return read
+            except Exception:
+                pass
+        return None
+
+    def __enter__(self):
+        import threading
+        if self._read is not None:
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def _run(self):
+        while not self._stop.wait(self.period):
+            try:
+                self.samples.append(self._read())
+            except Exception:
+                return
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join()
+
+    def summary(self):
+        vals = sorted(v for v in self.samples if v == v and v > 0)
+        if not vals:
+            return None
+        return {"median_mhz": vals[len(vals) // 2], "min_mhz": vals[0], "max_mhz": vals[-1],
+                "samples": len(vals), "source": self.source,
+                "peak_at_this_clock_tflops": round(PEAK_BF16_TFLOPS * vals[len(vals) // 2] / 2400.0, 1)}
+
+
+def time_forward(batch, seq, device, steps, warmup):
+    """The forward alone through the drop-in kernel handle (config 1: the
+    GPU side of the CPU forward baseline): median of five timed loops."""
+    import torch
+    import mimansm1_v1_amd as mm
+    gen = torch.Generator().manual_seed(0)
+    mk = lambda h: torch.randn(batch, seq, h, DIM, generator=gen).to(torch.bfloat16).to(device)
+    q, k, v = mk(HEADS), mk(KV_HEADS), mk(KV_HEADS)
+    kern = mm.get_kernel("fwd", batch, HEADS, seq, DIM, True, HEADS // KV_HEADS)
+    loops = []
+    for _ in range(5):
+        loops.append(_timed(lambda: kern(q, k, v), steps, warmup))
+    ms = sorted(loops)[2]
+    return {"batch": batch, "seq_len": seq, "ms_fwd": round(ms, 4),
+            "fwd_tflops": round(2 * gemm_unit(batch, seq) / (ms * 1e-3) / 1e12, 2)}
 
 
 def time_workload(wl, steps, warmup, repeats=5):
@@ -544,13 +629,19 @@ def cpu_baseline(config):
     batch = B if full else 1
     q, k, v, do = R.make_inputs(batch, S, HEADS, KV_HEADS, DIM, seed=0, dtype=torch.float32,
                                 rope_sigma=(config == 4))
-    flops = 7 * gemm_unit(batch, S)       # algorithmic 7*B*H*S^2*D (gemm_unit holds the causal 1/2)
     groups = HEADS // KV_HEADS
-    R.grads(q, k, v, do, True, groups)    # warm-up
+    fwd_only = config == 1
+    if fwd_only:
+        flops = 2 * gemm_unit(batch, S)
+        run = lambda: R.attention(q, k, v, True, groups)
+    else:
+        flops = 7 * gemm_unit(batch, S)   # algorithmic 7*B*H*S^2*D (gemm_unit holds the causal 1/2)
+        run = lambda: R.grads(q, k, v, do, True, groups)
+    run()                                 # warm-up
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        R.grads(q, k, v, do, True, groups)
+        run()
         times.append(time.perf_counter() - t0)
     med = sorted(times)[1]
     model = ""
@@ -569,10 +660,12 @@ def cpu_baseline(config):
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"fp32 torch autograd of the reference math (oracle/reference.py, AT:521-530) on "
-                   f"{what}: seq {S}, 10 query / 2 KV heads, d 128, causal fwd+bwd; 1 warm-up run, "
-                   f"median of 3 runs = {med:.2f} s per fwd+bwd; algorithmic flops 7*B*H*S^2*D "
-                   f"(causal halves counted) = {flops / 1e9:.1f} GFLOP; CPU: {model}"),
+        "sample": (f"fp32 torch {'forward' if fwd_only else 'autograd'} of the reference math "
+                   f"(oracle/reference.py, AT:521-530) on {what}: seq {S}, 10 query / 2 KV heads, d 128, "
+                   f"causal {'fwd' if fwd_only else 'fwd+bwd'}; 1 warm-up run, median of 3 runs = "
+                   f"{med:.3f} s per {'fwd' if fwd_only else 'fwd+bwd'}; algorithmic flops "
+                   f"{'2' if fwd_only else '7'}*B*H*S^2*D (causal halves counted) = {flops / 1e9:.2f} GFLOP; "
+                   f"CPU: {model}"),
     }
 
 
@@ -603,7 +696,14 @@ def main(argv=None):
         return 0
 
     results = {}
+    clock = None
     for cfg in [args.config] + [c for c in args.also if c != args.config]:
+        if cfg == 1:
+            res = time_forward(CONFIGS[1]["batch"], CONFIGS[1]["seq"], device, args.steps, args.warmup)
+            results[cfg] = res
+            print(f"[bench] config 1 (forward only): {res['ms_fwd']:.4f} ms, {res['fwd_tflops']:.1f} TFLOP/s",
+                  file=sys.stderr, flush=True)
+            continue
         if cfg == SUBLAYER_CONFIG:
             res = time_sublayer(2, 8192, device, args.steps, args.warmup)
             results[cfg] = res
@@ -614,15 +714,22 @@ def main(argv=None):
         B, S = CONFIGS[cfg]["batch"], CONFIGS[cfg]["seq"]
         tiles = select_tiles(B, S, args.tiles)
         wl = Workload(lib, B, S, device, tiles, rope_sigma=(cfg == 4))
-        ms, stages, loops = time_workload(wl, args.steps, args.warmup, args.repeats)
+        if cfg == args.config:
+            with ClockSampler() as sampler:
+                ms, stages, loops = time_workload(wl, args.steps, args.warmup, args.repeats)
+            clock = sampler.summary()
+        else:
+            ms, stages, loops = time_workload(wl, args.steps, args.warmup, args.repeats)
         unit = gemm_unit(B, S)
         flops = {"fwd": 2 * unit, "dkdv": 4 * unit, "dq": 3 * unit}
+        one_stream = sum(stages.values())
         res = {
             "ms_per_step": ms,
             "tflops": 7 * unit / (ms * 1e-3) / 1e12,
             "stage_ms": stages,
+            "ms_per_step_one_stream": one_stream,
             "fwd_tflops": 2 * unit / (stages["fwd"] * 1e-3) / 1e12,
-            "bwd_tflops": 5 * unit / ((ms - stages["fwd"]) * 1e-3) / 1e12,
+            "bwd_tflops": 5 * unit / ((one_stream - stages["fwd"]) * 1e-3) / 1e12,
             "kernel_tflops": {k: flops[k] / (stages[k] * 1e-3) / 1e12 for k in flops},
             "kernel_flops": flops,
             "tiles": tiles,
@@ -687,6 +794,12 @@ def main(argv=None):
             "causal": True, "parallelism": "single GPU",
         },
         "pct_of_peak": round(100 * main_res["tflops"] / PEAK_BF16_TFLOPS, 2),
+        "gpu_clock": clock,
+        "stage_schedule": ("stage_ms, fwd/bwd_tflops, kernel_tflops and the roofline's launch time come "
+                           "from the per-stage loop, every stage on one stream with an event after each; "
+                           "ms_per_step (and value) from the step loop, which runs dQ beside dK/dV on a "
+                           "second stream when the tile record says so (tiles.overlap)"),
+        "ms_per_step_one_stream": round(main_res["ms_per_step_one_stream"], 4),
         "fwd_tflops": round(main_res["fwd_tflops"], 2),
         "bwd_tflops": round(main_res["bwd_tflops"], 2),
         "stage_ms": {k: round(v, 4) for k, v in main_res["stage_ms"].items()},
@@ -704,6 +817,7 @@ def main(argv=None):
             "traffic": traffic,
             "flops_per_launch": main_res["kernel_flops"][dom],
             "avg_launch_ms": round(main_res["stage_ms"][dom], 4),
+            "launch_timing": "HIP events on the launch stream around the stage in the one-stream per-stage loop",
         },
     }
     if "ms_per_step_autograd" in main_res:
@@ -714,11 +828,15 @@ def main(argv=None):
         if cfg == SUBLAYER_CONFIG:
             out["config5"] = res
             continue
+        if cfg == 1:
+            out["config1"] = dict(res, note="forward only (BASELINE.json config 1), the drop-in kernel handle")
+            continue
         out[f"config{cfg}"] = {
             "batch": CONFIGS[cfg]["batch"], "seq_len": CONFIGS[cfg]["seq"],
             "tflops": round(res["tflops"], 2),
             "pct_of_peak": round(100 * res["tflops"] / PEAK_BF16_TFLOPS, 2),
             "ms_per_step": round(res["ms_per_step"], 4),
+            "ms_per_step_one_stream": round(res["ms_per_step_one_stream"], 4),
             "fwd_tflops": round(res["fwd_tflops"], 2), "bwd_tflops": round(res["bwd_tflops"], 2),
             "stage_ms": {k: round(v, 4) for k, v in res["stage_ms"].items()},
             "tiles": res["tiles"],
@@ -733,6 +851,11 @@ def main(argv=None):
         out["lm_head"] = head_res
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config)
+        for cfg in results:
+            if cfg in (1, 2, 4) and cfg != args.config:
+                out[f"config{cfg}"]["cpu_baseline"] = cpu_baseline(cfg)
+                print(f"[bench] cpu baseline config {cfg}: {out[f'config{cfg}']['cpu_baseline']['value']} TFLOP/s",
+                      file=sys.stderr, flush=True)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -114,8 +114,8 @@ int mm1_attn_delta(const void* o, const void* dO, float* delta,
                    int B, int S, int H, int D, void* stream);
 
 /* Bytes of the backward workspace of a shape (0 for a bad shape): fp16 dO,
- * the scaled Delta, the dO scale and the dK/dV partial sums (2 * G fp32
- * slots of [B, S, Hkv, D] when G = H / Hkv > 1).  No counterpart in the
+ * the scaled Delta, lse2 - log2(sm_scale), the dO scale and the dK/dV
+ * partial sums (2 * G fp32 slots of [B, S, Hkv, D] when G = H / Hkv > 1).  No counterpart in the
  * reference, whose backward takes caller-zeroed fp32 dQ/dK/dV accumulators
  * instead (attention_tilelang.py:381-383). */
 size_t mm1_attn_bwd_workspace_size(int B, int S, int H, int Hkv, int D);
@@ -157,10 +157,10 @@ size_t mm1_attn_bwd_noalloc_scratch_size(int B, int S, int H, int Hkv, int D, in
  * mm1_attn_bwd_dq_tiles and mm1_attn_bwd_dkdv_reduce_tiles split the last
  * one into two launches (same results).
  *  - mm1_attn_bwd_prep: Delta from o and the state, fp16 dO and its scale,
- *    into `workspace`.  mm1_attn_bwd_prep_delta takes the caller's delta
- *    instead of o (a state from mm1_attn_prep has no O residual).  The
- *    calls below read what a prep call wrote into the same workspace; the
- *    library cannot check that one did.
+ *    and lse2 - log2(sm_scale), into `workspace`.  mm1_attn_bwd_prep_delta
+ *    takes the caller's delta instead of o (a state from mm1_attn_prep has
+ *    no O residual).  The calls below read what a prep call wrote into the
+ *    same workspace (lse2 included); the library cannot check that one did.
  *  - mm1_attn_bwd_dkdv_tiles: dK/dV.  With H == Hkv it writes bf16 dk, dv
  *    directly.  Otherwise, with the per-head tiling (1) it writes the
  *    per-query-head fp32 partial sums into `workspace` and leaves dk/dv
@@ -185,24 +185,24 @@ size_t mm1_attn_bwd_noalloc_scratch_size(int B, int S, int H, int Hkv, int D, in
  * they replace flash_delta + flash_bwd + flash_unswizzle + casts
  * (attention_tilelang.py:192-323, :380-389); no counterpart as separate
  * calls. */
-int mm1_attn_bwd_prep(const void* o, const void* dO, const void* state, size_t state_bytes,
+int mm1_attn_bwd_prep(const void* o, const void* dO, const float* lse2, const void* state, size_t state_bytes,
                       void* workspace, size_t workspace_bytes,
                       int B, int S, int H, int Hkv, int D, float sm_scale, void* stream);
-int mm1_attn_bwd_prep_delta(const void* dO, const float* delta, const void* state, size_t state_bytes,
-                            void* workspace, size_t workspace_bytes,
+int mm1_attn_bwd_prep_delta(const void* dO, const float* delta, const float* lse2, const void* state,
+                            size_t state_bytes, void* workspace, size_t workspace_bytes,
                             int B, int S, int H, int Hkv, int D, float sm_scale, void* stream);
-int mm1_attn_bwd_dkdv_tiles(const float* lse2, const void* state, size_t state_bytes, void* dk, void* dv,
+int mm1_attn_bwd_dkdv_tiles(const void* state, size_t state_bytes, void* dk, void* dv,
                             void* workspace, size_t workspace_bytes,
                             int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                             int dkdv_tiles, void* stream);
 int mm1_attn_bwd_dkdv_reduce_tiles(void* workspace, size_t workspace_bytes, void* dk, void* dv,
                                    int B, int S, int H, int Hkv, int D, int causal, int dkdv_tiles,
                                    void* stream);
-int mm1_attn_bwd_dq_tiles(const float* lse2, const void* state, size_t state_bytes, void* dq,
+int mm1_attn_bwd_dq_tiles(const void* state, size_t state_bytes, void* dq,
                           void* workspace, size_t workspace_bytes,
                           int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                           int dq_tiles, void* stream);
-int mm1_attn_bwd_dq_reduce_tiles(const float* lse2, const void* state, size_t state_bytes,
+int mm1_attn_bwd_dq_reduce_tiles(const void* state, size_t state_bytes,
                                  void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
                                  int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
                                  int dkdv_tiles, int dq_tiles, void* stream);

@@ -27,8 +27,8 @@ SIGNATURES = {
     "mm1_attn_tile_desc": (ctypes.c_char_p, [_c_int, _c_int]),
     "mm1_attn_delta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "mm1_attn_bwd_workspace_size": (_c_size, SHAPE),
-    "mm1_attn_bwd_prep": (_c_int, [_vp, _vp, _vp, _c_size, _vp, _c_size] + SHAPE + [_c_float, _vp]),
-    "mm1_attn_bwd_prep_delta": (_c_int, [_vp, _vp, _vp, _c_size, _vp, _c_size] + SHAPE + [_c_float, _vp]),
+    "mm1_attn_bwd_prep": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _c_size] + SHAPE + [_c_float, _vp]),
+    "mm1_attn_bwd_prep_delta": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _c_size] + SHAPE + [_c_float, _vp]),
     "mm1_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _vp, _vp, _vp, _c_size] + SHAPE_CS + [_vp]),
     "mm1_attn_bwd_tiles": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _vp, _vp, _vp, _c_size] + SHAPE_CS
                            + [_c_int, _c_int, _vp]),
@@ -36,10 +36,10 @@ SIGNATURES = {
                                + [_c_int, _c_int, _vp]),
     "mm1_attn_bwd_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _vp, _vp, _vp] + SHAPE_CS + [_vp]),
     "mm1_attn_bwd_noalloc_scratch_size": (_c_size, SHAPE + [_c_int]),
-    "mm1_attn_bwd_dkdv_tiles": (_c_int, [_vp, _vp, _c_size, _vp, _vp, _vp, _c_size] + SHAPE_CS + [_c_int, _vp]),
+    "mm1_attn_bwd_dkdv_tiles": (_c_int, [_vp, _c_size, _vp, _vp, _vp, _c_size] + SHAPE_CS + [_c_int, _vp]),
     "mm1_attn_bwd_dkdv_reduce_tiles": (_c_int, [_vp, _c_size, _vp, _vp] + SHAPE + [_c_int, _c_int, _vp]),
-    "mm1_attn_bwd_dq_tiles": (_c_int, [_vp, _vp, _c_size, _vp, _vp, _c_size] + SHAPE_CS + [_c_int, _vp]),
-    "mm1_attn_bwd_dq_reduce_tiles": (_c_int, [_vp, _vp, _c_size, _vp, _vp, _vp, _vp, _c_size] + SHAPE_CS
+    "mm1_attn_bwd_dq_tiles": (_c_int, [_vp, _c_size, _vp, _vp, _c_size] + SHAPE_CS + [_c_int, _vp]),
+    "mm1_attn_bwd_dq_reduce_tiles": (_c_int, [_vp, _c_size, _vp, _vp, _vp, _vp, _c_size] + SHAPE_CS
                                      + [_c_int, _c_int, _vp]),
     "mm1_attn_dispatch_order": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                          _c_int, _vp, _c_int]),

@@ -240,11 +240,11 @@ class BwdKernel(_Kernel):
                                B, S, H, Hkv, D, _stream(q.device))
         _lib.check(rc, "mm1_attn_prep")
         ws = self._workspace(lib, q.device)
-        rc = lib.mm1_attn_bwd_prep_delta(grad_out.data_ptr(), delta.data_ptr(), state.data_ptr(), state.numel(),
-                                         ws.data_ptr(), ws.numel(), B, S, H, Hkv, D, self.sm_scale,
+        rc = lib.mm1_attn_bwd_prep_delta(grad_out.data_ptr(), delta.data_ptr(), lse.data_ptr(), state.data_ptr(),
+                                         state.numel(), ws.data_ptr(), ws.numel(), B, S, H, Hkv, D, self.sm_scale,
                                          _stream(q.device))
         _lib.check(rc, "mm1_attn_bwd_prep_delta")
-        self._stages(lib, lse, state, ws, dq, dk, dv)
+        self._stages(lib, state, ws, dq, dk, dv)
 
     def run_saved(self, out, grad_out, lse, state, dq, dk, dv):
         """dQ, dK, dV from the forward's (out, lse, state) and dO."""
@@ -255,27 +255,27 @@ class BwdKernel(_Kernel):
         self._check_grads(dq, dk, dv)
         lib = _lib.load()
         ws = self._workspace(lib, out.device)
-        rc = lib.mm1_attn_bwd_prep(out.data_ptr(), grad_out.data_ptr(), state.data_ptr(), state.numel(),
-                                   ws.data_ptr(), ws.numel(), B, S, H, Hkv, D, self.sm_scale,
+        rc = lib.mm1_attn_bwd_prep(out.data_ptr(), grad_out.data_ptr(), lse.data_ptr(), state.data_ptr(),
+                                   state.numel(), ws.data_ptr(), ws.numel(), B, S, H, Hkv, D, self.sm_scale,
                                    _stream(out.device))
         _lib.check(rc, "mm1_attn_bwd_prep")
-        self._stages(lib, lse, state, ws, dq, dk, dv)
+        self._stages(lib, state, ws, dq, dk, dv)
 
     def _workspace(self, lib, device):
         B, H, S, D, Hkv = self.batch, self.heads, self.seq_len, self.dim, self.kv_heads
         return torch.empty(lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, D), dtype=torch.uint8, device=device)
 
-    def _stages(self, lib, lse, state, ws, dq, dk, dv):
+    def _stages(self, lib, state, ws, dq, dk, dv):
         B, H, S, D, Hkv = self.batch, self.heads, self.seq_len, self.dim, self.kv_heads
         shape = (B, S, H, Hkv, D, int(self.causal), self.sm_scale)
         dkdv_tiles, dq_tiles = self.tiles
         st, wsp = (state.data_ptr(), state.numel()), (ws.data_ptr(), ws.numel())
         if not self.config.get("overlap_dq", OVERLAP_DQ):
-            rc = lib.mm1_attn_bwd_dkdv_tiles(lse.data_ptr(), *st, dk.data_ptr(), dv.data_ptr(), *wsp, *shape,
-                                             dkdv_tiles, _stream(dq.device))
+            rc = lib.mm1_attn_bwd_dkdv_tiles(*st, dk.data_ptr(), dv.data_ptr(), *wsp, *shape, dkdv_tiles,
+                                             _stream(dq.device))
             _lib.check(rc, "mm1_attn_bwd_dkdv_tiles")
-            rc = lib.mm1_attn_bwd_dq_reduce_tiles(lse.data_ptr(), *st, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                                  *wsp, *shape, dkdv_tiles, dq_tiles, _stream(dq.device))
+            rc = lib.mm1_attn_bwd_dq_reduce_tiles(*st, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), *wsp, *shape,
+                                                  dkdv_tiles, dq_tiles, _stream(dq.device))
             _lib.check(rc, "mm1_attn_bwd_dq_reduce_tiles")
             return
         main = torch.cuda.current_stream(dq.device)
@@ -284,11 +284,10 @@ class BwdKernel(_Kernel):
         fork.record(main)
         side.wait_event(fork)
         try:
-            rc = lib.mm1_attn_bwd_dq_tiles(lse.data_ptr(), *st, dq.data_ptr(), *wsp, *shape, dq_tiles,
-                                           side.cuda_stream)
+            rc = lib.mm1_attn_bwd_dq_tiles(*st, dq.data_ptr(), *wsp, *shape, dq_tiles, side.cuda_stream)
             _lib.check(rc, "mm1_attn_bwd_dq_tiles")
-            rc = lib.mm1_attn_bwd_dkdv_tiles(lse.data_ptr(), *st, dk.data_ptr(), dv.data_ptr(), *wsp, *shape,
-                                             dkdv_tiles, main.cuda_stream)
+            rc = lib.mm1_attn_bwd_dkdv_tiles(*st, dk.data_ptr(), dv.data_ptr(), *wsp, *shape, dkdv_tiles,
+                                             main.cuda_stream)
             _lib.check(rc, "mm1_attn_bwd_dkdv_tiles")
             rc = lib.mm1_attn_bwd_dkdv_reduce_tiles(*wsp, dk.data_ptr(), dv.data_ptr(), B, S, H, Hkv, D,
                                                     int(self.causal), dkdv_tiles, main.cuda_stream)

@@ -8,30 +8,32 @@
 //   P_ij    = exp2(s_ij * scale2 - lse2_i)         (:297), zero above the diagonal (:298-301)
 //   dP_ij   = dO_i . V_j                           (:304)
 //   dV_j   += sum_i P_ij dO_i                      (:307)
-//   dS_ij   = bf16(P_ij (dP_ij - Delta_i) sm_scale)  (:310, rounded to bf16 for the products)
+//   dS_ij   = P_ij (dP_ij - Delta_i) sm_scale      (:310)
 //   dK_j   += sum_i dS_ij Q_i                       (:311)
 //   dQ_i   += sum_j dS_ij K_j                       (:314)
-// with the bf16 roundings at the reference's points: P before dV^T, and
-// P (dP - Delta) sm_scale before dK^T and dQ (the dQ kernel takes sm_scale
-// into P through its lse2: exp2(s scale2 - lse2 + log2 sm_scale) = P sm_scale).
+// The reference rounds P and dS to bf16 before their products and takes
+// Delta from its bf16 O; here P and dS are rounded to fp16 (11 significant
+// bits), Delta is formed from 15 significant bits of the forward's O (the
+// bf16 O and its residual byte), and all products run on fp16 copies of Q,
+// K, V and of dO scaled by a power of two 2^E (attn_delta16_kernel,
+// attn_do16_kernel).  sm_scale enters through lse = lse2 - log2(sm_scale):
+// exp2(s scale2 - lse) = P sm_scale, so dS is one multiply.
 //
 // The decomposition here is atomic-free and deterministic:
-//   * attn_delta_kernel   : Delta, one 16-lane group per two (b, s, h) rows.
-//   * attn_dkdv_pipe_kernel / attn_dkdv_kernel : key-stationary.  Each wave
-//     pair keeps 32 keys of K and V and their dK/dV accumulators in
-//     registers while it walks query tiles, which arrive in LDS by DMA
-//     (row-major; transposed operands are read with the LDS transpose read).
-//     The default (grouped) tiling gives a workgroup one 128-key tile of one
-//     KV head and walks the query tiles of all G heads of the group, so the
-//     group sum stays in registers; only the long key tiles of a causal grid
-//     are split into chunks, whose fp32 partials go to a workspace
-//     [chunk][B][S][Hkv][D].  The per-head tilings give a workgroup one
-//     (128-key tile, query head) and write a partial per head.  The partials
-//     are summed in a fixed order and rounded once (in the dQ launch's tail,
-//     or attn_dkdv_reduce_kernel).
-//   * attn_dkdv_quad_kernel : the grouped walk with the 8 waves as two quads
-//     of single-product waves over 64 keys each (fewer LDS instructions per
-//     product, bitwise the same results).
+//   * attn_delta16_kernel / attn_do16_kernel : Delta, fp16 dO and its scale
+//     (attn_delta_kernel is the reference's flash_delta on the bf16 O).
+//   * attn_dkdv_pipe_kernel : key-stationary.  Each wave pair keeps 32 keys
+//     of K and V and their dK/dV accumulators in registers while it walks
+//     query tiles, which arrive in LDS by DMA (row-major; transposed operands
+//     are read with the LDS transpose read).  The default (grouped) tiling
+//     gives a workgroup one 128-key tile of one KV head and walks the query
+//     tiles of all G heads of the group, so the group sum stays in
+//     registers; only the long key tiles of a causal grid are split into
+//     chunks, whose fp32 partials go to a workspace [chunk][B][S][Hkv][D].
+//     The per-head tiling gives a workgroup one (128-key tile, query head)
+//     and writes a partial per head.  The partials are summed in a fixed
+//     order and rounded once (in the dQ launch's tail, or
+//     attn_dkdv_reduce_kernel).
 //   * attn_dq_kernel      : query-stationary over the packed GQA row space
 //     (as in the forward): K/V tiles in LDS serve all G heads of a group and
 //     dQ is written once in bf16 -- no fp32 scratch and no un-swizzle pass.
@@ -111,12 +113,16 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 //   Delta_i = sum_d O_id dO_id in fp32, O from the bf16 output and its
 //   residual byte (lo8_decode: 15 significant bits of the forward's fp32 O);
 //   with o == nullptr the caller's Delta is copied (mm1_attn_bwd_prep_delta).
+//   It stores -Delta (the products accumulate dP - Delta onto it) and
+//   lse = lse2 - log2(sm_scale) (so exp2(s scale2 - lse) is P sm_scale, the
+//   scaled softmax weight dS is formed from), both per (b, h, s) row.
 //   do16 = fp16(dO) (E = 0), and max|dO| of the workgroup's rows in
 //   part_max[blockIdx.x].  16 lanes per (b, s, h) row, grid-stride over pairs
 //   of rows.
 __global__ __launch_bounds__(256) void attn_delta16_kernel(
     const __bf16* __restrict__ o, const uint8_t* __restrict__ o_lo, const __bf16* __restrict__ dO,
-    const float* __restrict__ delta_in, float* __restrict__ delta, _Float16* __restrict__ do16,
+    const float* __restrict__ delta_in, const float* __restrict__ lse2, float log2_sm_scale,
+    float* __restrict__ ndelta, float* __restrict__ lse, _Float16* __restrict__ do16,
     float* __restrict__ part_max, int B, int S, int H) {
   const long nrows = (long)B * S * H;
   const int c = threadIdx.x & 15;
@@ -164,7 +170,8 @@ __global__ __launch_bounds__(256) void attn_delta16_kernel(
         const int sp = (int)(bs % S);
         const int bb = (int)(bs / S);
         const long i = ((long)bb * H + hh) * S + sp;
-        delta[i] = o ? v : delta_in[i];
+        ndelta[i] = -(o ? v : delta_in[i]);
+        lse[i] = lse2[i] - log2_sm_scale;
       };
       put(row0, acc0);
       if (row0 + 1 < nrows) put(row0 + 1, acc1);
@@ -186,7 +193,8 @@ __global__ __launch_bounds__(256) void attn_delta16_kernel(
 //     keep 11 significant bits, and values below fp16's normal range (2^-14,
 //     at most 2^-6 of the largest) lose at most 2^-25 absolutely;
 //   * otherwise E = -ilogb(mdo) (2^E mdo in [1, 2)), lowered until 2^E
-//     bound < 2^15.
+//     bound < 2^15.  E reaches 133 for the smallest bf16 (subnormal) dO;
+//     2^E is applied as two factors of at most 2^67 each (exact).
 // mdo == 0 (or a non-finite maximum, which the results then carry): E = 0.
 __device__ __forceinline__ int do_scale_exp(float mdo, float mv, float sm_scale) {
   if (!(mdo > 0.f) || !isfinite(mdo) || !isfinite(mv)) return 0;
@@ -195,13 +203,18 @@ __device__ __forceinline__ int do_scale_exp(float mdo, float mv, float sm_scale)
   if (mdo >= 0x1p-8f && mdo <= 0x1p8f && bound_ok) return 0;
   int e = -ilogbf(mdo);
   if (bound > 0.f && isfinite(bound)) e = min(e, 14 - ilogbf(bound));
-  return max(-120, min(120, e));
+  return max(-126, min(134, e));
+}
+
+// x * 2^e for |e| <= 134, as two exact power-of-two multiplies.
+__device__ __forceinline__ float scale_pow2(float x, int e) {
+  return x * ldexpf(1.f, e / 2) * ldexpf(1.f, e - e / 2);
 }
 
 // E from the partial maxima; scale[0] = 2^-E, scale[1] = 2^E (the kernels
 // that consume the scaled values multiply their dQ / dK / dV by scale[0]:
 // exact, a power of two).  With E != 0 it reconverts dO -> fp16(2^E dO) and
-// scales Delta by 2^E in place; with E == 0 (attn_delta16_kernel's
+// scales -Delta by 2^E in place; with E == 0 (attn_delta16_kernel's
 // conversion stands) every workgroup leaves after reading the maxima.  Each
 // workgroup reduces the n_dmax + n_vmax partial maxima itself (a few KiB,
 // L2-resident), so no other launch sits between the maxima and the
@@ -227,10 +240,9 @@ __global__ __launch_bounds__(256) void attn_do16_kernel(
   md = fmaxf(fmaxf(wm[0][0], wm[0][1]), fmaxf(wm[0][2], wm[0][3]));
   mv = fmaxf(fmaxf(wm[1][0], wm[1][1]), fmaxf(wm[1][2], wm[1][3]));
   const int e = do_scale_exp(md, mv, sm_scale);
-  const float up = ldexpf(1.f, e);
   if (blockIdx.x == 0 && threadIdx.x == 0) {
-    scale[0] = ldexpf(1.f, -e);
-    scale[1] = up;
+    scale[0] = ldexpf(1.f, -e);                 // 2^-134 .. 2^126: subnormal at the far end
+    scale[1] = e < 128 ? ldexpf(1.f, e) : INFINITY;
   }
   if (e == 0) return;
   const long stride = (long)gridDim.x * 256;
@@ -238,10 +250,10 @@ __global__ __launch_bounds__(256) void attn_do16_kernel(
     const bf16x8 x = *reinterpret_cast<const bf16x8*>(dO + 8 * i);
     f16x8 r;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) r[t] = (_Float16)((float)x[t] * up);
+    for (int t = 0; t < 8; ++t) r[t] = (_Float16)scale_pow2((float)x[t], e);
     *reinterpret_cast<f16x8*>(do16 + 8 * i) = r;
   }
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n_delta; i += stride) delta[i] *= up;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n_delta; i += stride) delta[i] = scale_pow2(delta[i], e);
 }
 
 // ---------------------------------------------------------------------------
@@ -291,8 +303,8 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // The query tiles are 32 rows (Q, dO row-major; the transposed operands of
 // dV^T and dK^T come from the LDS transpose read), and the work on a tile is
 // spread over four segments:
-//   segment s, P wave : S(s+1) = Q(s+1) K^T                | P(s) = exp2(S(s) scale2 - lse2), -P(s) sm_scale -> mailbox | dV^T += dO(s-1)^T P(s-1)
-//   segment s, dS wave: Delta - dP(s) = Delta + dO(s) (-V)^T | dS(s-1) = (-P(s-1) sm_scale) (Delta - dP(s-1))          | dK^T += Q(s-2)^T dS(s-2)
+//   segment s, P wave : S(s+1) = Q(s+1) K^T                 | P'(s) = exp2(S(s) scale2 - lse) = P sm_scale -> mailbox | dV^T += dO(s-1)^T P'(s-1)
+//   segment s, dS wave: dP(s) - Delta = -Delta + dO(s) V^T   | dS(s-1) = P'(s-1) (dP(s-1) - Delta)                     | dK^T += Q(s-2)^T dS(s-2)
 // Within a segment each wave's VALU work (middle column) depends on no
 // product of the same segment, so it runs under the wave's own products
 // (and, with two waves per SIMD, the other wave's), and the pair meets at one
@@ -300,15 +312,18 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // (fp16) stay in the P wave's registers, dP(s-1) and dS(s-2) (fp16) in the
 // dS wave's.  Each wave starts its segment with the accumulation product
 // (the P wave runs dV^T before S(s+1)), whose tile was published segments
-// earlier: its first operand fragments and the wave's lse2 / Delta vector
+// earlier: its first operand fragments and the wave's lse / -Delta vector
 // are read before the previous barrier, so right after a barrier the waves
 // issue products instead of all waiting on the LDS together.
 //
 // Operands: the fp16 copies q16, k16, v16 of the forward state and do16 =
-// fp16(2^E dO) with Delta scaled alike (attn_do16_kernel), so dP, dS and
-// the accumulators carry the factor 2^E; the epilogue multiplies dK and dV
-// by scale[0] = 2^-E.  F32OUT: dk / dv (and the partials) are fp32, the
-// values the bf16 path rounds.
+// fp16(2^E dO) with -Delta scaled alike (attn_do16_kernel), so dP, dS and
+// the accumulators carry the factor 2^E; the epilogue multiplies dK by
+// scale[0] = 2^-E.  The P wave's exponentials take lse = lse2 -
+// log2(sm_scale) and give P' = P sm_scale, which goes to the mailbox as is
+// (dS = P' (dP - Delta)) and, rounded to fp16, into dV^T: the epilogue
+// multiplies dV by 2^-E / sm_scale.  F32OUT: dk / dv (and the partials)
+// are fp32, the values the bf16 path rounds.
 //
 // Tile x of the ring lives in slot x % NSTAGE; it is first read in segment
 // x-1 and last in segment x+2, so segment s refills slot (s-3) % NSTAGE with
@@ -319,7 +334,7 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 template <int NSTAGE, bool CAUSAL, bool GROUP, bool RAGGED, bool F32OUT>
 __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
-    const _Float16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
+    const _Float16* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ ndelta,
     const float* __restrict__ scale, float* __restrict__ ws_dk, float* __restrict__ ws_dv,
     void* __restrict__ dk, void* __restrict__ dv,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, KeyTileOrder order,
@@ -334,7 +349,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   constexpr int QPW = 8 / DW;             // row quads of a 32-row tile each copying wave copies
   constexpr int BQ = 32;                  // query positions per tile
   constexpr int QT = BQ * HD * 2;         // one 32 x 128 fp16 operand tile
-  constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse2 x 32 | Delta x 32], 1 KiB aligned
+  constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse x 32 | -Delta x 32], 1 KiB aligned
   constexpr int MBOX = 32 * 32 * 4;       // one 32 x 32 fp32 P block
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + NP * 2 * KB * MBOX];
 
@@ -401,10 +416,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
 
   const int q_begin = CAUSAL ? kt * 128 : 0;
   const long qstride = (long)H * HD;
-  // walk head hh: Q / dO rows at grp_rows + hh*HD, lse2 / Delta at
-  // vec_src + hh*S (lanes 0-31 lse2, lanes 32-63 Delta)
+  // walk head hh: Q / dO rows at grp_rows + hh*HD, lse / -Delta at
+  // vec_src + hh*S (lanes 0-31 lse, lanes 32-63 -Delta)
   const long grp_rows = ((long)b * S * H + g * G + hbase) * HD;
-  const float* vec_src = (h ? delta : lse2) + ((long)b * H + g * G + hbase) * S + l32;
+  const float* vec_src = (h ? ndelta : lse) + ((long)b * H + g * G + hbase) * S + l32;
 
   // Position tiles are walked from the sequence end down to q_begin, so the
   // workgroups that start together read the same rows together; the first
@@ -419,7 +434,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     }
   };
   // LDS DMA, per copying wave and tile: row quads w, w + DW, ... of Q and of dO;
-  // wave 0 adds the lse2 | Delta vector.  (quad & 3) == (w & 3) for every quad
+  // wave 0 adds the lse | -Delta vector.  (quad & 3) == (w & 3) for every quad
   // of the wave, so one per-lane offset serves all of them.
   const uint32_t dma_off = tile_lane_off(qstride, tid);
   const uint32_t lds_smem = __builtin_amdgcn_readfirstlane(lds_addr(smem));
@@ -460,11 +475,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     advance(ih, itl);
   }
 
-  // This lane's key rows of K (P wave) or -V (dS wave) as the B operands,
-  // one per key block.  With -V the dP product accumulates onto Delta and
-  // gives Delta - dP, and the mailbox carries -P sm_scale, so dS = P (dP -
-  // Delta) sm_scale is one multiply; negating an fp16 is exact, so every
-  // value is the one of the unnegated arithmetic up to its sign.
+  // This lane's key rows of K (P wave) or V (dS wave) as the B operands,
+  // one per key block.  The dP product accumulates onto -Delta and gives
+  // dP - Delta, and the mailbox carries P sm_scale, so dS = P (dP - Delta)
+  // sm_scale is one multiply.
   f16x8 breg[KB][8];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
@@ -472,10 +486,6 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     const _Float16* src = (pwave ? k : v) + ((long)(b * S + kk) * Hkv + g) * HD + 8 * h;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = *reinterpret_cast<const f16x8*>(src + 16 * ks);
-    if (!pwave) {
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) breg[kb][ks] = neg8(breg[kb][ks]);
-    }
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) pin(breg[kb][ks]);
   }
@@ -537,7 +547,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // from tiles published by earlier barriers, so that after the barrier the
   // first product waits for no LDS read: the first PFT transposed fragments
   // of the accumulation product (P wave: dO(s) for dV^T; dS wave: Q(s-1) for
-  // dK^T) and, for the P wave, the lse2 vector of tile s+1 (its
+  // dK^T) and, for the P wave, the lse vector of tile s+1 (its
   // exponentials).  The dS wave reads Delta of tile s just before its dP
   // product, which starts from it (holding it across the barrier cost more
   // registers than the read).
@@ -554,15 +564,14 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   auto nothing = [](int) MM1_INLINE {};
   if (pwave) {
     product(smem, snext, nothing);
-    read_vec(reinterpret_cast<const float*>(smem + 2 * QT));        // lse2 of tile 0
+    read_vec(reinterpret_cast<const float*>(smem + 2 * QT));        // lse of tile 0
   }
-  const float neg_sm_scale = -sm_scale;
 
   // Segment s.  tn, tc, tp, tp2: ring slots of tiles s+1, s, s-1, s-2.
   // CUR: s < n_u; PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a
   // later segment reads what this one publishes (mailbox, ring).  In the last
   // segment with CUR, S(s+1) reads a slot holding another tile (or nothing
-  // yet) and is discarded, as is the lse2 read for segment s+1: every read
+  // yet) and is discarded, as is the lse read for segment s+1: every read
   // stays inside the ring.
   auto segment = [&](const char* tn, const char* tc, const char* tp, const char* tp2, int refill,
                      int s, auto role, auto cur, auto prev, auto prev2, auto sync) MM1_INLINE {
@@ -581,7 +590,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) lse4[a4] = nvec[a4];
       }
-      // P = exp2(S*scale2 - lse2) of register r of every key block
+      // P' = exp2(S*scale2 - lse) = P sm_scale of register r of every key block
       auto exp_at = [&](int r) MM1_INLINE {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -647,7 +656,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
           for (int a4 = 0; a4 < 4; ++a4) {
             f32x4 v4;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c] * neg_sm_scale;
+            for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c];
             *reinterpret_cast<f32x4*>(mb + kb * (MBOX / 4) + 256 * a4) = v4;
           }
           pb[kb][0] = pbn[kb][0];
@@ -657,9 +666,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
         read_vec(reinterpret_cast<const float*>(tn + 2 * QT));
       }
     } else {
-      // dS(s-1) = (-P(s-1) sm_scale) (Delta - dP(s-1)), computed in place of
-      // the mailbox values (-P sm_scale: the P wave, which has the shorter
-      // chain, applies the scale) between the products of
+      // dS(s-1) = P'(s-1) (dP(s-1) - Delta), computed in place of the
+      // mailbox values P' = P sm_scale between the products of
       // dK^T += Q(s-2)^T dS(s-2)
       f32x16 dsv[KB];
       if constexpr (PREV) {
@@ -714,9 +722,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
           sbp[kb][1] = sbn[kb][1];
         }
       }
-      // Delta - dP(s) = Delta + dO(s) (-V)^T, used by the next segment
+      // dP(s) - Delta = -Delta + dO(s) V^T, used by the next segment
       if constexpr (CUR) {
-        f32x16 dlt;   // Delta of tile s in the D layout (register r: query 8*(r/4) + 4*h + r%4)
+        f32x16 dlt;   // -Delta of tile s in the D layout (register r: query 8*(r/4) + 4*h + r%4)
         const float* dll = reinterpret_cast<const float*>(tc + 2 * QT) + BQ;
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) {
@@ -782,8 +790,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
 
   // D layout of dK^T / dV^T: register r of block db holds column
   // d = 32*db + 8*(r/4) + 4*h + (r%4) of this lane's key row.  The sums
-  // carry the factor 2^E of do16; times 2^-E (exact) they are dK, dV.
-  const float unscale = scale[0];
+  // carry the factor 2^E of do16 (dV also sm_scale, from P'): times 2^-E
+  // (and 1 / sm_scale) they are dK, dV.
+  const float unscale = pwave ? scale[0] / sm_scale : scale[0];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int key = kw0 + 32 * kb + l32;
@@ -917,7 +926,7 @@ __device__ __forceinline__ void tail_reduce(const TailReduce& red, int tid, int 
 template <int NW, int NSTAGE, bool CAUSAL, bool F32OUT = false>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
-    const _Float16* __restrict__ dO, const float* __restrict__ lse2, const float* __restrict__ delta,
+    const _Float16* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ ndelta,
     const float* __restrict__ scale, void* __restrict__ dq_out,
     int B, int S, int H, int Hkv, int G, float scale2, float sm_scale, int n_tiles, TailReduce red,
     const DispatchOrder ord) {
@@ -977,10 +986,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
       doreg[ks] = *reinterpret_cast<const f16x8*>(dO + roff + 16 * ks + 8 * h);
     }
     const long li = ((long)b * H + g * G + hh) * S + qp;
-    // P sm_scale = exp2(s scale2 - (lse2 - log2 sm_scale)): dS comes out
-    // scaled, and is rounded to fp16 with the scale in it, as the reference's
-    lse_i = lse2[li] - log2f(sm_scale);
-    dl_i = delta[li];
+    // P sm_scale = exp2(s scale2 - lse), lse = lse2 - log2 sm_scale (from the
+    // workspace): dS comes out scaled, and is rounded to fp16 with the scale
+    // in it, as the reference's
+    lse_i = lse[li];
+    dl_i = ndelta[li];   // -Delta
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) { pin(qreg[ks]); pin(doreg[ks]); }
     __asm__ volatile("" : "+v"(lse_i), "+v"(dl_i));
@@ -992,9 +1002,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     }
   }
 
-  f32x16 negdl;   // the initial accumulator of every dP^T block
+  f32x16 negdl;   // the initial accumulator of every dP^T block: -Delta
 #pragma unroll
-  for (int r = 0; r < 16; ++r) negdl[r] = -dl_i;
+  for (int r = 0; r < 16; ++r) negdl[r] = dl_i;
   f32x16 dqacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) dqacc[db] = zero16();
@@ -1130,13 +1140,14 @@ hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int 
 // then do16 = fp16(2^E dO), Delta *= 2^E and the scale cells: what the
 // dK/dV and dQ kernels read from the workspace.
 hipError_t launch_bwd_prep(const void* o, const uint8_t* o_lo, const void* dO, const float* delta_in,
-                           const float* vmax, char* ws, int B, int S, int H, int Hkv, float sm_scale,
-                           hipStream_t stream) {
+                           const float* lse2, const float* vmax, char* ws, int B, int S, int H, int Hkv,
+                           float sm_scale, hipStream_t stream) {
   const BwdWs w = bwd_ws(B, S, H, Hkv);
   float* delta = reinterpret_cast<float*>(ws + w.delta);
   float* dmax = reinterpret_cast<float*>(ws + w.dmax);
   hipLaunchKernelGGL(attn_delta16_kernel, dim3(kDeltaBlocks), dim3(256), 0, stream,
-                     static_cast<const __bf16*>(o), o_lo, static_cast<const __bf16*>(dO), delta_in, delta,
+                     static_cast<const __bf16*>(o), o_lo, static_cast<const __bf16*>(dO), delta_in, lse2,
+                     log2f(sm_scale), delta, reinterpret_cast<float*>(ws + w.lse),
                      reinterpret_cast<_Float16*>(ws + w.do16), dmax, B, S, H);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -1199,10 +1210,10 @@ TailReduce make_reduce(const float* partials, void* dk, void* dv, bool f32, int 
 // The fp16 operands and scaled values the dK/dV and dQ kernels read.
 struct BwdOperands {
   const _Float16 *q, *k, *v, *dO;
-  const float *lse2, *delta, *scale;
+  const float *lse, *ndelta, *scale;
 };
 
-BwdOperands bwd_operands(const char* state, const char* ws, const float* lse2, int B, int S, int H, int Hkv) {
+BwdOperands bwd_operands(const char* state, const char* ws, int B, int S, int H, int Hkv) {
   const FwdState f = fwd_state(B, S, H, Hkv);
   const BwdWs w = bwd_ws(B, S, H, Hkv);
   BwdOperands o;
@@ -1210,8 +1221,8 @@ BwdOperands bwd_operands(const char* state, const char* ws, const float* lse2, i
   o.k = reinterpret_cast<const _Float16*>(state + f.k16);
   o.v = reinterpret_cast<const _Float16*>(state + f.v16);
   o.dO = reinterpret_cast<const _Float16*>(ws + w.do16);
-  o.lse2 = lse2;
-  o.delta = reinterpret_cast<const float*>(ws + w.delta);
+  o.lse = reinterpret_cast<const float*>(ws + w.lse);
+  o.ndelta = reinterpret_cast<const float*>(ws + w.delta);
   o.scale = reinterpret_cast<const float*>(ws + w.scale);
   return o;
 }
@@ -1242,7 +1253,7 @@ static void launch_dkdv_pipe(const BwdOperands& op, float* ws_dk, float* ws_dv, 
   const int ws_rows = ws_slots(B, S, H, Hkv, causal, GROUP ? 0 : 1).rows;
 #define MM1_DKDV_PIPE(CS, RG)                                                                              \
   hipLaunchKernelGGL((attn_dkdv_pipe_kernel<7, CS, GROUP, RG, F32OUT>), grid, block, 0, stream, op.q, op.k, op.v, \
-                     op.dO, op.lse2, op.delta, op.scale, ws_dk, ws_dv, dk, dv, B, S, H, Hkv, G, scale2,         \
+                     op.dO, op.lse, op.ndelta, op.scale, ws_dk, ws_dv, dk, dv, B, S, H, Hkv, G, scale2,         \
                      sm_scale, order, L, C, *ord, ws_rows)
   if (causal) {
     if (ragged) MM1_DKDV_PIPE(true, true);
@@ -1257,11 +1268,10 @@ static void launch_dkdv_pipe(const BwdOperands& op, float* ws_dk, float* ws_dv, 
 // dK/dV from the state and a prepared workspace.  variant: 0 = over the
 // whole GQA group per key tile (chunked by dkdv_plan), 1 = one workgroup per
 // (key tile, query head).  f32: dk / dv are fp32.
-hipError_t launch_bwd_dkdv(const char* state, char* ws, const float* lse2, void* dk, void* dv, bool f32,
-                           int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
-                           hipStream_t stream) {
+hipError_t launch_bwd_dkdv(const char* state, char* ws, void* dk, void* dv, bool f32, int B, int S, int H,
+                           int Hkv, bool causal, float sm_scale, int variant, hipStream_t stream) {
   const float scale2 = sm_scale * 1.4426950408889634f;
-  const BwdOperands op = bwd_operands(state, ws, lse2, B, S, H, Hkv);
+  const BwdOperands op = bwd_operands(state, ws, B, S, H, Hkv);
   const WsSlots w = ws_slots(B, S, H, Hkv, causal, variant);
   float* ws_dk = H / Hkv > 1 ? reinterpret_cast<float*>(ws + bwd_ws(B, S, H, Hkv).partials) : nullptr;
   float* ws_dv = ws_dk ? ws_dk + (long)w.slots * w.stride : nullptr;
@@ -1296,10 +1306,10 @@ static void launch_dq_t(const BwdOperands& op, void* dq, int B, int S, int H, in
   dim3 grid(n_blocks), block(NW * 64);
   if (causal)
     hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, true, F32OUT>), grid, block, 0, stream, op.q, op.k, op.v, op.dO,
-                       op.lse2, op.delta, op.scale, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
+                       op.lse, op.ndelta, op.scale, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
   else
     hipLaunchKernelGGL((attn_dq_kernel<NW, NSTAGE, false, F32OUT>), grid, block, 0, stream, op.q, op.k, op.v, op.dO,
-                       op.lse2, op.delta, op.scale, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
+                       op.lse, op.ndelta, op.scale, dq, B, S, H, Hkv, G, scale2, sm_scale, n_qtiles, red, ord);
 }
 
 // dQ from the state and a prepared workspace.  variant: 0 = 4 waves x
@@ -1307,11 +1317,11 @@ static void launch_dq_t(const BwdOperands& op, void* dq, int B, int S, int H, in
 // CU).  reduce: also sum the dK/dV partials that tiling dkdv_variant left in
 // the workspace into dk, dv (what launch_bwd_reduce does), in the dQ grid's
 // tail.  f32: dq (and dk, dv) are fp32.
-hipError_t launch_bwd_dq(const char* state, char* ws, const float* lse2, void* dq, bool reduce, void* dk,
-                         void* dv, bool f32, int B, int S, int H, int Hkv, bool causal, float sm_scale,
-                         int variant, int dkdv_variant, hipStream_t stream) {
+hipError_t launch_bwd_dq(const char* state, char* ws, void* dq, bool reduce, void* dk, void* dv, bool f32,
+                         int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant, int dkdv_variant,
+                         hipStream_t stream) {
   const float scale2 = sm_scale * 1.4426950408889634f;
-  const BwdOperands op = bwd_operands(state, ws, lse2, B, S, H, Hkv);
+  const BwdOperands op = bwd_operands(state, ws, B, S, H, Hkv);
   const float* partials = reduce ? reinterpret_cast<const float*>(ws + bwd_ws(B, S, H, Hkv).partials) : nullptr;
   // with n_red = 1 << 30 every workgroup of the grid takes a slice
   const TailReduce red = make_reduce(partials, dk, dv, f32, B, S, H, Hkv, causal, dkdv_variant);

@@ -22,16 +22,15 @@ hipError_t launch_cvt16(const void* x, _Float16* x16, long n, hipStream_t stream
 hipError_t launch_delta(const void* o, const void* dO, float* delta, int B, int S, int H,
                         hipStream_t stream);
 hipError_t launch_bwd_prep(const void* o, const uint8_t* o_lo, const void* dO, const float* delta_in,
-                           const float* vmax, char* ws, int B, int S, int H, int Hkv, float sm_scale,
-                           hipStream_t stream);
-hipError_t launch_bwd_dkdv(const char* state, char* ws, const float* lse2, void* dk, void* dv, bool f32,
-                           int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant,
-                           hipStream_t stream);
+                           const float* lse2, const float* vmax, char* ws, int B, int S, int H, int Hkv,
+                           float sm_scale, hipStream_t stream);
+hipError_t launch_bwd_dkdv(const char* state, char* ws, void* dk, void* dv, bool f32, int B, int S, int H,
+                           int Hkv, bool causal, float sm_scale, int variant, hipStream_t stream);
 hipError_t launch_bwd_reduce(const char* ws, void* dk, void* dv, bool f32, int B, int S, int H, int Hkv,
                              bool causal, int dkdv_variant, hipStream_t stream);
-hipError_t launch_bwd_dq(const char* state, char* ws, const float* lse2, void* dq, bool reduce, void* dk,
-                         void* dv, bool f32, int B, int S, int H, int Hkv, bool causal, float sm_scale,
-                         int variant, int dkdv_variant, hipStream_t stream);
+hipError_t launch_bwd_dq(const char* state, char* ws, void* dq, bool reduce, void* dk, void* dv, bool f32,
+                         int B, int S, int H, int Hkv, bool causal, float sm_scale, int variant, int dkdv_variant,
+                         hipStream_t stream);
 size_t bwd_partials_bytes(int B, int S, int H, int Hkv, bool causal, int variant);
 size_t qknorm_bwd_workspace_bytes();
 hipError_t launch_qknorm_fwd(const void* qkv, const float* wq, const float* wk, const float* cos_t,
@@ -233,9 +232,10 @@ int fwd_any(const void* q, const void* k, const void* v, void* o, float* lse2, b
                                   B, S, H, Hkv, causal != 0, sm_scale, variant, static_cast<hipStream_t>(stream)));
 }
 
-int bwd_prep_any(const void* o, const void* dO, const float* delta_in, const void* state, size_t state_bytes,
-                 void* ws, size_t ws_bytes, int B, int S, int H, int Hkv, int D, float sm_scale, void* stream) {
-  if (!dO) return MM1_E_NULL;
+int bwd_prep_any(const void* o, const void* dO, const float* delta_in, const float* lse2, const void* state,
+                 size_t state_bytes, void* ws, size_t ws_bytes, int B, int S, int H, int Hkv, int D, float sm_scale,
+                 void* stream) {
+  if (!dO || !lse2) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
   if (rc) return rc;
   if (bad_scale(sm_scale)) return MM1_E_SCALE;
@@ -243,15 +243,14 @@ int bwd_prep_any(const void* o, const void* dO, const float* delta_in, const voi
   if (!aligned16(dO) || (o && !aligned16(o))) return MM1_E_ALIGN;
   const mm1::FwdState f = mm1::fwd_state(B, S, H, Hkv);
   const char* st = static_cast<const char*>(state);
-  return from_hip(mm1::launch_bwd_prep(o, reinterpret_cast<const uint8_t*>(st + f.olo), dO, delta_in,
+  return from_hip(mm1::launch_bwd_prep(o, reinterpret_cast<const uint8_t*>(st + f.olo), dO, delta_in, lse2,
                                        reinterpret_cast<const float*>(st + f.vmax), static_cast<char*>(ws), B, S,
                                        H, Hkv, sm_scale, static_cast<hipStream_t>(stream)));
 }
 
-int bwd_dkdv(const float* lse2, const void* state, size_t state_bytes, void* dk, void* dv, bool f32, void* ws,
-             size_t ws_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale, int tiles,
-             void* stream) {
-  if (!lse2 || !dk || !dv) return MM1_E_NULL;
+int bwd_dkdv(const void* state, size_t state_bytes, void* dk, void* dv, bool f32, void* ws, size_t ws_bytes,
+             int B, int S, int H, int Hkv, int D, int causal, float sm_scale, int tiles, void* stream) {
+  if (!dk || !dv) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
   if (rc) return rc;
   if (bad_scale(sm_scale)) return MM1_E_SCALE;
@@ -259,18 +258,17 @@ int bwd_dkdv(const float* lse2, const void* state, size_t state_bytes, void* dk,
   if (!aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
   const int variant = pick_tiles(MM1_TILES_DKDV, tiles);
   if (variant < 0) return MM1_E_TILES;
-  rc = from_hip(mm1::launch_bwd_dkdv(static_cast<const char*>(state), static_cast<char*>(ws), lse2, dk, dv, f32,
-                                     B, S, H, Hkv, causal != 0, sm_scale, variant,
-                                     static_cast<hipStream_t>(stream)));
+  rc = from_hip(mm1::launch_bwd_dkdv(static_cast<const char*>(state), static_cast<char*>(ws), dk, dv, f32, B, S,
+                                     H, Hkv, causal != 0, sm_scale, variant, static_cast<hipStream_t>(stream)));
   if (rc == MM1_OK && H / Hkv > 1) record_layout(layout_of(ws, variant, B, S, H, Hkv, causal != 0));
   return rc;
 }
 
 // dq, and with `reduce` the group sum of the dK/dV partials in the same launch.
-int bwd_dq(const float* lse2, const void* state, size_t state_bytes, void* dq, void* dk, void* dv, bool reduce,
-           bool f32, void* ws, size_t ws_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-           int tiles, int dkdv_tiles, void* stream) {
-  if (!lse2 || !dq) return MM1_E_NULL;
+int bwd_dq(const void* state, size_t state_bytes, void* dq, void* dk, void* dv, bool reduce, bool f32, void* ws,
+           size_t ws_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale, int tiles,
+           int dkdv_tiles, void* stream) {
+  if (!dq) return MM1_E_NULL;
   if (reduce && (!dk || !dv)) return MM1_E_NULL;
   int rc = check_shape(B, S, H, Hkv, D);
   if (rc) return rc;
@@ -282,8 +280,8 @@ int bwd_dq(const float* lse2, const void* state, size_t state_bytes, void* dq, v
   if (variant < 0 || dkdv_variant < 0) return MM1_E_TILES;
   if (reduce && H / Hkv > 1 && !layout_matches(layout_of(ws, dkdv_variant, B, S, H, Hkv, causal != 0)))
     return MM1_E_LAYOUT;
-  return from_hip(mm1::launch_bwd_dq(static_cast<const char*>(state), static_cast<char*>(ws), lse2, dq, reduce,
-                                     dk, dv, f32, B, S, H, Hkv, causal != 0, sm_scale, variant, dkdv_variant,
+  return from_hip(mm1::launch_bwd_dq(static_cast<const char*>(state), static_cast<char*>(ws), dq, reduce, dk, dv,
+                                     f32, B, S, H, Hkv, causal != 0, sm_scale, variant, dkdv_variant,
                                      static_cast<hipStream_t>(stream)));
 }
 
@@ -315,12 +313,13 @@ int bwd_all(const void* o, const void* dO, const float* lse2, const void* state,
   if ((rc = check_state_ws(state, state_bytes, ws, ws_bytes, B, S, H, Hkv))) return rc;
   if (!aligned16(o) || !aligned16(dO) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv)) return MM1_E_ALIGN;
   if (pick_tiles(MM1_TILES_DQ, dq_tiles) < 0 || pick_tiles(MM1_TILES_DKDV, dkdv_tiles) < 0) return MM1_E_TILES;
-  if ((rc = bwd_prep_any(o, dO, nullptr, state, state_bytes, ws, ws_bytes, B, S, H, Hkv, D, sm_scale, stream)))
+  if ((rc = bwd_prep_any(o, dO, nullptr, lse2, state, state_bytes, ws, ws_bytes, B, S, H, Hkv, D, sm_scale,
+                         stream)))
     return rc;
-  if ((rc = bwd_dkdv(lse2, state, state_bytes, dk, dv, f32, ws, ws_bytes, B, S, H, Hkv, D, causal, sm_scale,
-                     dkdv_tiles, stream)))
+  if ((rc = bwd_dkdv(state, state_bytes, dk, dv, f32, ws, ws_bytes, B, S, H, Hkv, D, causal, sm_scale, dkdv_tiles,
+                     stream)))
     return rc;
-  return bwd_dq(lse2, state, state_bytes, dq, dk, dv, true, f32, ws, ws_bytes, B, S, H, Hkv, D, causal, sm_scale,
+  return bwd_dq(state, state_bytes, dq, dk, dv, true, f32, ws, ws_bytes, B, S, H, Hkv, D, causal, sm_scale,
                 dq_tiles, dkdv_tiles, stream);
 }
 
@@ -395,26 +394,27 @@ size_t mm1_attn_bwd_workspace_size(int B, int S, int H, int Hkv, int D) {
   return mm1::bwd_ws(B, S, H, Hkv).bytes;
 }
 
-int mm1_attn_bwd_prep(const void* o, const void* dO, const void* state, size_t state_bytes, void* workspace,
-                      size_t workspace_bytes, int B, int S, int H, int Hkv, int D, float sm_scale, void* stream) {
+int mm1_attn_bwd_prep(const void* o, const void* dO, const float* lse2, const void* state, size_t state_bytes,
+                      void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv, int D, float sm_scale,
+                      void* stream) {
   if (!o) return MM1_E_NULL;
-  return bwd_prep_any(o, dO, nullptr, state, state_bytes, workspace, workspace_bytes, B, S, H, Hkv, D, sm_scale,
-                      stream);
-}
-
-int mm1_attn_bwd_prep_delta(const void* dO, const float* delta, const void* state, size_t state_bytes,
-                            void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv, int D,
-                            float sm_scale, void* stream) {
-  if (!delta) return MM1_E_NULL;
-  return bwd_prep_any(nullptr, dO, delta, state, state_bytes, workspace, workspace_bytes, B, S, H, Hkv, D,
+  return bwd_prep_any(o, dO, nullptr, lse2, state, state_bytes, workspace, workspace_bytes, B, S, H, Hkv, D,
                       sm_scale, stream);
 }
 
-int mm1_attn_bwd_dkdv_tiles(const float* lse2, const void* state, size_t state_bytes, void* dk, void* dv,
-                            void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv, int D, int causal,
-                            float sm_scale, int dkdv_tiles, void* stream) {
-  return bwd_dkdv(lse2, state, state_bytes, dk, dv, false, workspace, workspace_bytes, B, S, H, Hkv, D, causal,
-                  sm_scale, dkdv_tiles, stream);
+int mm1_attn_bwd_prep_delta(const void* dO, const float* delta, const float* lse2, const void* state,
+                            size_t state_bytes, void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv,
+                            int D, float sm_scale, void* stream) {
+  if (!delta) return MM1_E_NULL;
+  return bwd_prep_any(nullptr, dO, delta, lse2, state, state_bytes, workspace, workspace_bytes, B, S, H, Hkv, D,
+                      sm_scale, stream);
+}
+
+int mm1_attn_bwd_dkdv_tiles(const void* state, size_t state_bytes, void* dk, void* dv, void* workspace,
+                            size_t workspace_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
+                            int dkdv_tiles, void* stream) {
+  return bwd_dkdv(state, state_bytes, dk, dv, false, workspace, workspace_bytes, B, S, H, Hkv, D, causal, sm_scale,
+                  dkdv_tiles, stream);
 }
 
 int mm1_attn_bwd_dkdv_reduce_tiles(void* workspace, size_t workspace_bytes, void* dk, void* dv, int B, int S,
@@ -422,18 +422,17 @@ int mm1_attn_bwd_dkdv_reduce_tiles(void* workspace, size_t workspace_bytes, void
   return bwd_reduce(workspace, workspace_bytes, dk, dv, B, S, H, Hkv, D, causal, dkdv_tiles, stream);
 }
 
-int mm1_attn_bwd_dq_tiles(const float* lse2, const void* state, size_t state_bytes, void* dq, void* workspace,
-                          size_t workspace_bytes, int B, int S, int H, int Hkv, int D, int causal, float sm_scale,
-                          int dq_tiles, void* stream) {
-  return bwd_dq(lse2, state, state_bytes, dq, nullptr, nullptr, false, false, workspace, workspace_bytes, B, S, H,
-                Hkv, D, causal, sm_scale, dq_tiles, -1, stream);
+int mm1_attn_bwd_dq_tiles(const void* state, size_t state_bytes, void* dq, void* workspace, size_t workspace_bytes,
+                          int B, int S, int H, int Hkv, int D, int causal, float sm_scale, int dq_tiles, void* stream) {
+  return bwd_dq(state, state_bytes, dq, nullptr, nullptr, false, false, workspace, workspace_bytes, B, S, H, Hkv, D,
+                causal, sm_scale, dq_tiles, -1, stream);
 }
 
-int mm1_attn_bwd_dq_reduce_tiles(const float* lse2, const void* state, size_t state_bytes, void* dq, void* dk,
-                                 void* dv, void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv,
-                                 int D, int causal, float sm_scale, int dkdv_tiles, int dq_tiles, void* stream) {
-  return bwd_dq(lse2, state, state_bytes, dq, dk, dv, true, false, workspace, workspace_bytes, B, S, H, Hkv, D,
-                causal, sm_scale, dq_tiles, dkdv_tiles, stream);
+int mm1_attn_bwd_dq_reduce_tiles(const void* state, size_t state_bytes, void* dq, void* dk, void* dv,
+                                 void* workspace, size_t workspace_bytes, int B, int S, int H, int Hkv, int D,
+                                 int causal, float sm_scale, int dkdv_tiles, int dq_tiles, void* stream) {
+  return bwd_dq(state, state_bytes, dq, dk, dv, true, false, workspace, workspace_bytes, B, S, H, Hkv, D, causal,
+                sm_scale, dq_tiles, dkdv_tiles, stream);
 }
 
 int mm1_attn_bwd_tiles(const void* o, const void* dO, const float* lse2, const void* state, size_t state_bytes,
@@ -476,13 +475,13 @@ int mm1_attn_bwd_noalloc(const void* o, const void* dO, const float* lse2, const
   const mm1::FwdState f = mm1::fwd_state(B, S, H, Hkv);
   const char* sp = static_cast<const char*>(state);
   char* wp = static_cast<char*>(ws);
-  rc = from_hip(mm1::launch_bwd_prep(o, reinterpret_cast<const uint8_t*>(sp + f.olo), dO, nullptr,
+  rc = from_hip(mm1::launch_bwd_prep(o, reinterpret_cast<const uint8_t*>(sp + f.olo), dO, nullptr, lse2,
                                      reinterpret_cast<const float*>(sp + f.vmax), wp, B, S, H, Hkv, sm_scale, st));
   if (rc) return rc;
-  rc = from_hip(mm1::launch_bwd_dkdv(sp, wp, lse2, dk, dv, false, B, S, H, Hkv, causal != 0, sm_scale, 0, st));
+  rc = from_hip(mm1::launch_bwd_dkdv(sp, wp, dk, dv, false, B, S, H, Hkv, causal != 0, sm_scale, 0, st));
   if (rc) return rc;
-  return from_hip(mm1::launch_bwd_dq(sp, wp, lse2, dq, true, dk, dv, false, B, S, H, Hkv, causal != 0, sm_scale, 0,
-                                     0, st));
+  return from_hip(mm1::launch_bwd_dq(sp, wp, dq, true, dk, dv, false, B, S, H, Hkv, causal != 0, sm_scale, 0, 0,
+                                     st));
 }
 
 size_t mm1_attn_bwd_noalloc_scratch_size(int B, int S, int H, int Hkv, int D, int causal) {

@@ -38,14 +38,15 @@ inline FwdState fwd_state(int B, int S, int H, int Hkv) {
 
 // Backward workspace:
 //   do16     [B,S,H,D] fp16   fp16(2^E dO)
-//   delta    [B,H,S]   fp32   2^E Delta
+//   delta    [B,H,S]   fp32   -2^E Delta
+//   lse      [B,H,S]   fp32   lse2 - log2(sm_scale): exp2(s scale2 - lse) = P sm_scale
 //   dmax     [kDeltaBlocks] fp32  partial maxima of |dO|
 //   scale    [64] fp32        scale[0] = 2^-E, scale[1] = 2^E
 //   partials                  the dK/dV partial sums (fp32), as large as the
 //                             per-head tiling needs: 2 * G slots of
 //                             [B,S,Hkv,D] (none when G == 1)
 struct BwdWs {
-  size_t do16, delta, dmax, scale, partials, bytes;
+  size_t do16, delta, lse, dmax, scale, partials, bytes;
 };
 
 inline BwdWs bwd_ws(int B, int S, int H, int Hkv) {
@@ -54,7 +55,8 @@ inline BwdWs bwd_ws(int B, int S, int H, int Hkv) {
   BwdWs w;
   w.do16 = 0;
   w.delta = w.do16 + align256(nq * 2);
-  w.dmax = w.delta + align256((size_t)B * H * S * 4);
+  w.lse = w.delta + align256((size_t)B * H * S * 4);
+  w.dmax = w.lse + align256((size_t)B * H * S * 4);
   w.scale = w.dmax + align256(kDeltaBlocks * 4);
   w.partials = w.scale + 256;
   w.bytes = w.partials + (G > 1 ? align256((size_t)2 * G * nkv * 4) : 0);

@@ -75,15 +75,16 @@ def fwd(lib, q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=FAKE, st=FAKE, st_bytes=None, B
 def test_state_and_workspace_sizes(lib):
     """The forward state holds fp16 Q, K, V (2 bytes a value), the O residual
     (1 byte) and the max|V| partials; the backward workspace fp16 dO, the
-    scaled Delta, the dO maxima and scale, and 2 * G fp32 slots of partial
-    sums (none when G == 1).  Every region is 256-byte aligned."""
+    scaled Delta, lse2 - log2(sm_scale), the dO maxima and scale, and 2 * G
+    fp32 slots of partial sums (none when G == 1).  Every region is 256-byte
+    aligned."""
     up = lambda x: (x + 255) // 256 * 256
     B, S, H, Hkv = 2, 100, 10, 2
     nq, nkv = B * S * H * 128, B * S * Hkv * 128
     assert lib.mm1_attn_fwd_state_size(B, S, H, Hkv, 128) == up(2 * nq) + 2 * up(2 * nkv) + up(nq) + up(512 * 4)
-    base = up(2 * nq) + up(4 * B * H * S) + up(1024 * 4) + 256
+    base = up(2 * nq) + 2 * up(4 * B * H * S) + up(1024 * 4) + 256
     assert lib.mm1_attn_bwd_workspace_size(B, S, H, Hkv, 128) == base + up(2 * 5 * nkv * 4)
-    assert lib.mm1_attn_bwd_workspace_size(B, S, 4, 4, 128) == up(2 * B * S * 4 * 128) + up(4 * B * 4 * S) \
+    assert lib.mm1_attn_bwd_workspace_size(B, S, 4, 4, 128) == up(2 * B * S * 4 * 128) + 2 * up(4 * B * 4 * S) \
         + up(1024 * 4) + 256
     assert lib.mm1_attn_bwd_workspace_size(B, S, 10, 3, 128) == 0   # invalid shape
     assert lib.mm1_attn_fwd_state_size(B, S, 10, 2, 64) == 0
@@ -134,16 +135,19 @@ def test_bwd_argument_errors(lib):
     assert bwd(ws=FAKE + 4) == -6
     assert bwd(dq=FAKE + 2) == -6
     sz = (B, S, H, Hkv, 128)
-    assert lib.mm1_attn_bwd_prep(None, FAKE, FAKE, nst, FAKE, need, *sz, 0.1, None) == -1
-    assert lib.mm1_attn_bwd_prep(FAKE, FAKE, FAKE, nst, FAKE, need - 8, *sz, 0.1, None) == -4
-    assert lib.mm1_attn_bwd_prep(FAKE, FAKE, FAKE, nst, FAKE, need, *sz, 0.0, None) == -5
-    assert lib.mm1_attn_bwd_prep_delta(FAKE, None, FAKE, nst, FAKE, need, *sz, 0.1, None) == -1
-    assert lib.mm1_attn_bwd_prep_delta(FAKE + 2, FAKE, FAKE, nst, FAKE, need, *sz, 0.1, None) == -6
+    assert lib.mm1_attn_bwd_prep(None, FAKE, FAKE, FAKE, nst, FAKE, need, *sz, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_prep(FAKE, FAKE, None, FAKE, nst, FAKE, need, *sz, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_prep(FAKE, FAKE, FAKE, FAKE, nst, FAKE, need - 8, *sz, 0.1, None) == -4
+    assert lib.mm1_attn_bwd_prep(FAKE, FAKE, FAKE, FAKE, nst, FAKE, need, *sz, 0.0, None) == -5
+    assert lib.mm1_attn_bwd_prep_delta(FAKE, None, FAKE, FAKE, nst, FAKE, need, *sz, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_prep_delta(FAKE, FAKE, None, FAKE, nst, FAKE, need, *sz, 0.1, None) == -1
+    assert lib.mm1_attn_bwd_prep_delta(FAKE + 2, FAKE, FAKE, FAKE, nst, FAKE, need, *sz, 0.1, None) == -6
     cs = sz + (1, 0.1)
-    assert lib.mm1_attn_bwd_dq_tiles(FAKE, FAKE, nst, None, FAKE, need, *cs, 0, None) == -1
-    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, nst, FAKE, FAKE, None, FAKE, need, *cs, 0, 0, None) == -1
-    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, nst, FAKE, FAKE, FAKE, None, 0, *cs, 0, 0, None) == -1
-    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, nst, FAKE, FAKE, FAKE, FAKE + 4, need, *cs, 0, 0,
+    assert lib.mm1_attn_bwd_dq_tiles(FAKE, nst, None, FAKE, need, *cs, 0, None) == -1
+    assert lib.mm1_attn_bwd_dkdv_tiles(FAKE, nst, None, FAKE, FAKE, need, *cs, 0, None) == -1
+    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, nst, FAKE, FAKE, None, FAKE, need, *cs, 0, 0, None) == -1
+    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, nst, FAKE, FAKE, FAKE, None, 0, *cs, 0, 0, None) == -1
+    assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, nst, FAKE, FAKE, FAKE, FAKE + 4, need, *cs, 0, 0,
                                             None) == -6
     assert lib.mm1_attn_bwd_dkdv_reduce_tiles(None, 0, FAKE, FAKE, *sz, 1, 0, None) == -1
     assert lib.mm1_attn_bwd_dkdv_reduce_tiles(FAKE, need - 1, FAKE, FAKE, *sz, 1, 0, None) == -4
@@ -170,14 +174,14 @@ def test_reduce_refuses_a_workspace_without_matching_partials(lib):
     cs = (B, S, H, Hkv, 128, 1, 0.1)
     for t in range(lib.mm1_attn_tile_count(1)):
         assert lib.mm1_attn_bwd_dkdv_reduce_tiles(ws, need, FAKE, FAKE, B, S, H, Hkv, 128, 1, t, None) == E_LAYOUT
-        assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, FAKE, nst, FAKE, FAKE, FAKE, ws, need, *cs, t, 0,
+        assert lib.mm1_attn_bwd_dq_reduce_tiles(FAKE, nst, FAKE, FAKE, FAKE, ws, need, *cs, t, 0,
                                                 None) == E_LAYOUT
     # argument errors still come first, and a tiling out of range is MM1_E_TILES
     assert lib.mm1_attn_bwd_dkdv_reduce_tiles(ws, need, FAKE, FAKE, B, S, H, Hkv, 128, 1, 99, None) == -7
     assert lib.mm1_attn_bwd_dkdv_reduce_tiles(None, 0, FAKE, FAKE, B, S, H, Hkv, 128, 1, 0, None) == -1
     # the dQ call without the sum needs no record
-    assert lib.mm1_attn_bwd_dq_tiles(FAKE, FAKE, nst, FAKE, ws, need, *cs, 9, None) == -7
-    assert lib.mm1_attn_bwd_dkdv_tiles(FAKE, FAKE, nst, FAKE, FAKE, ws, need, *cs, 9, None) == -7
+    assert lib.mm1_attn_bwd_dq_tiles(FAKE, nst, FAKE, ws, need, *cs, 9, None) == -7
+    assert lib.mm1_attn_bwd_dkdv_tiles(FAKE, nst, FAKE, FAKE, ws, need, *cs, 9, None) == -7
 
 
 def test_layout_record_is_keyed_by_address_only():
