@@ -37,6 +37,12 @@
 #include "attn_layout.h"
 #include "mm1_common.h"
 
+// 1: the forward stores its fp16 copy of Q after the prologue's wait
+// (store_q16); 0: with the loads, before it.
+#ifndef MM1_FWD_Q16_LATE
+#define MM1_FWD_Q16_LATE 1
+#endif
+
 namespace mm1 {
 
 constexpr float kRescaleThreshold = 8.0f;   // log2 units
@@ -88,7 +94,7 @@ __device__ __forceinline__ void load_q16(f16x8 (&qreg)[8], const __bf16* q, _Flo
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
       qreg[ks] = bf16_to_f16(*reinterpret_cast<const bf16x8*>(q + roff + 16 * ks + 8 * h));
-    if (q16) {
+    if (!MM1_FWD_Q16_LATE && q16) {
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) *reinterpret_cast<f16x8*>(q16 + roff + 16 * ks + 8 * h) = qreg[ks];
     }
@@ -100,6 +106,16 @@ __device__ __forceinline__ void load_q16(f16x8 (&qreg)[8], const __bf16* q, _Flo
 #pragma unroll
       for (int t = 0; t < 8; ++t) qreg[ks][t] = (_Float16)0.f;
     }
+  }
+}
+
+// The fp16 copy of the wave's query rows (q16 != nullptr), stored after the
+// prologue's wait for its K / V copies: the wait counts stores too, so a
+// store issued before it would hold the first tile back.
+__device__ __forceinline__ void store_q16(const f16x8 (&qreg)[8], _Float16* q16, long roff, bool valid, int h) {
+  if (MM1_FWD_Q16_LATE && q16 && valid) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) *reinterpret_cast<f16x8*>(q16 + roff + 16 * ks + 8 * h) = qreg[ks];
   }
 }
 
@@ -207,7 +223,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   const int rr = rw0 + l32;
   const int qpos = rr / G;
   const int hq = rr - qpos * G;
-  load_q16(qreg, q, q16, ((long)(b * S + qpos) * H + g * G + hq) * HD, rr < R, h);
+  const long qoff = ((long)(b * S + qpos) * H + g * G + hq) * HD;
+  load_q16(qreg, q, q16, qoff, rr < R, h);
 
   f32x16 oacc[4];
 #pragma unroll
@@ -216,6 +233,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_kernel(
   const LdsBases lb = make_lds_bases(lane);
   wait_dma();
   __syncthreads();
+  store_q16(qreg, q16, qoff, rr < R, h);
 
   // One key tile; the loop below runs it NSTAGE times per trip so the ring
   // slot (and every LDS offset) is a compile-time constant.
@@ -374,7 +392,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   const int rr = rw0 + l32;
   const int qpos = rr / G;
   const int hq = rr - qpos * G;
-  load_q16(qreg, q, q16, ((long)(b * S + qpos) * H + g * G + hq) * HD, rr < R, h);
+  const long qoff = ((long)(b * S + qpos) * H + g * G + hq) * HD;
+  load_q16(qreg, q, q16, qoff, rr < R, h);
 
   f32x16 oacc[4];
 #pragma unroll
@@ -384,6 +403,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_pp_kernel(
   const LdsBases lb = make_lds_bases(lane);
   wait_dma();
   __syncthreads();
+  store_q16(qreg, q16, qoff, rr < R, h);
 
   // part 1 of tile kt from K slot J
   auto part1 = [&](auto jslot, int kt) {

@@ -9,7 +9,10 @@ namespace mm1 {
 
 // Grid sizes of the conversion kernels: one partial maximum per workgroup.
 constexpr int kCvtBlocks = 512;     // attn_cvt16_kernel (K, V, Q)
-constexpr int kDeltaBlocks = 1024;  // attn_delta16_kernel (max|dO|)
+#ifndef MM1_DELTA_BLOCKS
+#define MM1_DELTA_BLOCKS 1024
+#endif
+constexpr int kDeltaBlocks = MM1_DELTA_BLOCKS;  // attn_delta16_kernel (max|dO|)
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
