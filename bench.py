@@ -20,7 +20,9 @@ against the bf16 dense MFMA peak (the fp16 products of the kernels run at the
 same rate); ``cpu_baseline`` is the fp32 reference math (oracle, torch
 autograd) timed on this host's cores on the same workload (or one batch
 element of it when host RAM is short), and each extra config carries its own;
-``gpu_clock`` is the shader clock sampled while the timed loops ran.
+``gpu_clock`` is the shader clock the GPU holds under the same step run back
+to back for two seconds after the timed loops (``pct_of_clock_peak`` relates
+the value to the MFMA peak at that clock).
 """
 from __future__ import annotations
 
@@ -213,72 +215,81 @@ class Workload:
             marks[3].record(self.stream)
 
 
-class ClockSampler:
-    """Samples the GPU's shader (GFX) clock from a host thread while the
-    timed loops run: amdsmi's current clock, else the sysfs DPM table's
-    current level.  Reports the median, min and max of the samples in MHz."""
+def _clock_reader():
+    """A function returning the GPU's current shader (GFX) clock in MHz, and
+    its source: amdsmi's GPU metrics (the mean over the XCDs), else its clock
+    info, else the sysfs DPM table's current level; (None, None) if none."""
+    try:
+        import amdsmi
+        amdsmi.amdsmi_init()
+        handle = amdsmi.amdsmi_get_processor_handles()[0]
 
-    def __init__(self, period_s=0.01):
-        import threading
-        self.period, self.samples, self.source = period_s, [], None
-        self._stop = threading.Event()
-        self._thread = None
-        self._read = self._probe()
+        def metrics():
+            clks = [c for c in amdsmi.amdsmi_get_gpu_metrics_info(handle)["current_gfxclks"]
+                    if isinstance(c, (int, float)) and 0 < c < 65535]
+            return sum(clks) / len(clks)
 
-    def _probe(self):
-        try:
-            import amdsmi
-            amdsmi.amdsmi_init()
-            handle = amdsmi.amdsmi_get_processor_handles()[0]
-            read = lambda: float(amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.GFX)["clk"])
-            read()
-            self.source = "amdsmi GFX clock"
-            return read
-        except Exception:
-            pass
-        import glob
-        import re
-        paths = sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
-        if paths:
-            def read():
-                for line in open(paths[0]):
-                    if line.strip().endswith("*"):
-                        return float(re.search(r"(\d+)\s*Mhz", line, re.I).group(1))
-                return float("nan")
+        def info():
+            return float(amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.GFX)["clk"])
+
+        for read, src in ((metrics, "amdsmi gpu_metrics current_gfxclks (mean over XCDs)"),
+                          (info, "amdsmi clock info (GFX)")):
             try:
                 read()
-                self.source = f"sysfs {paths[0]}"
-                return read
+                return read, src
             except Exception:
                 pass
+    except Exception:
+        pass
+    import glob
+    import re
+    paths = sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+    if paths:
+        def sysfs():
+            for line in open(paths[0]):
+                if line.strip().endswith("*"):
+                    return float(re.search(r"(\d+)\s*Mhz", line, re.I).group(1))
+            return float("nan")
+        try:
+            sysfs()
+            return sysfs, f"sysfs {paths[0]}"
+        except Exception:
+            pass
+    return None, None
+
+
+def sustained_clock(step, seconds=2.0, settle=0.5):
+    """The shader clock the GPU holds under the timed workload: runs `step`
+    back to back for `seconds` and reads the clock after each batch of steps
+    (a device synchronisation apart) once `settle` seconds have passed -- the
+    SMU's readings lag the load by a fraction of a second, so samples taken
+    during a short timed loop read the idle clock.  Median, min, max in MHz."""
+    import time
+    import torch
+    read, source = _clock_reader()
+    if read is None:
         return None
-
-    def __enter__(self):
-        import threading
-        if self._read is not None:
-            self._thread = threading.Thread(target=self._run, daemon=True)
-            self._thread.start()
-        return self
-
-    def _run(self):
-        while not self._stop.wait(self.period):
+    samples = []
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(4):
+            step()
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+        if t >= settle:
             try:
-                self.samples.append(self._read())
+                samples.append(read())
             except Exception:
-                return
-
-    def __exit__(self, *exc):
-        self._stop.set()
-        if self._thread is not None:
-            self._thread.join()
-
-    def summary(self):
-        vals = sorted(v for v in self.samples if v == v and v > 0)
-        if not vals:
-            return None
-        return {"median_mhz": vals[len(vals) // 2], "min_mhz": vals[0], "max_mhz": vals[-1],
-                "samples": len(vals), "source": self.source,
-                "peak_at_this_clock_tflops": round(PEAK_BF16_TFLOPS * vals[len(vals) // 2] / 2400.0, 1)}
+                break
+        if t >= seconds:
+            break
+    vals = sorted(v for v in samples if v == v and v > 0)
+    if not vals:
+        return None
+    med = vals[len(vals) // 2]
+    return {"median_mhz": round(med, 1), "min_mhz": round(vals[0], 1), "max_mhz": round(vals[-1], 1),
+            "samples": len(vals), "seconds": seconds, "source": source,
+            "peak_at_this_clock_tflops": round(PEAK_BF16_TFLOPS * med / 2400.0, 1)}
 
 
 def time_forward(batch, seq, device, steps, warmup):
@@ -714,12 +725,9 @@ def main(argv=None):
         B, S = CONFIGS[cfg]["batch"], CONFIGS[cfg]["seq"]
         tiles = select_tiles(B, S, args.tiles)
         wl = Workload(lib, B, S, device, tiles, rope_sigma=(cfg == 4))
+        ms, stages, loops = time_workload(wl, args.steps, args.warmup, args.repeats)
         if cfg == args.config:
-            with ClockSampler() as sampler:
-                ms, stages, loops = time_workload(wl, args.steps, args.warmup, args.repeats)
-            clock = sampler.summary()
-        else:
-            ms, stages, loops = time_workload(wl, args.steps, args.warmup, args.repeats)
+            clock = sustained_clock(wl.step)
         unit = gemm_unit(B, S)
         flops = {"fwd": 2 * unit, "dkdv": 4 * unit, "dq": 3 * unit}
         one_stream = sum(stages.values())
@@ -795,6 +803,8 @@ def main(argv=None):
         },
         "pct_of_peak": round(100 * main_res["tflops"] / PEAK_BF16_TFLOPS, 2),
         "gpu_clock": clock,
+        "pct_of_clock_peak": (round(100 * main_res["tflops"] / clock["peak_at_this_clock_tflops"], 2)
+                              if clock else None),
         "stage_schedule": ("stage_ms, fwd/bwd_tflops, kernel_tflops and the roofline's launch time come "
                            "from the per-stage loop, every stage on one stream with an event after each; "
                            "ms_per_step (and value) from the step loop, which runs dQ beside dK/dV on a "

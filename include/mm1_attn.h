@@ -30,9 +30,10 @@
  *
  * The forward state.  The forward leaves in a caller-owned buffer
  * (mm1_attn_fwd_state_size bytes) what the backward reads: the fp16 copies
- * of q, k, v, the residual O - bf16(O) of its fp32 output rounded to bf16
- * (so the backward's Delta = rowsum(O dO) sees 16 significant bits of O),
- * and max|V|.  A caller keeps it with (o, lse2) until the backward, as the
+ * of q, k, v, one residual byte per value of its fp32 output O (the 8
+ * mantissa bits below bf16's, so the backward's Delta = rowsum(O dO) sees
+ * 15 significant bits of O: the bf16 o and this byte) and partial maxima of
+ * |V|.  A caller keeps it with (o, lse2) until the backward, as the
  * reference's FlashAttention.forward saves (q, k, v, out, lse)
  * (attention_tilelang.py:365).
  *
@@ -137,9 +138,13 @@ int mm1_attn_bwd(const void* o, const void* dO, const float* lse2,
  * serving loops, harnesses that forbid hipMalloc.  No counterpart in the
  * reference.  It calls no allocating routine: the backward workspace of the
  * default tilings goes to a static device array of
- * MM1_NOALLOC_SCRATCH_BYTES (256 MiB) that each device the library runs on
- * holds from the library's load until the process ends (a device-side
- * static of the code object, not a hipMalloc).
+ * MM1_NOALLOC_SCRATCH_BYTES (256 MiB), a device-side static of the library's
+ * code object (not a hipMalloc).  A device maps it when the first
+ * mm1_attn_bwd_noalloc call runs there (the HIP runtime then loads the code
+ * object that holds it) and holds it until the process ends; loading the
+ * library and calling its other entry points do not map it (they map the
+ * kernels' code objects, about 2 MiB; tests/test_gpu_memory.py measures
+ * both).
  * mm1_attn_bwd_noalloc_scratch_size() gives the bytes a shape needs (about
  * 150 MiB at the training shapes of 16,384 tokens); a shape needing more
  * returns MM1_E_SCRATCH.  Every call on one device shares that device's

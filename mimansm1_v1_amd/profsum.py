@@ -19,6 +19,7 @@ dispatch of the calibration runs).
 from __future__ import annotations
 
 import argparse
+import re
 import csv
 import json
 import sqlite3
@@ -32,18 +33,40 @@ SHORT = {
     "attn_dq_kernel": "dq",
     "attn_dkdv_reduce_kernel": "reduce",
     "attn_delta_kernel": "delta",
+    "attn_delta16_kernel": "delta16",
+    "attn_do16_kernel": "do16",
+    "attn_cvt16_kernel": "cvt16",
 }
 
 
+def demangle(name: str) -> str:
+    """`mm1::kernel<args>` for this library's mangled kernel names (the
+    profiler records some of them mangled, and binutils' demangler predates
+    the _Float16 mangling they contain); other names unchanged."""
+    m = re.match(r"_ZN3mm1(\d+)", name)
+    if not m:
+        return name
+    n = int(m.group(1))
+    rest = name[m.end():]
+    base = rest[:n]
+    rest = rest[n:]
+    if not rest.startswith("I"):
+        return f"mm1::{base}"
+    args = []
+    for kind, val in re.findall(r"L([ib])(\d+)E", rest[:rest.find("EEv") + 1] if "EEv" in rest else rest):
+        args.append(("true" if val == "1" else "false") if kind == "b" else val)
+    return f"mm1::{base}<{', '.join(args)}>"
+
+
 def kernel_key(name: str) -> str:
-    base = name.replace("void ", "").split("(")[0].split("<")[0]
+    base = demangle(name).replace("void ", "").split("(")[0].split("<")[0]
     return base.split("::")[-1]
 
 
 def trace_table(db: str):
     con = sqlite3.connect(db)
     rows = con.execute("select name, total_calls, average, percentage from top_kernels").fetchall()
-    return [(kernel_key(n), n.split("(")[0].replace("void ", ""), c, avg, pct) for n, c, avg, pct in rows]
+    return [(kernel_key(n), demangle(n).split("(")[0].replace("void ", ""), c, avg, pct) for n, c, avg, pct in rows]
 
 
 def _median(xs):
@@ -78,7 +101,7 @@ def dispatch_stats(spans):
 def trace_dispatches(db: str):
     con = sqlite3.connect(db)
     spans = con.execute("select name, start, end from kernels").fetchall()
-    return dispatch_stats([(n.split("(")[0].replace("void ", ""), s, e) for n, s, e in spans])
+    return dispatch_stats([(demangle(n).split("(")[0].replace("void ", ""), s, e) for n, s, e in spans])
 
 
 def counter_means(path: str):

@@ -12,7 +12,9 @@ For each shape and kernel (attention_fwd, attention_bwd -- keyed
 compiled gfx950 tilings are timed on synthetic inputs and the winner is
 written to the tile store at once, so an interrupted run keeps what it
 measured and a re-run skips what is known.  The reference's SwiGLU and LM-head
-jobs (tune.py:59-64) belong to kernels this library does not build.
+jobs (tune.py:59-64) are not run: this library builds those kernels
+(`csrc/swiglu.hip`, `csrc/lm_head.hip`) with one gfx950 tiling each, so there
+is nothing to choose; their `get_kernel` handles return that tiling.
 
     python -m mimansm1_v1_amd.tune                 # both shapes
     python -m mimansm1_v1_amd.tune --stage 0       # just 8 x 2048
