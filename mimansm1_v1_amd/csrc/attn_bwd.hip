@@ -285,6 +285,13 @@ __device__ __forceinline__ int key_tile_item(int slot, int nbh, int n_kt, KeyTil
   return kt < n_kt ? kt * nbh + part / o.q : -1;
 }
 
+template <int V>
+using ic = std::integral_constant<int, V>;
+template <class T>
+struct is_ic : std::false_type {};
+template <int V>
+struct is_ic<std::integral_constant<int, V>> : std::true_type {};
+
 // Calls f(integral_constant<J>) for J = 0 .. N-1 while it returns true.
 template <int J, int N, class F>
 __device__ __forceinline__ void unroll_while(F&& f) {
@@ -349,9 +356,19 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   constexpr int QPW = 8 / DW;             // row quads of a 32-row tile each copying wave copies
   constexpr int BQ = 32;                  // query positions per tile
   constexpr int QT = BQ * HD * 2;         // one 32 x 128 fp16 operand tile
-  constexpr int BUF = 2 * QT + 1024;      // Q, dO, [lse x 32 | -Delta x 32], 1 KiB aligned
+  // LDS: three rings of NSTAGE slots -- Q tiles, dO tiles, [lse x 32 |
+  // -Delta x 32] vectors -- then the mailboxes.  Every read of a Q tile lies
+  // below 64 KiB (it takes the per-lane bases of make_lds_bases plus a
+  // constant in the offset field); dO tiles and vectors are read through
+  // per-lane bases that hold their ring's offset (below).
+  constexpr int QR = 0;                   // Q ring
+  constexpr int DR = NSTAGE * QT;         // dO ring
+  constexpr int VR = 2 * NSTAGE * QT;     // vector ring
+  constexpr int VSLOT = 256;
+  constexpr int MB0 = VR + NSTAGE * VSLOT;
   constexpr int MBOX = 32 * 32 * 4;       // one 32 x 32 fp32 P block
-  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF + NP * 2 * KB * MBOX];
+  static_assert(QR + NSTAGE * QT + 4096 <= 0x10000, "Q reads must reach every Q slot by the offset field");
+  __shared__ __attribute__((aligned(1024))) char smem[MB0 + NP * 2 * KB * MBOX];
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
@@ -412,7 +429,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // mailbox of this pair: two slots of KB blocks; a block is
   // [register group a4][lane] x 4 floats, so each 16-byte access of a wave
   // is one contiguous 1 KiB row
-  float* const mbox = reinterpret_cast<float*>(smem + NSTAGE * BUF + pair * 2 * KB * MBOX) + lane * 4;
+  float* const mbox = reinterpret_cast<float*>(smem + MB0 + pair * 2 * KB * MBOX) + lane * 4;
 
   const int q_begin = CAUSAL ? kt * 128 : 0;
   const long qstride = (long)H * HD;
@@ -445,15 +462,16 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
     const int p0 = tile_p0(t);
     const long rows = grp_rows + (long)hh * HD + (long)p0 * qstride;
     const float* vs = vec_src + (long)hh * S;
-    const uint32_t l = lds_smem + slot * BUF;
+    const uint32_t lq = lds_smem + QR + slot * QT, ld = lds_smem + DR + slot * QT;
+    const uint32_t lv = lds_smem + VR + slot * VSLOT;
     if (!decltype(may_be_partial)::value || p0 + BQ <= S) {
 #pragma unroll
       for (int i = 0; i < QPW; ++i) {
         const int quad = w + DW * i;
-        dma16_sbase(dma_off, q + rows + (long)(4 * quad) * qstride, l + quad * 1024);
-        dma16_sbase(dma_off, dO + rows + (long)(4 * quad) * qstride, l + QT + quad * 1024);
+        dma16_sbase(dma_off, q + rows + (long)(4 * quad) * qstride, lq + quad * 1024);
+        dma16_sbase(dma_off, dO + rows + (long)(4 * quad) * qstride, ld + quad * 1024);
       }
-      if (w == 0) dma4(vs + p0, l + 2 * QT);
+      if (w == 0) dma4(vs + p0, lv);
     } else {   // same DMA count per wave as a full tile
       const int L = tid & 63;
 #pragma unroll
@@ -462,10 +480,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
         const int row = 4 * quad + (L >> 4);
         const int chunk = (L & 15) ^ swz(row);
         const long src = rows + (long)min(row, S - p0 - 1) * qstride + 8 * chunk;
-        dma16(q + src, l + quad * 1024);
-        dma16(dO + src, l + QT + quad * 1024);
+        dma16(q + src, lq + quad * 1024);
+        dma16(dO + src, ld + quad * 1024);
       }
-      if (w == 0) dma4(vs + min(p0, S - 1 - l32), l + 2 * QT);
+      if (w == 0) dma4(vs + min(p0, S - 1 - l32), lv);
     }
   };
   int itl = u0 / HW, ih = u0 - itl * HW;      // issue cursor
@@ -506,37 +524,95 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   f32x16 dpp[KB];      // dS wave: dP(s-1)
   f16x8 sbp[KB][2];    // dS wave: dS(s-2) as the B operand of dK^T
   const LdsBases lb = make_lds_bases(lane);
+  // Reads.  The ring slots of the walk's segments are compile-time constants
+  // (the walk is unrolled by the ring depth), so each read is a per-lane
+  // base plus a constant in the ds instruction's 16-bit offset field.  The
+  // dO and vector rings lie past 64 KiB: their reads take per-lane bases
+  // that hold the ring's offset, opaque to the compiler (it would otherwise
+  // fold the offset into the constant and add it back with a VALU
+  // instruction per read).  Each role sets the bases it reads with: the P
+  // wave dO^T (transposed) and the lse vector, the dS wave dO rows and the
+  // -Delta vector.  The last two segments, whose slots depend on the walk's
+  // length, take a run-time slot and plain addresses.
+  using lds_cp = const MM1_LDS char*;
+  lds_cp dbase[8], vbase;
+  auto set_bases = [&](bool pw) MM1_INLINE {
+    const lds_cp d = (lds_cp)smem + DR;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      dbase[i] = d + (pw ? lb.tr[i >> 1][i & 1] : (lb.row ^ (32 * i)));
+      __asm__ volatile("" : "+v"(dbase[i]));
+    }
+    vbase = (lds_cp)smem + VR + 16 * h;
+    __asm__ volatile("" : "+v"(vbase));
+  };
+  // fragments of the tile in ring slot `sl` (an integral_constant): rows of Q
+  // / dO (the A operands of S / dP), transposed fragments (blk, ks) of Q / dO
+  // (the A operands of dK^T / dV^T), 4 of a lane's 16 per-row vector values
+  // (byte offset `vec`: 0 lse, 4*BQ -Delta; rows 8*a4 + 4*h .. +3)
+  auto slot_of = [](auto sl) MM1_INLINE { return (int)sl; };
+  auto q_rows = [&](auto sl, int ks) MM1_INLINE { return rows_a(smem + QR + slot_of(sl) * QT, lb, 0, ks); };
+  auto q_tr = [&](auto sl, int blk, int ks) MM1_INLINE {
+    return tr_a(smem + QR + slot_of(sl) * QT, lb, blk, ks);
+  };
+  auto do_rows = [&](auto sl, int ks) MM1_INLINE {
+    if constexpr (is_ic<decltype(sl)>::value)
+      return *reinterpret_cast<const MM1_LDS f16x8*>(dbase[ks] + decltype(sl)::value * QT);
+    else
+      return rows_a(smem + DR + sl * QT, lb, 0, ks);
+  };
+  auto do_tr = [&](auto sl, int blk, int ks) MM1_INLINE {
+    if constexpr (is_ic<decltype(sl)>::value) {
+      f16x8 out;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const f16x4 v4 = __builtin_bit_cast(
+            f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                       (MM1_LDS fp16x4_tr*)(dbase[2 * blk + r] + (decltype(sl)::value * QT + 4096 * ks))));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[4 * r + e] = v4[e];
+      }
+      return out;
+    } else {
+      return tr_a(smem + DR + sl * QT, lb, blk, ks);
+    }
+  };
+  auto vec4 = [&](auto sl, int vec, int a4) MM1_INLINE {
+    if constexpr (is_ic<decltype(sl)>::value)
+      return *reinterpret_cast<const MM1_LDS f32x4*>(vbase + (decltype(sl)::value * VSLOT + vec + 32 * a4));
+    else
+      return *reinterpret_cast<const f32x4*>(smem + VR + sl * VSLOT + vec + 32 * a4 + 16 * h);
+  };
   wait_dma();
   __syncthreads();
   // S = Q K^T / dP = dO V^T of one tile, per key block (D layout: register r
   // holds query 8*(r/4) + 4*h + (r%4) of the tile, lane l32 holds key
-  // kw0 + 32*kb + l32); each row fragment is read once for all key blocks
-  // (accumulated onto c0)
-  auto product_onto = [&](const char* t, f32x16 (&sacc)[KB], const f32x16& c0,
+  // kw0 + 32*kb + l32); each row fragment (rows(ks)) is read once for all
+  // key blocks (accumulated onto c0)
+  auto product_onto = [&](auto&& rows, f32x16 (&sacc)[KB], const f32x16& c0,
                           auto&& between) MM1_INLINE {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) sacc[kb] = c0;
     mfma_chain<8, MM1_DKDV_PF_ROWS>(
-        [&](int ks) MM1_INLINE { return rows_a(t, lb, 0, ks); },
+        [&](int ks) MM1_INLINE { return rows(ks); },
         [&](int ks, const f16x8& fa) MM1_INLINE {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) sacc[kb] = mfma32h(fa, breg[kb][ks], sacc[kb]);
         },
         between);
   };
-  auto product = [&](const char* t, f32x16 (&sacc)[KB], auto&& between) MM1_INLINE {
-    product_onto(t, sacc, zero16(), between);
+  auto product = [&](auto&& rows, f32x16 (&sacc)[KB], auto&& between) MM1_INLINE {
+    product_onto(rows, sacc, zero16(), between);
   };
   // dV^T += dO^T P (P wave) / dK^T += Q^T dS (dS wave) of one tile: product
-  // i = 4*kh + db takes the transposed fragment (db, kh) of tile t and the B
-  // operand bop[kb][kh]; its first PFT fragments were read before the
-  // segment's barrier (first)
+  // i = 4*kh + db takes the transposed fragment tr(i) = (db, kh) of the tile
+  // and the B operand bop[kb][kh]; its first PFT fragments were read before
+  // the segment's barrier (first)
   constexpr int PFT = MM1_DKDV_PF_TR;
-  auto tr_frag = [&](const char* t, int i) MM1_INLINE { return tr_a(t, lb, i & 3, i >> 2); };
-  auto accumulate_tile = [&](const f16x8 (&first)[PFT], const char* t, const f16x8 (&bop)[KB][2],
+  auto accumulate_tile = [&](const f16x8 (&first)[PFT], auto&& tr, const f16x8 (&bop)[KB][2],
                              auto&& between) MM1_INLINE {
     mfma_chain_from<8, PFT>(
-        first, [&](int i) MM1_INLINE { return tr_frag(t, i); },
+        first, [&](int i) MM1_INLINE { return tr(i); },
         [&](int i, const f16x8& a) MM1_INLINE {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) accumulate(acc[kb][i & 3], a, bop[kb][i >> 2]);
@@ -553,28 +629,35 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // registers than the read).
   f16x8 nfa[PFT];
   f32x4 nvec[4];
-  auto read_first = [&](const char* t) MM1_INLINE {
+  auto read_first = [&](auto&& tr) MM1_INLINE {
 #pragma unroll
-    for (int i = 0; i < PFT; ++i) nfa[i] = tr_frag(t, i);
+    for (int i = 0; i < PFT; ++i) nfa[i] = tr(i);
   };
-  auto read_vec = [&](const float* vsrc) MM1_INLINE {
+  auto read_lse = [&](auto sl) MM1_INLINE {
 #pragma unroll
-    for (int a4 = 0; a4 < 4; ++a4) nvec[a4] = *reinterpret_cast<const f32x4*>(vsrc + 8 * a4 + 4 * h);
+    for (int a4 = 0; a4 < 4; ++a4) nvec[a4] = vec4(sl, 0, a4);
   };
   auto nothing = [](int) MM1_INLINE {};
-  if (pwave) {
-    product(smem, snext, nothing);
-    read_vec(reinterpret_cast<const float*>(smem + 2 * QT));        // lse of tile 0
-  }
 
-  // Segment s.  tn, tc, tp, tp2: ring slots of tiles s+1, s, s-1, s-2.
-  // CUR: s < n_u; PREV: tile s-1 exists; PREV2: tile s-2 exists; SYNC: a
-  // later segment reads what this one publishes (mailbox, ring).  In the last
-  // segment with CUR, S(s+1) reads a slot holding another tile (or nothing
-  // yet) and is discarded, as is the lse read for segment s+1: every read
-  // stays inside the ring.
-  auto segment = [&](const char* tn, const char* tc, const char* tp, const char* tp2, int refill,
-                     int s, auto role, auto cur, auto prev, auto prev2, auto sync) MM1_INLINE {
+  // Segment s, its tile in ring slot cs = s % NSTAGE, an integral_constant
+  // or (the last two segments) an int; tn, tc, tp, tp2: the slots of tiles
+  // s+1, s, s-1, s-2.  CUR: s < n_u; PREV: tile s-1 exists; PREV2: tile s-2
+  // exists; SYNC: a later segment reads what this one publishes (mailbox,
+  // ring).  In the last segment with CUR, S(s+1) reads a slot holding
+  // another tile (or nothing yet) and is discarded, as is the lse read for
+  // segment s+1: every read stays inside the ring.
+  auto shift = [](auto sl, auto d) MM1_INLINE {
+    if constexpr (is_ic<decltype(sl)>::value)
+      return ic<(decltype(sl)::value + decltype(d)::value) % NSTAGE>{};
+    else
+      return (sl + decltype(d)::value) % NSTAGE;
+  };
+  auto segment = [&](auto cslot, int s, auto role, auto cur, auto prev, auto prev2, auto sync) MM1_INLINE {
+    const auto tn = shift(cslot, ic<1>{});
+    const auto tc = cslot;
+    const auto tp = shift(cslot, ic<NSTAGE - 1>{});
+    const auto tp2 = shift(cslot, ic<NSTAGE - 2>{});
+    const int refill = slot_of(shift(cslot, ic<NSTAGE - 3>{}));
     constexpr bool PW = decltype(role)::value;
     constexpr bool CUR = decltype(cur)::value, PREV = decltype(prev)::value;
     constexpr bool PREV2 = decltype(prev2)::value, SYNC = decltype(sync)::value;
@@ -634,7 +717,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
         for (int kb = 0; kb < KB; ++kb) sv[kb] = snext[kb];
       }
       if constexpr (PREV) {
-        accumulate_tile(nfa, tp + QT, pb, [&](int i) MM1_INLINE {
+        accumulate_tile(nfa, [&](int i) MM1_INLINE { return do_tr(tp, i & 3, i >> 2); }, pb, [&](int i) MM1_INLINE {
           if constexpr (CUR) {
             exp_at(2 * i);
             exp_at(2 * i + 1);
@@ -646,7 +729,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
       }
       if constexpr (CUR) {
         mask();
-        product(tn, snext, [&](int ks) MM1_INLINE { pack_at(ks); });
+        product([&](int ks) MM1_INLINE { return q_rows(tn, ks); }, snext, [&](int ks) MM1_INLINE { pack_at(ks); });
       }
       if constexpr (CUR) {
         float* mb = mbox + (s & 1) * (KB * MBOX / 4);
@@ -662,8 +745,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
           pb[kb][0] = pbn[kb][0];
           pb[kb][1] = pbn[kb][1];
         }
-        read_first(tc + QT);
-        read_vec(reinterpret_cast<const float*>(tn + 2 * QT));
+        read_first([&](int i) MM1_INLINE { return do_tr(tc, i & 3, i >> 2); });
+        read_lse(tn);
       }
     } else {
       // dS(s-1) = P'(s-1) (dP(s-1) - Delta), computed in place of the
@@ -700,7 +783,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
         }
       };
       if constexpr (PREV2) {
-        accumulate_tile(nfa, tp2, sbp, [&](int i) MM1_INLINE {
+        accumulate_tile(nfa, [&](int i) MM1_INLINE { return q_tr(tp2, i & 3, i >> 2); }, sbp, [&](int i) MM1_INLINE {
           if constexpr (PREV) {
             ds_at(2 * i);
             ds_at(2 * i + 1);
@@ -725,16 +808,15 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
       // dP(s) - Delta = -Delta + dO(s) V^T, used by the next segment
       if constexpr (CUR) {
         f32x16 dlt;   // -Delta of tile s in the D layout (register r: query 8*(r/4) + 4*h + r%4)
-        const float* dll = reinterpret_cast<const float*>(tc + 2 * QT) + BQ;
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) {
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dll + 8 * a4 + 4 * h);
+          const f32x4 d4 = vec4(tc, 4 * BQ, a4);
 #pragma unroll
           for (int c = 0; c < 4; ++c) dlt[4 * a4 + c] = d4[c];
         }
-        product_onto(tc + QT, dpp, dlt, nothing);
+        product_onto([&](int ks) MM1_INLINE { return do_rows(tc, ks); }, dpp, dlt, nothing);
       }
-      if constexpr (PREV) read_first(tp);
+      if constexpr (PREV) read_first([&](int i) MM1_INLINE { return q_tr(tp, i & 3, i >> 2); });
     }
     if constexpr (CUR) advance(ch, ctl);
     if constexpr (SYNC) {
@@ -758,32 +840,30 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   // slot, and so every LDS offset, is a compile-time constant.
   using T = std::true_type;
   using F = std::false_type;
-  auto slot = [&](int c) MM1_INLINE { return smem + c * BUF; };
   auto run = [&](auto role) MM1_INLINE {
-    const char* s0p = slot(0);
-    const char* s1p = slot(1);
+    set_bases(decltype(role)::value);
+    if constexpr (decltype(role)::value) {
+      product([&](int ks) MM1_INLINE { return q_rows(ic<0>{}, ks); }, snext, nothing);
+      read_lse(ic<0>{});        // lse of tile 0
+    }
     if (n_u == 1) {
-      segment(s1p, s0p, s0p, s0p, NSTAGE - 3, 0, role, T{}, F{}, F{}, T{});
-      segment(s0p, s0p, s0p, s0p, 0, 1, role, F{}, T{}, F{}, F{});
-      segment(s0p, s0p, s0p, s0p, 0, 2, role, F{}, F{}, T{}, F{});
+      segment(ic<0>{}, 0, role, T{}, F{}, F{}, T{});
+      segment(ic<1>{}, 1, role, F{}, T{}, F{}, F{});
+      segment(ic<2>{}, 2, role, F{}, F{}, T{}, F{});
       return;
     }
-    segment(s1p, s0p, s0p, s0p, NSTAGE - 3, 0, role, T{}, F{}, F{}, T{});
-    segment(slot(2), s1p, s0p, s0p, NSTAGE - 2, 1, role, T{}, T{}, F{}, T{});
+    segment(ic<0>{}, 0, role, T{}, F{}, F{}, T{});
+    segment(ic<1>{}, 1, role, T{}, T{}, F{}, T{});
     for (int b0 = 2; b0 < n_u; b0 += NSTAGE) {
       unroll_while<0, NSTAGE>([&](auto j) MM1_INLINE {
-        constexpr int C = (2 + decltype(j)::value) % NSTAGE;
         const int s = b0 + decltype(j)::value;
         if (s >= n_u) return false;
-        segment(slot((C + 1) % NSTAGE), slot(C), slot((C + NSTAGE - 1) % NSTAGE),
-                slot((C + NSTAGE - 2) % NSTAGE), (C + NSTAGE - 3) % NSTAGE, s, role, T{}, T{}, T{}, T{});
+        segment(ic<(2 + decltype(j)::value) % NSTAGE>{}, s, role, T{}, T{}, T{}, T{});
         return true;
       });
     }
-    const char* tl = slot((n_u - 1) % NSTAGE);
-    const char* tl2 = slot((n_u - 2) % NSTAGE);
-    segment(tl, tl, tl, tl2, 0, n_u, role, F{}, T{}, T{}, F{});
-    segment(tl, tl, tl, tl, 0, n_u + 1, role, F{}, F{}, T{}, F{});
+    segment(n_u % NSTAGE, n_u, role, F{}, T{}, T{}, F{});
+    segment((n_u + 1) % NSTAGE, n_u + 1, role, F{}, F{}, T{}, F{});
   };
   if (pwave) run(std::true_type{});
   else run(std::false_type{});
