@@ -1012,10 +1012,16 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
     const DispatchOrder ord) {
   constexpr int BM = NW * 32;
   constexpr int BN = TILE_ROWS;
-  constexpr int BUF = 2 * TILE_BYTES;   // K, V
+  // LDS: a ring of K tiles, then a ring of V tiles.  The K reads (rows and
+  // transposed) stay below 64 KiB, where a ds instruction's offset field
+  // reaches every slot from the per-lane bases; when the V ring ends past 64
+  // KiB its row reads take per-lane bases that hold the ring's offset (VHI).
+  constexpr int KR = 0, VR = NSTAGE * TILE_BYTES;
+  constexpr bool VHI = VR + NSTAGE * TILE_BYTES > 0x10000;
   constexpr int DMA_PER_TILE = 2 * (16 / NW);
-  static_assert(NSTAGE * BUF >= NW * 8192, "the epilogue stages 8 KiB per wave in the ring");
-  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * BUF];
+  static_assert(2 * NSTAGE * TILE_BYTES >= NW * 8192, "the epilogue stages 8 KiB per wave in the ring");
+  static_assert(VR <= 0x10000, "K reads must reach every K slot by the offset field");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * NSTAGE * TILE_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index (uniform)
@@ -1043,14 +1049,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
   const _Float16* kbase = k + ((long)b * S * Hkv + g) * HD;
   const _Float16* vbase = v + ((long)b * S * Hkv + g) * HD;
   const uint32_t dma_off = tile_lane_off(kvstride, tid);
-  auto issue_tile = [&](char* buf, int kt) {
+  auto issue_tile = [&](int slot, int kt) {
     const int nk = kt * BN;
-    tile_dma<NW>(buf, kbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
-    tile_dma<NW>(buf + TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
+    tile_dma<NW>(smem + KR + slot * TILE_BYTES, kbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
+    tile_dma<NW>(smem + VR + slot * TILE_BYTES, vbase + (long)nk * kvstride, kvstride, S - nk, dma_off, tid);
   };
 #pragma unroll
   for (int st = 0; st < NSTAGE - 1; ++st)
-    if (st < n_kt) issue_tile(smem + st * BUF, st);
+    if (st < n_kt) issue_tile(st, st);
 
   const int rr = rw0 + l32;
   const int qp = rr / G;
@@ -1089,15 +1095,31 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
 #pragma unroll
   for (int db = 0; db < 4; ++db) dqacc[db] = zero16();
   const LdsBases lb = make_lds_bases(lane);
+  using lds_cp = const MM1_LDS char*;
+  lds_cp vrow[8];   // VHI: per-lane bases of the V row reads, VR included, opaque to the compiler
+  if constexpr (VHI) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      vrow[ks] = (lds_cp)smem + VR + (lb.row ^ (32 * ks));
+      __asm__ volatile("" : "+v"(vrow[ks]));
+    }
+  }
+  // row fragment (jb, ks) of the V tile in slot P
+  auto v_rows = [&](auto slot, int jb, int ks) MM1_INLINE {
+    constexpr int P = decltype(slot)::value;
+    if constexpr (VHI)
+      return *reinterpret_cast<const MM1_LDS f16x8*>(vrow[ks] + (P * TILE_BYTES + jb * 8192));
+    else
+      return rows_a(smem + VR + P * TILE_BYTES, lb, jb, ks);
+  };
   wait_dma();
   __syncthreads();
 
   auto step = [&](auto slot, int kt) {
     constexpr int P = decltype(slot)::value;
-    const char* kl = smem + P * BUF;
-    const char* vl = kl + TILE_BYTES;
+    const char* kl = smem + KR + P * TILE_BYTES;
     const bool prefetch = kt + NSTAGE - 1 < n_kt;
-    if (prefetch) issue_tile(smem + ((P + NSTAGE - 1) % NSTAGE) * BUF, kt + NSTAGE - 1);
+    if (prefetch) issue_tile((P + NSTAGE - 1) % NSTAGE, kt + NSTAGE - 1);
     const int k0 = kt * BN;
     if (wave_active && (!CAUSAL || k0 <= pw_hi)) {
       const bool need_mask = CAUSAL ? (k0 + BN - 1 > pw_lo) : (k0 + BN > S);
@@ -1115,13 +1137,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_dq_kernel(
 #pragma unroll
         for (int ks = 0; ks < PF; ++ks) {
           ka[ks] = rows_a(kl, lb, jb, ks);
-          va[ks] = rows_a(vl, lb, jb, ks);
+          va[ks] = v_rows(slot, jb, ks);
         }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
           if (ks + PF < 8) {
             ka[(ks + PF) % (PF + 1)] = rows_a(kl, lb, jb, ks + PF);
-            va[(ks + PF) % (PF + 1)] = rows_a(vl, lb, jb, ks + PF);
+            va[(ks + PF) % (PF + 1)] = v_rows(slot, jb, ks + PF);
           }
           // keep the reads ahead: the scheduler would otherwise sink them
           // to their products and expose the LDS latency on every pair
