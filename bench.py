@@ -78,6 +78,10 @@ def parse(argv=None):
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run --steps device-to-device copies of MIB MiB (a plain copy "
                          "kernel of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only run the matrix-core issue-rate probe (probe/mfma_ceiling.hip): "
+                         "FLOP/s of fp16 32x32x16 products alone and with fixed mixes of VALU / LDS "
+                         "instructions, and the clock under each")
     ap.add_argument("--traffic", default=None,
                     help="JSON with HBM bytes per launch from rocprofv3 --pmc "
                          "(default profiles/traffic_config<N>.json if present)")
@@ -290,6 +294,79 @@ def sustained_clock(step, seconds=2.0, settle=0.5):
     return {"median_mhz": round(med, 1), "min_mhz": round(vals[0], 1), "max_mhz": round(vals[-1], 1),
             "samples": len(vals), "seconds": seconds, "source": source,
             "peak_at_this_clock_tflops": round(PEAK_BF16_TFLOPS * med / 2400.0, 1)}
+
+
+MFMA_CEILING_MODES = ("products only", "+4 fma", "+4 fma +1 exp", "A from LDS (b128)",
+                      "A and B from LDS (b128 + 2 tr_b64)",
+                      "dK/dV mix (2 LDS, 3 fma, 0.5 exp)", "LDS reads only (b128)",
+                      "LDS reads only (tr_b64)")
+MFMA_CEILING_LDS_ONLY = (6, 7)   # no products: LDS bytes per second instead
+
+
+def mfma_ceiling(device, seconds=1.5, settle=0.5):
+    """The matrix-core issue-rate probe (probe/mfma_ceiling.hip, built into
+    _lib/libmm1probe.so): for each instruction mix, 512 workgroups of 4
+    waves (two waves per SIMD, as the attention kernels run) issue 4
+    independent fp16 32x32x16 product chains for `seconds`, launch after
+    launch; the median launch time gives TFLOP/s, and the clock is read after
+    each launch once `settle` seconds have passed."""
+    import ctypes
+    import time
+    import torch
+    from mimansm1_v1_amd import build as B
+    path = B.probe_path()
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: run python -m mimansm1_v1_amd.build")
+    lib = ctypes.CDLL(str(path))
+    fn = lib.mm1_probe_mfma_ceiling
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    blocks, iters = 512, 20000
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=device)
+    read, source = _clock_reader()
+    flop = blocks * 4 * iters * 4 * 32768.0
+    rows = []
+    for mode, name in enumerate(MFMA_CEILING_MODES):
+        stream = torch.cuda.current_stream().cuda_stream
+        if fn(mode, out.data_ptr(), blocks, iters, stream) != 0:
+            raise RuntimeError(f"probe mode {mode} failed to launch")
+        torch.cuda.synchronize()
+        times, clocks = [], []
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn(mode, out.data_ptr(), blocks, iters, stream)
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+            if read is not None and time.perf_counter() - t0 >= settle:
+                try:
+                    clocks.append(read())
+                except Exception:
+                    pass
+        ms = sorted(times)[len(times) // 2]
+        clk = sorted(clocks)[len(clocks) // 2] if clocks else None
+        if mode in MFMA_CEILING_LDS_ONLY:
+            nbytes = blocks * 4 * iters * 4096.0      # 4 KiB of LDS reads per wave and trip
+            tbs = nbytes / ms / 1e9
+            per_clk = nbytes / (ms * 1e-3) / (clk * 1e6) / 256 if clk else None
+            rows.append({"mode": mode, "mix": name, "ms": round(ms, 4), "lds_tbytes_per_s": round(tbs, 2),
+                         "bytes_per_clk_per_cu": round(per_clk, 1) if per_clk else None,
+                         "clock_mhz": round(clk, 1) if clk else None})
+            print(f"[mfma-ceiling] {name:36s} {tbs:7.2f} TB/s of LDS reads, "
+                  f"{per_clk or float('nan'):5.1f} B/clk/CU  clock {clk or float('nan'):6.0f} MHz",
+                  file=sys.stderr, flush=True)
+            continue
+        tf = flop / ms / 1e9
+        rows.append({"mode": mode, "mix": name, "ms": round(ms, 4), "tflops": round(tf, 1),
+                     "pct_of_peak": round(100 * tf / PEAK_BF16_TFLOPS, 1),
+                     "clock_mhz": round(clk, 1) if clk else None})
+        print(f"[mfma-ceiling] {name:36s} {tf:7.1f} TFLOP/s ({100 * tf / PEAK_BF16_TFLOPS:4.1f}% of "
+              f"{PEAK_BF16_TFLOPS:.0f})  clock {clk or float('nan'):6.0f} MHz", file=sys.stderr, flush=True)
+    return {"probe": "mfma_ceiling", "instruction": "v_mfma_f32_32x32x16_f16", "workgroups": blocks,
+            "waves_per_simd": 2, "products_per_launch": blocks * 4 * iters * 4, "clock_source": source,
+            "modes": rows}
 
 
 def time_forward(batch, seq, device, steps, warmup):
@@ -704,6 +781,10 @@ def main(argv=None):
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": n * 4, "launches": args.steps}), flush=True)
+        return 0
+
+    if args.mfma_ceiling:
+        print(json.dumps(mfma_ceiling(device)), flush=True)
         return 0
 
     results = {}

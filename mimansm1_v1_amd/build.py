@@ -3,8 +3,10 @@
     python -m mimansm1_v1_amd.build [--verbose] [--resource-usage]
 
 Compiles every ``csrc/*.hip`` for ``--offload-arch=gfx950`` and links them into
-``mimansm1_v1_amd/_lib/libmm1attn.so``.  No GPU is needed (hipcc
-cross-compiles).  The library is loaded with ctypes by ``_lib.py``.
+``mimansm1_v1_amd/_lib/libmm1attn.so``, and ``probe/mfma_ceiling.hip`` into
+``_lib/libmm1probe.so`` (the matrix-core issue-rate probe that
+``bench.py --mfma-ceiling`` runs; not part of the attention ABI).  No GPU is
+needed (hipcc cross-compiles).  The libraries are loaded with ctypes.
 """
 from __future__ import annotations
 
@@ -20,6 +22,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT_DIR = PKG / "_lib"
 LIB_NAME = "libmm1attn.so"
+PROBE_SRC = PKG / "probe" / "mfma_ceiling.hip"
+PROBE_LIB = "libmm1probe.so"
 ARCH = "gfx950"
 
 # Packed fp32 VALU ops are disabled for all device code (the hardware pool
@@ -86,6 +90,22 @@ def build(verbose: bool = False, resource_usage: bool = False) -> Path:
     os.replace(tmp, out)
     if verbose:
         print(f"[build] wrote {out}")
+    build_probe(cc)
+    return out
+
+
+def probe_path() -> Path:
+    return OUT_DIR / PROBE_LIB
+
+
+def build_probe(cc: str) -> Path:
+    out = probe_path()
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [cc, *DEVICE_FLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, out)
     return out
 
 

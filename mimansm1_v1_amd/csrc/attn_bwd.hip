@@ -306,12 +306,14 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // One workgroup per 128-key tile, 8 waves in 4 pairs, one pair per SIMD; a
 // pair owns 32 keys of the tile and splits the work by role: the P wave
 // keeps K (B operand) and the dV^T accumulators, the dS wave V and dK^T.  P
-// goes from the P wave to the dS wave through a two-slot fp32 LDS mailbox.
+// goes from the P wave to the dS wave through a two-slot LDS mailbox, as the
+// fp16 values the P wave's dV^T product takes (half the LDS bytes of fp32,
+// which the kernel's LDS traffic is the tightest limit on).
 // The query tiles are 32 rows (Q, dO row-major; the transposed operands of
 // dV^T and dK^T come from the LDS transpose read), and the work on a tile is
 // spread over four segments:
 //   segment s, P wave : S(s+1) = Q(s+1) K^T                 | P'(s) = exp2(S(s) scale2 - lse) = P sm_scale -> mailbox | dV^T += dO(s-1)^T P'(s-1)
-//   segment s, dS wave: dP(s) - Delta = -Delta + dO(s) V^T   | dS(s-1) = P'(s-1) (dP(s-1) - Delta)                     | dK^T += Q(s-2)^T dS(s-2)
+//   segment s, dS wave: dP(s) - Delta = -Delta + dO(s) V^T   | dS(s-1) = fp16(P'(s-1)) (dP(s-1) - Delta)               | dK^T += Q(s-2)^T dS(s-2)
 // Within a segment each wave's VALU work (middle column) depends on no
 // product of the same segment, so it runs under the wave's own products
 // (and, with two waves per SIMD, the other wave's), and the pair meets at one
@@ -327,9 +329,9 @@ __device__ __forceinline__ void unroll_while(F&& f) {
 // fp16(2^E dO) with -Delta scaled alike (attn_do16_kernel), so dP, dS and
 // the accumulators carry the factor 2^E; the epilogue multiplies dK by
 // scale[0] = 2^-E.  The P wave's exponentials take lse = lse2 -
-// log2(sm_scale) and give P' = P sm_scale, which goes to the mailbox as is
-// (dS = P' (dP - Delta)) and, rounded to fp16, into dV^T: the epilogue
-// multiplies dV by 2^-E / sm_scale.  F32OUT: dk / dv (and the partials)
+// log2(sm_scale) and give P' = P sm_scale, which is rounded to fp16 for
+// dV^T and for the mailbox (dS = fp16(P') (dP - Delta) in fp32, rounded to
+// fp16 for dK^T): the epilogue multiplies dV by 2^-E / sm_scale.  F32OUT: dk / dv (and the partials)
 // are fp32, the values the bf16 path rounds.
 //
 // Tile x of the ring lives in slot x % NSTAGE; it is first read in segment
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   constexpr int VR = 2 * NSTAGE * QT;     // vector ring
   constexpr int VSLOT = 256;
   constexpr int MB0 = VR + NSTAGE * VSLOT;
-  constexpr int MBOX = 32 * 32 * 4;       // one 32 x 32 fp32 P block
+  constexpr int MBOX = 32 * 32 * 2;       // one 32 x 32 fp16 P block
   static_assert(QR + NSTAGE * QT + 4096 <= 0x10000, "Q reads must reach every Q slot by the offset field");
   __shared__ __attribute__((aligned(1024))) char smem[MB0 + NP * 2 * KB * MBOX];
 
@@ -427,9 +429,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
   }
   const int kw0 = kt * 128 + 32 * KB * pair;   // this pair's first key
   // mailbox of this pair: two slots of KB blocks; a block is
-  // [register group a4][lane] x 4 floats, so each 16-byte access of a wave
-  // is one contiguous 1 KiB row
-  float* const mbox = reinterpret_cast<float*>(smem + MB0 + pair * 2 * KB * MBOX) + lane * 4;
+  // [register half j][lane] x 8 fp16 (registers 8j .. 8j+7 of the lane's P'
+  // block), so each 16-byte access of a wave is one contiguous 1 KiB row
+  _Float16* const mbox = reinterpret_cast<_Float16*>(smem + MB0 + pair * 2 * KB * MBOX) + lane * 8;
 
   const int q_begin = CAUSAL ? kt * 128 : 0;
   const long qstride = (long)H * HD;
@@ -732,16 +734,12 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
         product([&](int ks) MM1_INLINE { return q_rows(tn, ks); }, snext, [&](int ks) MM1_INLINE { pack_at(ks); });
       }
       if constexpr (CUR) {
-        float* mb = mbox + (s & 1) * (KB * MBOX / 4);
+        // the fp16 P'(s) of the dV^T product goes to the mailbox as well
+        _Float16* mb = mbox + (s & 1) * (KB * MBOX / 2);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-            f32x4 v4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) v4[c] = sv[kb][4 * a4 + c];
-            *reinterpret_cast<f32x4*>(mb + kb * (MBOX / 4) + 256 * a4) = v4;
-          }
+          for (int j = 0; j < 2; ++j) *reinterpret_cast<f16x8*>(mb + kb * (MBOX / 2) + 512 * j) = pbn[kb][j];
           pb[kb][0] = pbn[kb][0];
           pb[kb][1] = pbn[kb][1];
         }
@@ -749,26 +747,23 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
         read_lse(tn);
       }
     } else {
-      // dS(s-1) = P'(s-1) (dP(s-1) - Delta), computed in place of the
-      // mailbox values P' = P sm_scale between the products of
-      // dK^T += Q(s-2)^T dS(s-2)
+      // dS(s-1) = P'(s-1) (dP(s-1) - Delta) from the mailbox's fp16
+      // P' = P sm_scale, between the products of dK^T += Q(s-2)^T dS(s-2)
       f32x16 dsv[KB];
+      f16x8 pm[KB][2];   // P'(s-1) in fp16, as the P wave's dV^T product takes it
       if constexpr (PREV) {
-        const float* mb = mbox + ((s - 1) & 1) * (KB * MBOX / 4);
+        const _Float16* mb = mbox + ((s - 1) & 1) * (KB * MBOX / 2);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4) {
-            const f32x4 p4 = *reinterpret_cast<const f32x4*>(mb + kb * (MBOX / 4) + 256 * a4);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) dsv[kb][4 * a4 + c] = p4[c];
-          }
+          for (int j = 0; j < 2; ++j) pm[kb][j] = *reinterpret_cast<const f16x8*>(mb + kb * (MBOX / 2) + 512 * j);
         }
       }
       auto ds_at = [&](int r) MM1_INLINE {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          float x = dsv[kb][r] * dpp[kb][r];
+          // one v_fma_mix_f32: the fp16 operand is widened inside the fma
+          float x = fmaf((float)pm[kb][r >> 3][r & 7], dpp[kb][r], 0.f);
           pin(x);
           dsv[kb][r] = x;
         }

@@ -47,6 +47,21 @@ def test_exports_every_declared_symbol(lib):
         getattr(lib, n)
 
 
+def test_probe_library_apart_from_the_abi(lib):
+    """The matrix-core probe bench.py --mfma-ceiling runs is its own library:
+    built in-tree beside the attention library, exporting only its entry
+    point, which the attention library does not carry."""
+    from mimansm1_v1_amd import build as B
+    path = B.probe_path()
+    assert path.exists() and ROOT in path.parents
+    probe = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True,
+                           check=True).stdout
+    assert set(re.findall(r"\bT (mm1_\w+)", probe)) == {"mm1_probe_mfma_ceiling"}
+    attn = subprocess.run(["nm", "-D", "--defined-only", str(_lib.library_path())], capture_output=True,
+                          text=True, check=True).stdout
+    assert "mm1_probe_mfma_ceiling" not in attn
+
+
 def test_version_matches_header(lib):
     m = re.search(r"#define MM1_ATTN_VERSION (\d+)", HEADER.read_text())
     assert lib.mm1_attn_version() == int(m.group(1))
