@@ -731,15 +731,21 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv_pipe_kernel(
       }
       if constexpr (CUR) {
         mask();
-        product([&](int ks) MM1_INLINE { return q_rows(tn, ks); }, snext, [&](int ks) MM1_INLINE { pack_at(ks); });
+        // the fp16 P'(s) of the dV^T product goes to the mailbox as well, each
+        // half as soon as it is packed (spreading the writes over the product)
+        _Float16* mb = mbox + (s & 1) * (KB * MBOX / 2);
+        product([&](int ks) MM1_INLINE { return q_rows(tn, ks); }, snext, [&](int ks) MM1_INLINE {
+          pack_at(ks);
+          if ((ks & 3) == 3) {
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+              *reinterpret_cast<f16x8*>(mb + kb * (MBOX / 2) + 512 * (ks >> 2)) = pbn[kb][ks >> 2];
+          }
+        });
       }
       if constexpr (CUR) {
-        // the fp16 P'(s) of the dV^T product goes to the mailbox as well
-        _Float16* mb = mbox + (s & 1) * (KB * MBOX / 2);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-          for (int j = 0; j < 2; ++j) *reinterpret_cast<f16x8*>(mb + kb * (MBOX / 2) + 512 * j) = pbn[kb][j];
           pb[kb][0] = pbn[kb][0];
           pb[kb][1] = pbn[kb][1];
         }
