@@ -35,7 +35,8 @@ __global__ __launch_bounds__(256) void mfma_ceiling_kernel(float* __restrict__ o
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int i = tid; i < 16384 / 4; i += 256) reinterpret_cast<float*>(lds)[i] = 1e-3f * (float)(i & 255);
   __syncthreads();
-  // every wave reads the same 4 KiB (as the kernels' waves share a tile);
+  // every wave reads the same LDS bytes (as the kernels' waves share a
+  // tile): A fragments from the first 8 KiB, B from the second;
   // consecutive 16 (8) bytes per lane: no bank conflicts
   const char* a_base = lds + 16 * lane;
   const char* b_base = lds + 8192 + 8 * lane;
