@@ -299,7 +299,8 @@ def sustained_clock(step, seconds=2.0, settle=0.5):
 MFMA_CEILING_MODES = ("products only", "+4 fma", "+4 fma +1 exp", "A from LDS (b128)",
                       "A and B from LDS (b128 + 2 tr_b64)",
                       "dK/dV mix (2 LDS, 3 fma, 0.5 exp)", "LDS reads only (b128)",
-                      "LDS reads only (tr_b64)")
+                      "LDS reads only (tr_b64)", "products only, 1 dependent chain",
+                      "products only, 2 dependent chains")
 MFMA_CEILING_LDS_ONLY = (6, 7)   # no products: LDS bytes per second instead
 
 

@@ -18,6 +18,9 @@
 //      an exp every other product
 //   6  no products: 4 ds_read_b128 per trip (LDS read bandwidth)
 //   7  no products: 8 ds_read_b64_tr_b16 per trip (transposed reads)
+//   8  products only, one dependent chain per wave (each product
+//      accumulates onto the previous one's result)
+//   9  products only, two dependent chains per wave
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -69,10 +72,11 @@ __global__ __launch_bounds__(256) void mfma_ceiling_kernel(float* __restrict__ o
     return r;
   };
 
+  constexpr bool A_LDS = MODE >= 3 && MODE <= 5;   // A operand read from LDS each trip
   f16x8 fa[4], fb[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    fa[j] = MODE >= 3 && MODE != 7 ? read_a(j) : a;
+    fa[j] = A_LDS || MODE == 6 ? read_a(j) : a;
     fb[j] = (MODE == 4 || MODE == 7 || (MODE == 5 && (j & 1) == 0)) ? read_b(j) : b;
   }
   f16x8 ld[4] = {a, a, a, b};
@@ -89,9 +93,11 @@ __global__ __launch_bounds__(256) void mfma_ceiling_kernel(float* __restrict__ o
                           : read_b(j, o >> 1);
         continue;
       }
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[j], fb[j], acc[j], 0, 0, 0);
+      // modes 8, 9: one / two accumulators for the trip's four products
+      constexpr int NACC = MODE == 8 ? 1 : MODE == 9 ? 2 : 4;
+      acc[j % NACC] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[j], fb[j], acc[j % NACC], 0, 0, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (MODE >= 3) {
+      if (A_LDS) {
         fa[j] = read_a(j);   // for the next trip
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
@@ -138,6 +144,8 @@ extern "C" int mm1_probe_mfma_ceiling(int mode, float* out, int blocks, int iter
     case 5: hipLaunchKernelGGL(mfma_ceiling_kernel<5>, g, t, 0, stream, out, iters, 0.999f); break;
     case 6: hipLaunchKernelGGL(mfma_ceiling_kernel<6>, g, t, 0, stream, out, iters, 0.999f); break;
     case 7: hipLaunchKernelGGL(mfma_ceiling_kernel<7>, g, t, 0, stream, out, iters, 0.999f); break;
+    case 8: hipLaunchKernelGGL(mfma_ceiling_kernel<8>, g, t, 0, stream, out, iters, 0.999f); break;
+    case 9: hipLaunchKernelGGL(mfma_ceiling_kernel<9>, g, t, 0, stream, out, iters, 0.999f); break;
     default: return (int)hipErrorInvalidValue;
   }
   return (int)hipGetLastError();
